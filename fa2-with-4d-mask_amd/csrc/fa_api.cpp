@@ -1,0 +1,247 @@
+// C ABI of libfa2_4d_mask.so: argument validation, planning, kernel launch.
+//
+// Every entry point checks its arguments on the host before any HIP call and
+// returns an FA_ERR_* code with nothing enqueued when they are unusable, so the
+// validation paths run (and are tested) on machines without a GPU.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "../../include/fa2_4d_mask.h"
+#include "fa_kernels.h"
+
+namespace fa {
+int fwd_block_rows();
+int dkdv_block_keys();
+int dq_block_rows();
+}  // namespace fa
+
+namespace {
+
+thread_local char g_err[512] = "no error";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof g_err, fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+// Rows of a [.., T, H, D] operand must start on 16 bytes: base aligned and the
+// batch/time/head strides multiples of 8 elements (16-bit data).
+int check_operand(const char* name, const void* p, int64_t sb, int64_t st, int64_t sh) {
+  if (!p) return fail(FA_ERR_NULL, "%s is NULL", name);
+  if (!aligned16(p)) return fail(FA_ERR_STRIDE, "%s base pointer is not 16-byte aligned", name);
+  if (sb % 8 || st % 8 || sh % 8)
+    return fail(FA_ERR_STRIDE, "%s strides (b=%lld, t=%lld, h=%lld) must be multiples of 8 elements", name,
+                (long long)sb, (long long)st, (long long)sh);
+  return FA_OK;
+}
+
+int check_dims(int32_t B, int32_t Tq, int32_t Tk, int32_t Hq, int32_t Hk, int32_t D, int32_t dtype, float scale) {
+  if (B < 1 || Tq < 1 || Tk < 1 || Hq < 1 || Hk < 1)
+    return fail(FA_ERR_SHAPE, "sizes must be >= 1 (B=%d Tq=%d Tk=%d Hq=%d Hk=%d)", B, Tq, Tk, Hq, Hk);
+  if (Hq % Hk != 0)
+    return fail(FA_ERR_SHAPE, "query heads (%d) must be divisible by key/value heads (%d)", Hq, Hk);
+  if (D != 64 && D != 128) return fail(FA_ERR_HEAD_DIM, "head_dim %d not supported (64, 128)", D);
+  if (dtype != FA_DTYPE_BF16 && dtype != FA_DTYPE_FP16) return fail(FA_ERR_DTYPE, "unsupported dtype code %d", dtype);
+  if (!std::isfinite(scale)) return fail(FA_ERR_SCALE, "scale must be finite");
+  // 32-bit indices inside the kernels: rows of every head must fit.
+  if ((int64_t)B * Hq * (int64_t)Tq >= (1LL << 31) || (int64_t)B * Hk * (int64_t)Tk >= (1LL << 31))
+    return fail(FA_ERR_SHAPE, "problem too large for 32-bit row indices");
+  return FA_OK;
+}
+
+int check_mask_score(const uint8_t* mask, int64_t msb, int64_t msh, int64_t msq, const float* score, int64_t ssb,
+                     int64_t ssh, int64_t ssq) {
+  if (mask && (msb < 0 || msh < 0 || msq < 0)) return fail(FA_ERR_STRIDE, "mask strides must be non-negative");
+  if (score && (ssb < 0 || ssh < 0 || ssq < 0)) return fail(FA_ERR_STRIDE, "score strides must be non-negative");
+  return FA_OK;
+}
+
+// 32-bit (mask) / 128-bit (score) loads need every row start aligned.
+int mask_vec_ok(const uint8_t* m, int64_t sb, int64_t sh, int64_t sq) {
+  return m && ((uintptr_t)m % 4 == 0) && sb % 4 == 0 && sh % 4 == 0 && sq % 4 == 0;
+}
+int score_vec_ok(const float* s, int64_t sb, int64_t sh, int64_t sq) {
+  return s && ((uintptr_t)s % 16 == 0) && sb % 4 == 0 && sh % 4 == 0 && sq % 4 == 0;
+}
+
+int launch_status(hipError_t e, const char* what) {
+  if (e != hipSuccess) return fail(FA_ERR_LAUNCH, "%s launch failed: %s", what, hipGetErrorString(e));
+  return FA_OK;
+}
+
+int choose_split(const FaBwdParams* p) {
+  if (p->kv_split > 0) return p->kv_split;
+  const int G = p->heads_q / p->heads_k;
+  const int nkt = (p->seqlen_k + fa::dkdv_block_keys() - 1) / fa::dkdv_block_keys();
+  const int64_t base = (int64_t)p->batch * p->heads_k * nkt;
+  const int64_t target = 512;  // two workgroups per CU on a 256-CU part
+  int split = 1;
+  while (split * 2 <= G && G % (split * 2) == 0 && base * split < target) split *= 2;
+  return split;
+}
+
+void fill_scales(float scale, float* scale_log2_fwd, float* qsign, int* zero, float* scale_log2_bwd) {
+  *zero = scale == 0.f;
+  *qsign = scale < 0.f ? -1.f : 1.f;
+  const float l2e = 1.4426950408889634f;
+  *scale_log2_fwd = *zero ? 1.f : std::fabs(scale) * l2e;
+  *scale_log2_bwd = *zero ? 1.f : scale * l2e;
+}
+
+}  // namespace
+
+extern "C" {
+
+int fa_abi_version(void) { return FA_ABI_VERSION; }
+
+const char* fa_last_error(void) { return g_err; }
+
+int fa_fwd(const FaFwdParams* p) {
+  if (!p) return fail(FA_ERR_NULL, "params is NULL");
+  int st = check_dims(p->batch, p->seqlen_q, p->seqlen_k, p->heads_q, p->heads_k, p->head_dim, p->dtype, p->scale);
+  if (st) return st;
+  if ((st = check_operand("q", p->q, p->q_stride_b, p->q_stride_t, p->q_stride_h))) return st;
+  if ((st = check_operand("k", p->k, p->k_stride_b, p->k_stride_t, p->k_stride_h))) return st;
+  if ((st = check_operand("v", p->v, p->v_stride_b, p->v_stride_t, p->v_stride_h))) return st;
+  if ((st = check_operand("o", p->o, p->o_stride_b, p->o_stride_t, p->o_stride_h))) return st;
+  if (!p->lse) return fail(FA_ERR_NULL, "lse is NULL");
+  if ((st = check_mask_score(p->mask, p->mask_stride_b, p->mask_stride_h, p->mask_stride_q, p->score,
+                             p->score_stride_b, p->score_stride_h, p->score_stride_q)))
+    return st;
+
+  fa::FwdArgs a{};
+  a.q = p->q; a.k = p->k; a.v = p->v; a.o = p->o; a.lse = p->lse;
+  a.mask = p->mask; a.score = p->score;
+  a.qsb = p->q_stride_b; a.qst = p->q_stride_t; a.qsh = p->q_stride_h;
+  a.ksb = p->k_stride_b; a.kst = p->k_stride_t; a.ksh = p->k_stride_h;
+  a.vsb = p->v_stride_b; a.vst = p->v_stride_t; a.vsh = p->v_stride_h;
+  a.osb = p->o_stride_b; a.ost = p->o_stride_t; a.osh = p->o_stride_h;
+  a.msb = p->mask_stride_b; a.msh = p->mask_stride_h; a.msq = p->mask_stride_q;
+  a.ssb = p->score_stride_b; a.ssh = p->score_stride_h; a.ssq = p->score_stride_q;
+  a.B = p->batch; a.Tq = p->seqlen_q; a.Tk = p->seqlen_k; a.Hq = p->heads_q; a.Hk = p->heads_k;
+  a.G = p->heads_q / p->heads_k;
+  a.nqt = (p->seqlen_q + fa::fwd_block_rows() - 1) / fa::fwd_block_rows();
+  float sl2b;
+  fill_scales(p->scale, &a.scale_log2, &a.qsign, &a.zero_scale, &sl2b);
+  a.mask_vec = mask_vec_ok(p->mask, p->mask_stride_b, p->mask_stride_h, p->mask_stride_q);
+  a.score_vec = score_vec_ok(p->score, p->score_stride_b, p->score_stride_h, p->score_stride_q);
+  return launch_status(fa::launch_fwd(a, p->head_dim, p->dtype, p->is_causal != 0, (hipStream_t)p->stream), "fa_fwd");
+}
+
+static int check_bwd(const FaBwdParams* p, int split) {
+  int st = check_dims(p->batch, p->seqlen_q, p->seqlen_k, p->heads_q, p->heads_k, p->head_dim, p->dtype, p->scale);
+  if (st) return st;
+  if ((st = check_operand("q", p->q, p->q_stride_b, p->q_stride_t, p->q_stride_h))) return st;
+  if ((st = check_operand("k", p->k, p->k_stride_b, p->k_stride_t, p->k_stride_h))) return st;
+  if ((st = check_operand("v", p->v, p->v_stride_b, p->v_stride_t, p->v_stride_h))) return st;
+  if ((st = check_operand("o", p->o, p->o_stride_b, p->o_stride_t, p->o_stride_h))) return st;
+  if ((st = check_operand("dout", p->dout, p->do_stride_b, p->do_stride_t, p->do_stride_h))) return st;
+  if ((st = check_operand("dq", p->dq, p->dq_stride_b, p->dq_stride_t, p->dq_stride_h))) return st;
+  if ((st = check_operand("dk", p->dk, p->dk_stride_b, p->dk_stride_t, p->dk_stride_h))) return st;
+  if ((st = check_operand("dv", p->dv, p->dv_stride_b, p->dv_stride_t, p->dv_stride_h))) return st;
+  if (!p->lse) return fail(FA_ERR_NULL, "lse is NULL");
+  if (!p->delta) return fail(FA_ERR_NULL, "delta is NULL");
+  if (!p->dead_flags) return fail(FA_ERR_NULL, "dead_flags is NULL");
+  if (p->atomic_dq && !p->dq_accum) return fail(FA_ERR_WORKSPACE, "atomic dQ needs dq_accum");
+  if (p->atomic_dq && !aligned16(p->dq_accum)) return fail(FA_ERR_STRIDE, "dq_accum must be 16-byte aligned");
+  const int G = p->heads_q / p->heads_k;
+  if (split < 1 || G % split != 0) return fail(FA_ERR_SHAPE, "kv_split %d must divide the group size %d", split, G);
+  if (split > 1 && (!p->dk_accum || !p->dv_accum))
+    return fail(FA_ERR_WORKSPACE, "kv_split %d needs dk_accum and dv_accum", split);
+  if (split > 1 && (!aligned16(p->dk_accum) || !aligned16(p->dv_accum)))
+    return fail(FA_ERR_STRIDE, "dk_accum/dv_accum must be 16-byte aligned");
+  return check_mask_score(p->mask, p->mask_stride_b, p->mask_stride_h, p->mask_stride_q, p->score,
+                          p->score_stride_b, p->score_stride_h, p->score_stride_q);
+}
+
+int fa_bwd_plan(const FaBwdParams* p, FaBwdPlan* plan) {
+  if (!p || !plan) return fail(FA_ERR_NULL, "params or plan is NULL");
+  int st = check_dims(p->batch, p->seqlen_q, p->seqlen_k, p->heads_q, p->heads_k, p->head_dim, p->dtype, p->scale);
+  if (st) return st;
+  const int split = choose_split(p);
+  const int G = p->heads_q / p->heads_k;
+  if (split < 1 || G % split != 0) return fail(FA_ERR_SHAPE, "kv_split %d must divide the group size %d", split, G);
+  plan->kv_split = split;
+  plan->needs_dq_accum = p->atomic_dq ? 1 : 0;
+  plan->dq_accum_elems = p->atomic_dq ? (int64_t)p->batch * p->seqlen_q * p->heads_q * p->head_dim : 0;
+  plan->dkv_accum_elems = split > 1 ? (int64_t)p->batch * p->seqlen_k * p->heads_k * p->head_dim : 0;
+  return FA_OK;
+}
+
+int fa_bwd_preprocess(const FaBwdParams* p) {
+  if (!p) return fail(FA_ERR_NULL, "params is NULL");
+  const int split = choose_split(p);
+  int st = check_bwd(p, split);
+  if (st) return st;
+  fa::PreArgs a{};
+  a.o = p->o; a.dout = p->dout; a.lse = p->lse; a.delta = p->delta; a.dead = p->dead_flags;
+  a.dq_accum = p->atomic_dq ? p->dq_accum : nullptr;
+  a.osb = p->o_stride_b; a.ost = p->o_stride_t; a.osh = p->o_stride_h;
+  a.dsb = p->do_stride_b; a.dst = p->do_stride_t; a.dsh = p->do_stride_h;
+  a.B = p->batch; a.Tq = p->seqlen_q; a.Hq = p->heads_q; a.Hk = p->heads_k; a.G = p->heads_q / p->heads_k;
+  return launch_status(fa::launch_preprocess(a, p->head_dim, p->dtype, (hipStream_t)p->stream), "fa_bwd_preprocess");
+}
+
+int fa_bwd(const FaBwdParams* p) {
+  if (!p) return fail(FA_ERR_NULL, "params is NULL");
+  const int split = choose_split(p);
+  int st = check_bwd(p, split);
+  if (st) return st;
+  const hipStream_t s = (hipStream_t)p->stream;
+  fa::BwdArgs a{};
+  a.q = p->q; a.k = p->k; a.v = p->v; a.dout = p->dout;
+  a.lse = p->lse; a.delta = p->delta; a.dead = p->dead_flags;
+  a.mask = p->mask; a.score = p->score;
+  a.dq_accum = p->dq_accum; a.dk_accum = p->dk_accum; a.dv_accum = p->dv_accum;
+  a.dk = p->dk; a.dv = p->dv; a.dq = p->dq;
+  a.qsb = p->q_stride_b; a.qst = p->q_stride_t; a.qsh = p->q_stride_h;
+  a.ksb = p->k_stride_b; a.kst = p->k_stride_t; a.ksh = p->k_stride_h;
+  a.vsb = p->v_stride_b; a.vst = p->v_stride_t; a.vsh = p->v_stride_h;
+  a.dsb = p->do_stride_b; a.dst = p->do_stride_t; a.dsh = p->do_stride_h;
+  a.dqsb = p->dq_stride_b; a.dqst = p->dq_stride_t; a.dqsh = p->dq_stride_h;
+  a.dksb = p->dk_stride_b; a.dkst = p->dk_stride_t; a.dksh = p->dk_stride_h;
+  a.dvsb = p->dv_stride_b; a.dvst = p->dv_stride_t; a.dvsh = p->dv_stride_h;
+  a.msb = p->mask_stride_b; a.msh = p->mask_stride_h; a.msq = p->mask_stride_q;
+  a.ssb = p->score_stride_b; a.ssh = p->score_stride_h; a.ssq = p->score_stride_q;
+  a.B = p->batch; a.Tq = p->seqlen_q; a.Tk = p->seqlen_k; a.Hq = p->heads_q; a.Hk = p->heads_k;
+  a.G = p->heads_q / p->heads_k;
+  a.nkt = (p->seqlen_k + fa::dkdv_block_keys() - 1) / fa::dkdv_block_keys();
+  a.nqt = (p->seqlen_q + fa::dq_block_rows() - 1) / fa::dq_block_rows();
+  a.split = split;
+  a.do_dq = p->atomic_dq ? 1 : 0;
+  a.scale = p->scale;
+  float sl2f;
+  fill_scales(p->scale, &sl2f, &a.qsign, &a.zero_scale, &a.scale_log2);
+  a.mask_vec = mask_vec_ok(p->mask, p->mask_stride_b, p->mask_stride_h, p->mask_stride_q);
+  a.score_vec = score_vec_ok(p->score, p->score_stride_b, p->score_stride_h, p->score_stride_q);
+  const bool causal = p->is_causal != 0;
+
+  if ((st = launch_status(fa::launch_bwd_dkdv(a, p->head_dim, p->dtype, causal, s), "dkdv"))) return st;
+  if (p->atomic_dq) {
+    fa::CvtArgs c{p->dq_accum, p->dq, p->dq_stride_b, p->dq_stride_t, p->dq_stride_h,
+                  p->batch, p->seqlen_q, p->heads_q, p->head_dim};
+    if ((st = launch_status(fa::launch_convert(c, p->dtype, s), "dq convert"))) return st;
+  } else {
+    if ((st = launch_status(fa::launch_bwd_dq(a, p->head_dim, p->dtype, causal, s), "dq"))) return st;
+  }
+  if (split > 1) {
+    fa::CvtArgs ck{p->dk_accum, p->dk, p->dk_stride_b, p->dk_stride_t, p->dk_stride_h,
+                   p->batch, p->seqlen_k, p->heads_k, p->head_dim};
+    if ((st = launch_status(fa::launch_convert(ck, p->dtype, s), "dk convert"))) return st;
+    fa::CvtArgs cv{p->dv_accum, p->dv, p->dv_stride_b, p->dv_stride_t, p->dv_stride_h,
+                   p->batch, p->seqlen_k, p->heads_k, p->head_dim};
+    if ((st = launch_status(fa::launch_convert(cv, p->dtype, s), "dv convert"))) return st;
+  }
+  return FA_OK;
+}
+
+}  // extern "C"

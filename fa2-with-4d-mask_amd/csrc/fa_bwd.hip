@@ -1,0 +1,661 @@
+// FlashAttention-2 backward for gfx950 (MI355X) with optional 4D keep-mask and
+// 4D fp32 score.  Restates the maths of the reference's TileLang backward
+// (python/fa2.py:142-426) as hand-written wave64 MFMA kernels:
+//
+//   preprocess   Delta[b,h,i] = sum_d O*dO (fp32)          (python/fa2.py:142-179)
+//                + zeroes the fp32 dQ accumulator, marks rows with no kept key
+//   dkdv         one workgroup per (128 keys, kv-head, batch[, head split]);
+//                loops over the query heads of the GQA group and the query
+//                tiles, so dK/dV of a group meet in registers, not atomics
+//                (python/fa2.py:181-302 / 305-426 reduce over the group with
+//                atomics or a host sum instead).  Optionally also produces dQ
+//                with fp32 atomics (use_atomic_backward=True).
+//   dq           deterministic dQ (use_atomic_backward=False): one workgroup per
+//                (128 query rows, head, batch), recomputes P and dS per key tile.
+//   convert      fp32 accumulators -> bf16/fp16 outputs.
+//
+// Per query tile (64 rows) and wave (32 keys) the dkdv kernel runs
+//   S  = Q K^T, dP = dO V^T     A = Q / dO rows from LDS, B = K / V resident
+//   P  = exp2(S*scale*log2e - LSE2), dS = P (dP - Delta) scale   (fp32)
+//   dV += P^T dO, dK += dS^T Q  A = P / dS straight from the accumulators,
+//                               B = dO / Q through ds_read_b64_tr_b16
+//   dQ  = dS K                  dS goes through LDS (key-major) and is read
+//                               back transposed; K^T resident in registers
+#include "fa_common.h"
+#include "fa_kernels.h"
+
+namespace fa {
+namespace {
+
+template <typename T>
+__device__ __forceinline__ u32x2 pack4(float x0, float x1, float x2, float x3) {
+  typedef T T4 __attribute__((ext_vector_type(4)));
+  T4 v;
+  v[0] = (T)x0; v[1] = (T)x1; v[2] = (T)x2; v[3] = (T)x3;
+  return __builtin_bit_cast(u32x2, v);
+}
+
+template <typename T>
+__device__ __forceinline__ float to_f(T x) { return (float)x; }
+
+// ---------------------------------------------------------------------------
+// preprocess: Delta, dead-row flags, zeroed dQ accumulator rows
+// ---------------------------------------------------------------------------
+template <typename T, int D>
+__global__ __launch_bounds__(256) void preprocess_kernel(const PreArgs a) {
+  constexpr int CH = D / 8;            // 16-byte chunks per row
+  constexpr int CPT = CH / 4;          // chunks per thread (4 threads per row)
+  const int h = blockIdx.y, b = blockIdx.z;
+  const int r = threadIdx.x >> 2, part = threadIdx.x & 3;
+  const int q = blockIdx.x * 64 + r;
+  float acc = 0.f;
+  if (q < a.Tq) {
+    const T* op = (const T*)a.o + b * a.osb + (int64_t)q * a.ost + h * a.osh;
+    const T* dp = (const T*)a.dout + b * a.dsb + (int64_t)q * a.dst + h * a.dsh;
+#pragma unroll
+    for (int u = 0; u < CPT; ++u) {
+      const int c = part + 4 * u;
+      const auto ov = as_vec8<T>(gload16(op + c * 8));
+      const auto dv = as_vec8<T>(gload16(dp + c * 8));
+#pragma unroll
+      for (int t = 0; t < 8; ++t) acc = fmaf(to_f<T>(ov[t]), to_f<T>(dv[t]), acc);
+    }
+  }
+  acc += __shfl_xor(acc, 1);
+  acc += __shfl_xor(acc, 2);
+  if (q < a.Tq) {
+    if (a.dq_accum) {
+      float* z = a.dq_accum + (((int64_t)b * a.Tq + q) * a.Hq + h) * D + part * (D / 4);
+#pragma unroll
+      for (int u = 0; u < D / 16; ++u) *(f32x4*)(z + 4 * u) = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    if (part == 0) {
+      const int64_t ri = ((int64_t)b * a.Hq + h) * a.Tq + q;
+      const bool dead = a.lse[ri] == kPosInf;
+      a.delta[ri] = dead ? 0.f : acc;
+      if (dead) a.dead[b * a.Hk + h / a.G] = 1;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dK / dV (+ atomic dQ)
+// ---------------------------------------------------------------------------
+constexpr int kKvBN = 128;   // keys per workgroup (4 waves x 32)
+constexpr int kKvBM = 64;    // query rows per inner tile
+
+template <typename T, int D, bool CAUSAL, bool MASK, bool SCORE, bool DQ>
+__global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdArgs a) {
+  using V8 = typename Vec8<T>::type;
+  constexpr int BN = kKvBN, BM = kKvBM;
+  constexpr int DS = D / 16, NB = D / 32, CH = D / 8;
+  // Q/dO tiles are read both row-wise (ds_read_b128, 16 rows) and by the
+  // transpose read (4 rows): a stride of 20 dwords mod 64 makes the first
+  // conflict-free and the second at most 2-way.
+  constexpr int QS = D + 40;
+  constexpr int QT = BM * QS;
+  constexpr int SS = BM + 40;            // dS tile [BN keys][BM queries]
+  constexpr int UQ = BM * CH / 256;      // chunks per thread per Q (or dO) tile
+  constexpr int NPAIR = (BM / 32) * NB / 4;  // (q-block, d-block) dQ pairs per wave
+  static_assert(NPAIR == 1 || NPAIR == 2, "dQ work split");
+  static_assert(BN * QS <= 2 * QT, "K staging fits in the Q buffers");
+  __shared__ __attribute__((aligned(16))) T sQ[2 * QT];
+  __shared__ __attribute__((aligned(16))) T sdO[2 * QT];
+  __shared__ __attribute__((aligned(16))) T sdS[DQ ? BN * SS : 8];
+  __shared__ __attribute__((aligned(16))) float sL[2 * BM];
+  __shared__ __attribute__((aligned(16))) float sDl[2 * BM];
+
+  const int nblk = a.B * a.Hk * a.nkt * a.split;
+  const int W = xcd_remap(blockIdx.x, nblk);
+  const int per_bk = a.split * a.nkt;
+  const int bk = W / per_bk;
+  const int rem = W - bk * per_bk;
+  const int sp = rem / a.nkt;
+  const int kt = rem - sp * a.nkt;        // ascending = most causal work first
+  const int b = bk / a.Hk, kvh = bk - b * a.Hk;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, hf = lane >> 5;
+  const int Tq = a.Tq, Tk = a.Tk;
+  const int kt0 = kt * BN, kw0 = kt0 + wave * 32;
+  const int key = kw0 + l32;              // this lane's key (column of S)
+  const float c2 = a.scale_log2, scale = a.scale;
+  const int tr_row = (lane >> 2) & 3;
+  const int tr_col = ((lane >> 4) & 1) * 16 + (lane & 3) * 4;
+
+  const T* __restrict__ kp = (const T*)a.k + b * a.ksb + kvh * a.ksh;
+  const T* __restrict__ vp = (const T*)a.v + b * a.vsb + kvh * a.vsh;
+
+  // K, V fragments: B operands of S = Q K^T and dP = dO V^T.
+  V8 kf[DS], vf[DS];
+  if (key < Tk) {
+#pragma unroll
+    for (int ds = 0; ds < DS; ++ds) {
+      kf[ds] = as_vec8<T>(gload16(kp + (int64_t)key * a.kst + ds * 16 + hf * 8));
+      vf[ds] = as_vec8<T>(gload16(vp + (int64_t)key * a.vst + ds * 16 + hf * 8));
+    }
+  } else {
+#pragma unroll
+    for (int ds = 0; ds < DS; ++ds) {
+      kf[ds] = as_vec8<T>(u32x4{0, 0, 0, 0});
+      vf[ds] = as_vec8<T>(u32x4{0, 0, 0, 0});
+    }
+  }
+
+  // K^T fragment for dQ = dS K: B[key slot][d], k-step s covers block keys
+  // 16 s .. 16 s + 15, slot (hf, t) <-> key 16 s + 8 hf + t.
+  const int db = (wave * NPAIR) / 2;      // this wave's 32-wide d block of dQ
+  V8 ktf[DQ ? 8 : 1];
+  if constexpr (DQ) {
+#pragma unroll
+    for (int u = 0; u < BN * CH / 256; ++u) {
+      const int idx = tid + u * 256;
+      const int r = idx / CH, c = idx % CH;
+      const int kk = kt0 + r;
+      const u32x4 x = kk < Tk ? gload16(kp + (int64_t)kk * a.kst + c * 8) : u32x4{0, 0, 0, 0};
+      lds_write16(sQ + r * QS + c * 8, x);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      const int row = s * 16 + 8 * hf + tr_row;
+      const int col = db * 32 + tr_col;
+      ktf[s] = cat_tr<T>(lds_read_tr(sQ + row * QS + col), lds_read_tr(sQ + (row + 4) * QS + col));
+    }
+    __syncthreads();
+  }
+
+  const int gsz = a.G / a.split;
+  const int g0 = sp * gsz;
+  const int qt_first = CAUSAL ? kt0 / BM : 0;
+  const int nqt = (Tq + BM - 1) / BM;
+  const int nq = max(0, nqt - qt_first);
+  const int iters = gsz * nq;
+
+  u32x4 qreg[UQ], dreg[UQ];
+  float lreg = 0.f;
+  auto load_q = [&](int it) {
+    const int g = g0 + it / nq, qt = qt_first + it % nq;
+    const int h = kvh * a.G + g, qs = qt * BM;
+    const T* qp = (const T*)a.q + b * a.qsb + h * a.qsh;
+    const T* dp = (const T*)a.dout + b * a.dsb + h * a.dsh;
+#pragma unroll
+    for (int u = 0; u < UQ; ++u) {
+      const int idx = tid + u * 256;
+      const int r = idx / CH, c = idx % CH;
+      const int row = qs + r;
+      if (row < Tq) {
+        qreg[u] = gload16(qp + (int64_t)row * a.qst + c * 8);
+        dreg[u] = gload16(dp + (int64_t)row * a.dst + c * 8);
+      } else {
+        qreg[u] = u32x4{0, 0, 0, 0};
+        dreg[u] = u32x4{0, 0, 0, 0};
+      }
+    }
+    if (tid < BM) {
+      const int row = qs + tid;
+      lreg = row < Tq ? a.lse[((int64_t)b * a.Hq + h) * Tq + row] : kPosInf;
+    } else if (tid < 2 * BM) {
+      const int row = qs + tid - BM;
+      lreg = row < Tq ? a.delta[((int64_t)b * a.Hq + h) * Tq + row] : 0.f;
+    }
+  };
+  auto store_q = [&](int buf) {
+#pragma unroll
+    for (int u = 0; u < UQ; ++u) {
+      const int idx = tid + u * 256;
+      const int r = idx / CH, c = idx % CH;
+      lds_write16(sQ + buf * QT + r * QS + c * 8, qreg[u]);
+      lds_write16(sdO + buf * QT + r * QS + c * 8, dreg[u]);
+    }
+    if (tid < BM) sL[buf * BM + tid] = lreg;
+    else if (tid < 2 * BM) sDl[buf * BM + tid - BM] = lreg;
+  };
+
+  f32x16 dk[NB], dv[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) { dk[nb] = f32x16{}; dv[nb] = f32x16{}; }
+
+  if (iters > 0) {
+    load_q(0);
+    store_q(0);
+  }
+  __syncthreads();
+
+  for (int it = 0; it < iters; ++it) {
+    const int buf = it & 1;
+    const int g = g0 + it / nq, qt = qt_first + it % nq;
+    const int h = kvh * a.G + g, qs = qt * BM;
+    if (it + 1 < iters) load_q(it + 1);
+    const T* Qs = sQ + buf * QT;
+    const T* dOs = sdO + buf * QT;
+    const bool active = !CAUSAL || (qs + BM - 1 >= kw0);
+    if (active) {
+      // ---- S = Q K^T, dP = dO V^T ----------------------------------------------
+      f32x16 sacc[2], pacc[2];
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) {
+        sacc[qb] = f32x16{};
+        pacc[qb] = f32x16{};
+#pragma unroll
+        for (int ds = 0; ds < DS; ++ds) {
+          const u32x4 xq = lds_read16(Qs + (qb * 32 + l32) * QS + ds * 16 + hf * 8);
+          sacc[qb] = mfma32(as_vec8<T>(xq), kf[ds], sacc[qb]);
+          const u32x4 xd = lds_read16(dOs + (qb * 32 + l32) * QS + ds * 16 + hf * 8);
+          pacc[qb] = mfma32(as_vec8<T>(xd), vf[ds], pacc[qb]);
+        }
+      }
+      // lane's entry (qb, i) is query qs + 32 qb + 8 (i/4) + 4 hf + i%4, key `key`
+
+      // ---- P and dS ------------------------------------------------------------
+      const bool edge = MASK || (CAUSAL && kw0 + 31 > qs);
+      const int kc = min(key, Tk - 1);
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+        for (int gi = 0; gi < 4; ++gi) {
+          const int qr0 = qb * 32 + gi * 8 + hf * 4;
+          const f32x4 L4 = *(const FA_LDS f32x4*)(uintptr_t)(sL + buf * BM + qr0);
+          const f32x4 D4 = *(const FA_LDS f32x4*)(uintptr_t)(sDl + buf * BM + qr0);
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const int i = gi * 4 + t;
+            const int q = qs + qr0 + t;
+            const int qc = min(q, Tq - 1);
+            float s = sacc[qb][i];
+            if constexpr (SCORE) {
+              const float sc = a.score[b * a.ssb + h * a.ssh + (int64_t)qc * a.ssq + kc];
+              s += key < Tk ? sc : 0.f;
+            }
+            if (a.zero_scale) s = 0.f;
+            float p = exp2_fast(fmaf(s, c2, -L4[t]));
+            if (edge) {
+              bool keep = true;
+              if constexpr (CAUSAL) keep = key <= q;
+              if constexpr (MASK) keep = keep && key < Tk && a.mask[b * a.msb + h * a.msh + (int64_t)qc * a.msq + kc] != 0;
+              p = keep ? p : 0.f;
+            }
+            sacc[qb][i] = p;
+            pacc[qb][i] = p * (pacc[qb][i] - D4[t]) * scale;
+          }
+        }
+
+      // ---- dV += P^T dO, dK += dS^T Q --------------------------------------------
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          const V8 pa = pack8<T>(sacc[qb][8 * c + 0], sacc[qb][8 * c + 1], sacc[qb][8 * c + 2], sacc[qb][8 * c + 3],
+                                 sacc[qb][8 * c + 4], sacc[qb][8 * c + 5], sacc[qb][8 * c + 6], sacc[qb][8 * c + 7]);
+          const V8 dsa = pack8<T>(pacc[qb][8 * c + 0], pacc[qb][8 * c + 1], pacc[qb][8 * c + 2], pacc[qb][8 * c + 3],
+                                  pacc[qb][8 * c + 4], pacc[qb][8 * c + 5], pacc[qb][8 * c + 6], pacc[qb][8 * c + 7]);
+          const int row = qb * 32 + 16 * c + 4 * hf + tr_row;
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb) {
+            const int col = nb * 32 + tr_col;
+            const V8 bo = cat_tr<T>(lds_read_tr(dOs + row * QS + col), lds_read_tr(dOs + (row + 8) * QS + col));
+            dv[nb] = mfma32(pa, bo, dv[nb]);
+            const V8 bq = cat_tr<T>(lds_read_tr(Qs + row * QS + col), lds_read_tr(Qs + (row + 8) * QS + col));
+            dk[nb] = mfma32(dsa, bq, dk[nb]);
+          }
+        }
+      if constexpr (DQ) {
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+          for (int gi = 0; gi < 4; ++gi)
+            lds_write8(sdS + (wave * 32 + l32) * SS + qb * 32 + gi * 8 + hf * 4,
+                       pack4<T>(pacc[qb][gi * 4 + 0], pacc[qb][gi * 4 + 1], pacc[qb][gi * 4 + 2], pacc[qb][gi * 4 + 3]));
+      }
+    } else if constexpr (DQ) {
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+        for (int gi = 0; gi < 4; ++gi)
+          lds_write8(sdS + (wave * 32 + l32) * SS + qb * 32 + gi * 8 + hf * 4, u32x2{0u, 0u});
+    }
+
+    if constexpr (DQ) {
+      __syncthreads();  // every wave's dS is in LDS
+      // ---- dQ = dS K over the workgroup's 128 keys, atomically added -----------
+#pragma unroll
+      for (int pp = 0; pp < NPAIR; ++pp) {
+        const int qb = (wave * NPAIR + pp) & 1;
+        f32x16 acc = f32x16{};
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+          const int row = s * 16 + 8 * hf + tr_row;
+          const int col = qb * 32 + tr_col;
+          const V8 av = cat_tr<T>(lds_read_tr(sdS + row * SS + col), lds_read_tr(sdS + (row + 4) * SS + col));
+          acc = mfma32(av, ktf[s], acc);
+        }
+        float* dqp = a.dq_accum + (int64_t)h * D + db * 32 + l32;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int q = qs + qb * 32 + 8 * (i >> 2) + 4 * hf + (i & 3);
+          if (q < Tq) unsafeAtomicAdd(dqp + ((int64_t)b * Tq + q) * a.Hq * D, acc[i]);
+        }
+      }
+    }
+
+    if (it + 1 < iters) store_q(buf ^ 1);
+    __syncthreads();
+  }
+
+  // ---- epilogue: dK, dV (dV of a kv-head with a dead row is NaN) ----------------
+  const bool dead = a.dead[b * a.Hk + kvh] != 0;
+  const float nanv = __builtin_nanf("");
+  if (a.split == 1) {
+    T* dkp = (T*)a.dk + b * a.dksb + kvh * a.dksh;
+    T* dvp = (T*)a.dv + b * a.dvsb + kvh * a.dvsh;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int kr = kw0 + 8 * (i >> 2) + 4 * hf + (i & 3);
+        if (kr < Tk) {
+          dkp[(int64_t)kr * a.dkst + nb * 32 + l32] = (T)dk[nb][i];
+          dvp[(int64_t)kr * a.dvst + nb * 32 + l32] = (T)(dead ? nanv : dv[nb][i]);
+        }
+      }
+  } else {
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int kr = kw0 + 8 * (i >> 2) + 4 * hf + (i & 3);
+        if (kr < Tk) {
+          const int64_t o = (((int64_t)b * Tk + kr) * a.Hk + kvh) * D + nb * 32 + l32;
+          unsafeAtomicAdd(a.dk_accum + o, dk[nb][i]);
+          unsafeAtomicAdd(a.dv_accum + o, dead ? nanv : dv[nb][i]);
+        }
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// deterministic dQ
+// ---------------------------------------------------------------------------
+constexpr int kDqBM = 128;   // query rows per workgroup (4 waves x 32)
+constexpr int kDqBN = 64;    // keys per tile
+
+template <typename T, int D, bool CAUSAL, bool MASK, bool SCORE>
+__global__ __launch_bounds__(256, 1) void dq_kernel(const BwdArgs a) {
+  using V8 = typename Vec8<T>::type;
+  constexpr int BM = kDqBM, BN = kDqBN;
+  constexpr int DS = D / 16, NB = D / 32, CH = D / 8;
+  constexpr int KS = D + 40;   // K: row-wise and transposed reads
+  constexpr int VS = D + 8;    // V: row-wise reads only
+  constexpr int KT = BN * KS, VT = BN * VS;
+  constexpr int U = BN * CH / 256;
+  constexpr int OS = D + 8;
+  static_assert(4 * 32 * OS <= 2 * (KT + VT), "dQ staging fits");
+  __shared__ __attribute__((aligned(16))) T smem[2 * (KT + VT)];
+
+  const int nblk = a.B * a.Hq * a.nqt;
+  const int W = xcd_remap(blockIdx.x, nblk);
+  const int per_kv = a.G * a.nqt;
+  const int bk = W / per_kv;
+  const int rem = W - bk * per_kv;
+  const int qt_rev = rem / a.G;
+  const int g = rem - qt_rev * a.G;
+  const int qt = a.nqt - 1 - qt_rev;
+  const int b = bk / a.Hk, kvh = bk - b * a.Hk;
+  const int h = kvh * a.G + g;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, hf = lane >> 5;
+  const int q0 = qt * BM, q0w = q0 + wave * 32;
+  const int qrow = q0w + l32;
+  const int Tq = a.Tq, Tk = a.Tk;
+  const float c2 = a.scale_log2, scale = a.scale;
+
+  const T* __restrict__ qp = (const T*)a.q + b * a.qsb + h * a.qsh;
+  const T* __restrict__ dp = (const T*)a.dout + b * a.dsb + h * a.dsh;
+  const T* __restrict__ kp = (const T*)a.k + b * a.ksb + kvh * a.ksh;
+  const T* __restrict__ vp = (const T*)a.v + b * a.vsb + kvh * a.vsh;
+
+  V8 qf[DS], dof[DS];
+  float lse_q = kPosInf, delta_q = 0.f;
+  if (qrow < Tq) {
+#pragma unroll
+    for (int ds = 0; ds < DS; ++ds) {
+      qf[ds] = as_vec8<T>(gload16(qp + (int64_t)qrow * a.qst + ds * 16 + hf * 8));
+      dof[ds] = as_vec8<T>(gload16(dp + (int64_t)qrow * a.dst + ds * 16 + hf * 8));
+    }
+    lse_q = a.lse[((int64_t)b * a.Hq + h) * Tq + qrow];
+    delta_q = a.delta[((int64_t)b * a.Hq + h) * Tq + qrow];
+  } else {
+#pragma unroll
+    for (int ds = 0; ds < DS; ++ds) {
+      qf[ds] = as_vec8<T>(u32x4{0, 0, 0, 0});
+      dof[ds] = as_vec8<T>(u32x4{0, 0, 0, 0});
+    }
+  }
+  const int qrow_c = min(qrow, Tq - 1);
+  const uint8_t* mrow = nullptr;
+  const float* srow = nullptr;
+  if constexpr (MASK) mrow = a.mask + b * a.msb + h * a.msh + (int64_t)qrow_c * a.msq;
+  if constexpr (SCORE) srow = a.score + b * a.ssb + h * a.ssh + (int64_t)qrow_c * a.ssq;
+
+  const int kv_end = CAUSAL ? min(Tk, q0 + BM) : Tk;
+  const int ntiles = (kv_end + BN - 1) / BN;
+
+  u32x4 kreg[U], vreg[U];
+  auto load_tile = [&](int k0) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int idx = tid + u * 256;
+      const int r = idx / CH, c = idx % CH;
+      const int kk = k0 + r;
+      if (kk < Tk) {
+        kreg[u] = gload16(kp + (int64_t)kk * a.kst + c * 8);
+        vreg[u] = gload16(vp + (int64_t)kk * a.vst + c * 8);
+      } else {
+        kreg[u] = u32x4{0, 0, 0, 0};
+        vreg[u] = u32x4{0, 0, 0, 0};
+      }
+    }
+  };
+  auto store_tile = [&](int buf) {
+    T* ks = smem + buf * (KT + VT);
+    T* vs = ks + KT;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int idx = tid + u * 256;
+      const int r = idx / CH, c = idx % CH;
+      lds_write16(ks + r * KS + c * 8, kreg[u]);
+      lds_write16(vs + r * VS + c * 8, vreg[u]);
+    }
+  };
+
+  f32x16 qacc[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) qacc[nb] = f32x16{};
+  const int tr_row = 4 * hf + ((lane >> 2) & 3);
+  const int tr_col = ((lane >> 4) & 1) * 16 + (lane & 3) * 4;
+
+  load_tile(0);
+  store_tile(0);
+  __syncthreads();
+  for (int j = 0; j < ntiles; ++j) {
+    const int k0 = j * BN;
+    const bool more = j + 1 < ntiles;
+    if (more) load_tile(k0 + BN);
+    const T* ks = smem + (j & 1) * (KT + VT);
+    const T* vs = ks + KT;
+    const bool active = !CAUSAL || (k0 <= q0w + 31);
+    if (active) {
+      f32x16 sacc[2], pacc[2];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        sacc[kb] = f32x16{};
+        pacc[kb] = f32x16{};
+#pragma unroll
+        for (int ds = 0; ds < DS; ++ds) {
+          const u32x4 kx = lds_read16(ks + (kb * 32 + l32) * KS + ds * 16 + hf * 8);
+          sacc[kb] = mfma32(as_vec8<T>(kx), qf[ds], sacc[kb]);
+          const u32x4 vx = lds_read16(vs + (kb * 32 + l32) * VS + ds * 16 + hf * 8);
+          pacc[kb] = mfma32(as_vec8<T>(vx), dof[ds], pacc[kb]);
+        }
+      }
+      const bool edge = MASK || (k0 + BN > Tk) || (CAUSAL && k0 + BN - 1 > q0w);
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int gi = 0; gi < 4; ++gi) {
+          const int kk = k0 + kb * 32 + gi * 8 + hf * 4;
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const int i = gi * 4 + t;
+            const int kx = kk + t;
+            float s = sacc[kb][i];
+            if constexpr (SCORE) s += kx < Tk ? srow[kx] : 0.f;
+            if (a.zero_scale) s = 0.f;
+            float p = exp2_fast(fmaf(s, c2, -lse_q));
+            if (edge) {
+              bool keep = kx < Tk;
+              if constexpr (CAUSAL) keep = keep && kx <= qrow;
+              if constexpr (MASK) keep = keep && mrow[min(kx, Tk - 1)] != 0;
+              p = keep ? p : 0.f;
+            }
+            sacc[kb][i] = p * (pacc[kb][i] - delta_q) * scale;
+          }
+        }
+      // dQ^T += K^T dS^T: A = K^T via transpose reads, B = dS^T from registers
+#pragma unroll
+      for (int kk2 = 0; kk2 < 4; ++kk2) {
+        const int kb = kk2 >> 1, c = kk2 & 1;
+        const V8 dsb = pack8<T>(sacc[kb][8 * c + 0], sacc[kb][8 * c + 1], sacc[kb][8 * c + 2], sacc[kb][8 * c + 3],
+                                sacc[kb][8 * c + 4], sacc[kb][8 * c + 5], sacc[kb][8 * c + 6], sacc[kb][8 * c + 7]);
+        const int row = kb * 32 + 16 * c + tr_row;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+          const int col = nb * 32 + tr_col;
+          const V8 ak = cat_tr<T>(lds_read_tr(ks + row * KS + col), lds_read_tr(ks + (row + 8) * KS + col));
+          qacc[nb] = mfma32(ak, dsb, qacc[nb]);
+        }
+      }
+    }
+    if (more) store_tile((j + 1) & 1);
+    __syncthreads();
+  }
+
+  T* os = smem + wave * 32 * OS;
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+    for (int gi = 0; gi < 4; ++gi)
+      lds_write8(os + l32 * OS + nb * 32 + gi * 8 + hf * 4,
+                 pack4<T>(qacc[nb][gi * 4 + 0], qacc[nb][gi * 4 + 1], qacc[nb][gi * 4 + 2], qacc[nb][gi * 4 + 3]));
+  __syncthreads();
+  T* dqp = (T*)a.dq + b * a.dqsb + h * a.dqsh;
+#pragma unroll
+  for (int u = 0; u < 32 * CH / 64; ++u) {
+    const int idx = lane + u * 64;
+    const int r = idx / CH, c = idx % CH;
+    const int qr = q0w + r;
+    if (qr < Tq) gstore16(dqp + (int64_t)qr * a.dqst + c * 8, lds_read16(os + r * OS + c * 8));
+  }
+}
+
+// ---------------------------------------------------------------------------
+// fp32 accumulator -> dtype
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(256) void convert_kernel(const CvtArgs a) {
+  const int64_t nchunk = (int64_t)a.B * a.T * a.H * (a.D / 8);
+  const int cpr = a.D / 8;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < nchunk; i += (int64_t)gridDim.x * 256) {
+    const int c = (int)(i % cpr);
+    int64_t rest = i / cpr;
+    const int hh = (int)(rest % a.H); rest /= a.H;
+    const int t = (int)(rest % a.T);
+    const int bb = (int)(rest / a.T);
+    const float* s = a.src + i * 8;
+    const f32x4 x0 = *(const f32x4*)s, x1 = *(const f32x4*)(s + 4);
+    const auto v = pack8<T>(x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]);
+    T* d = (T*)a.dst + bb * a.sb + (int64_t)t * a.st + hh * a.sh + c * 8;
+    gstore16(d, as_u32x4<T>(v));
+  }
+}
+
+template <typename T, int D, bool CAUSAL, bool DQ>
+hipError_t launch_dkdv_t(const BwdArgs& a, hipStream_t s) {
+  const dim3 grid((unsigned)(a.B * a.Hk * a.nkt * a.split)), block(256);
+  const bool m = a.mask != nullptr, sc = a.score != nullptr;
+  if (m && sc) hipLaunchKernelGGL((dkdv_kernel<T, D, CAUSAL, true, true, DQ>), grid, block, 0, s, a);
+  else if (m) hipLaunchKernelGGL((dkdv_kernel<T, D, CAUSAL, true, false, DQ>), grid, block, 0, s, a);
+  else if (sc) hipLaunchKernelGGL((dkdv_kernel<T, D, CAUSAL, false, true, DQ>), grid, block, 0, s, a);
+  else hipLaunchKernelGGL((dkdv_kernel<T, D, CAUSAL, false, false, DQ>), grid, block, 0, s, a);
+  return hipGetLastError();
+}
+
+template <typename T, int D>
+hipError_t launch_dkdv_d(const BwdArgs& a, bool causal, hipStream_t s) {
+  if (a.do_dq) return causal ? launch_dkdv_t<T, D, true, true>(a, s) : launch_dkdv_t<T, D, false, true>(a, s);
+  return causal ? launch_dkdv_t<T, D, true, false>(a, s) : launch_dkdv_t<T, D, false, false>(a, s);
+}
+
+template <typename T, int D, bool CAUSAL>
+hipError_t launch_dq_t(const BwdArgs& a, hipStream_t s) {
+  const dim3 grid((unsigned)(a.B * a.Hq * a.nqt)), block(256);
+  const bool m = a.mask != nullptr, sc = a.score != nullptr;
+  if (m && sc) hipLaunchKernelGGL((dq_kernel<T, D, CAUSAL, true, true>), grid, block, 0, s, a);
+  else if (m) hipLaunchKernelGGL((dq_kernel<T, D, CAUSAL, true, false>), grid, block, 0, s, a);
+  else if (sc) hipLaunchKernelGGL((dq_kernel<T, D, CAUSAL, false, true>), grid, block, 0, s, a);
+  else hipLaunchKernelGGL((dq_kernel<T, D, CAUSAL, false, false>), grid, block, 0, s, a);
+  return hipGetLastError();
+}
+
+template <typename T>
+hipError_t launch_pre_t(const PreArgs& a, int D, hipStream_t s) {
+  const dim3 grid((unsigned)((a.Tq + 63) / 64), (unsigned)a.Hq, (unsigned)a.B), block(256);
+  if (D == 128) hipLaunchKernelGGL((preprocess_kernel<T, 128>), grid, block, 0, s, a);
+  else if (D == 64) hipLaunchKernelGGL((preprocess_kernel<T, 64>), grid, block, 0, s, a);
+  else return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+}  // namespace
+
+int dkdv_block_keys() { return kKvBN; }
+int dq_block_rows() { return kDqBM; }
+
+hipError_t launch_preprocess(const PreArgs& a, int D, int dtype, hipStream_t s) {
+  return dtype == 0 ? launch_pre_t<bf16>(a, D, s) : launch_pre_t<f16>(a, D, s);
+}
+
+hipError_t launch_bwd_dkdv(const BwdArgs& a, int D, int dtype, bool causal, hipStream_t s) {
+  if (dtype == 0) {
+    if (D == 128) return launch_dkdv_d<bf16, 128>(a, causal, s);
+    if (D == 64) return launch_dkdv_d<bf16, 64>(a, causal, s);
+  } else {
+    if (D == 128) return launch_dkdv_d<f16, 128>(a, causal, s);
+    if (D == 64) return launch_dkdv_d<f16, 64>(a, causal, s);
+  }
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_bwd_dq(const BwdArgs& a, int D, int dtype, bool causal, hipStream_t s) {
+  if (dtype == 0) {
+    if (D == 128) return causal ? launch_dq_t<bf16, 128, true>(a, s) : launch_dq_t<bf16, 128, false>(a, s);
+    if (D == 64) return causal ? launch_dq_t<bf16, 64, true>(a, s) : launch_dq_t<bf16, 64, false>(a, s);
+  } else {
+    if (D == 128) return causal ? launch_dq_t<f16, 128, true>(a, s) : launch_dq_t<f16, 128, false>(a, s);
+    if (D == 64) return causal ? launch_dq_t<f16, 64, true>(a, s) : launch_dq_t<f16, 64, false>(a, s);
+  }
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_convert(const CvtArgs& a, int dtype, hipStream_t s) {
+  const int64_t nchunk = (int64_t)a.B * a.T * a.H * (a.D / 8);
+  int64_t blocks = (nchunk + 255) / 256;
+  if (blocks > 65536) blocks = 65536;
+  if (blocks < 1) blocks = 1;
+  if (dtype == 0) hipLaunchKernelGGL((convert_kernel<bf16>), dim3((unsigned)blocks), dim3(256), 0, s, a);
+  else hipLaunchKernelGGL((convert_kernel<f16>), dim3((unsigned)blocks), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+}  // namespace fa

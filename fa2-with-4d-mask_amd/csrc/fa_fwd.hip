@@ -1,0 +1,329 @@
+// FlashAttention-2 forward for gfx950 (MI355X) with optional 4D keep-mask and
+// 4D fp32 score.  Restates the maths of the reference's TileLang forward
+// (python/fa2.py:22-139) as a hand-written wave64 MFMA kernel.
+//
+// Work decomposition: one workgroup of 4 waves per (128 query rows, query
+// head, batch); each wave owns 32 query rows and walks the key axis in tiles
+// of 64 keys.  Per tile and wave:
+//   S^T[key, q] = K Q^T        32x32x16 MFMA, A = K rows from LDS, B = Q
+//                              fragment resident in registers
+//   online softmax in base 2   each lane owns one query row (32 keys of it),
+//                              the other half of the row sits in lane ^ 32
+//   O^T[d, q] += V^T P^T       A = V^T via ds_read_b64_tr_b16 from the
+//                              row-major V tile, B = P straight from the S^T
+//                              accumulator registers (no LDS round trip)
+// K/V tiles are double-buffered in LDS (prefetched into registers one tile
+// ahead).  The running maximum is only moved when a tile's maximum exceeds it
+// by more than 2^8 (exact: O and l are rescaled consistently; p <= 256), which
+// removes the accumulator rescale from almost every tile.
+#include "fa_common.h"
+#include "fa_kernels.h"
+
+namespace fa {
+namespace {
+
+constexpr int kBM = 128;        // query rows per workgroup
+constexpr int kBN = 64;         // keys per tile
+constexpr int kThreads = 256;
+constexpr float kRescaleLog2 = 8.0f;
+
+__device__ __forceinline__ uint32_t load_mask4(const uint8_t* row, int kk, int Tk, bool vec) {
+  if (vec && kk + 4 <= Tk) return *(const uint32_t*)(row + kk);
+  uint32_t r = 0;
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+    if (kk + t < Tk) r |= (uint32_t)(row[kk + t] != 0) << (8 * t);
+  return r;
+}
+
+__device__ __forceinline__ f32x4 load_score4(const float* row, int kk, int Tk, bool vec) {
+  if (vec && kk + 4 <= Tk) return *(const f32x4*)(row + kk);
+  f32x4 r;
+#pragma unroll
+  for (int t = 0; t < 4; ++t) r[t] = (kk + t < Tk) ? row[kk + t] : 0.f;
+  return r;
+}
+
+template <typename T>
+__device__ __forceinline__ u32x2 pack4(float x0, float x1, float x2, float x3) {
+  typedef T T4 __attribute__((ext_vector_type(4)));
+  T4 v;
+  v[0] = (T)x0; v[1] = (T)x1; v[2] = (T)x2; v[3] = (T)x3;
+  return __builtin_bit_cast(u32x2, v);
+}
+
+template <typename T, int D, bool CAUSAL, bool MASK, bool SCORE>
+__global__ __launch_bounds__(kThreads, 2) void fwd_kernel(const FwdArgs a) {
+  using V8 = typename Vec8<T>::type;
+  constexpr int BM = kBM, BN = kBN;
+  constexpr int DS = D / 16;            // k-steps of S^T
+  constexpr int NB = D / 32;            // 32-wide d blocks of O^T
+  constexpr int CH = D / 8;             // 16-byte chunks per row
+  // Padded row strides (elements): K rows are read 16 rows x 16 B at a time
+  // (stride = 4 dwords mod 64 banks), V rows by the transpose read 4 rows x
+  // 64 B at a time (stride = 16 dwords mod 64 banks): both conflict-free, and
+  // every LDS address is a per-lane base plus an immediate offset.
+  constexpr int KS = D + 8, VS = D + 32;
+  constexpr int KT = BN * KS, VT = BN * VS;  // elements of one K / V tile
+  constexpr int U = BN * CH / kThreads; // 16-byte chunks per thread per tile
+  constexpr int OS = D + 8;             // epilogue O staging stride
+  static_assert(4 * 32 * OS <= 2 * (KT + VT), "O staging fits in the K/V buffers");
+  __shared__ __attribute__((aligned(16))) T smem[2 * (KT + VT)];  // K0 V0 K1 V1
+
+  // ---- which (batch, head, query tile) -------------------------------------
+  // Logical order (b, kv-head, [query tile descending, head in group]); with
+  // the XCD remap each XCD works on few kv-heads (K/V stay in its L2) and
+  // causal work is dispatched longest-first.
+  const int nblk = a.B * a.Hq * a.nqt;
+  const int W = xcd_remap(blockIdx.x, nblk);
+  const int per_kv = a.G * a.nqt;
+  const int bk = W / per_kv;
+  const int rem = W - bk * per_kv;
+  const int qt_rev = rem / a.G;
+  const int g = rem - qt_rev * a.G;
+  const int qt = a.nqt - 1 - qt_rev;
+  const int b = bk / a.Hk, kvh = bk - b * a.Hk;
+  const int h = kvh * a.G + g;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, hf = lane >> 5;
+  const int q0 = qt * BM, q0w = q0 + wave * 32;
+  const int qrow = q0w + l32;
+  const int Tq = a.Tq, Tk = a.Tk;
+
+  const T* __restrict__ qp = (const T*)a.q + b * a.qsb + h * a.qsh;
+  const T* __restrict__ kp = (const T*)a.k + b * a.ksb + kvh * a.ksh;
+  const T* __restrict__ vp = (const T*)a.v + b * a.vsb + kvh * a.vsh;
+
+  // ---- Q fragment: lane holds Q[qrow][16 ds + 8 hf + 0..7] -------------------
+  V8 qf[DS];
+  {
+    const uint32_t neg = a.qsign < 0.f ? 0x80008000u : 0u;
+    if (qrow < Tq) {
+      const T* src = qp + (int64_t)qrow * a.qst + hf * 8;
+#pragma unroll
+      for (int ds = 0; ds < DS; ++ds) {
+        u32x4 x = gload16(src + ds * 16);
+        x ^= neg;
+        qf[ds] = as_vec8<T>(x);
+      }
+    } else {
+#pragma unroll
+      for (int ds = 0; ds < DS; ++ds) qf[ds] = as_vec8<T>(u32x4{0, 0, 0, 0});
+    }
+  }
+
+  const int kv_end = CAUSAL ? min(Tk, q0 + BM) : Tk;
+  const int ntiles = (kv_end + BN - 1) / BN;
+
+  u32x4 kreg[U], vreg[U];
+  auto load_tile = [&](int k0) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int idx = tid + u * kThreads;
+      const int r = idx / CH, c = idx % CH;
+      const int key = k0 + r;
+      if (key < Tk) {
+        kreg[u] = gload16(kp + (int64_t)key * a.kst + c * 8);
+        vreg[u] = gload16(vp + (int64_t)key * a.vst + c * 8);
+      } else {
+        kreg[u] = u32x4{0, 0, 0, 0};
+        vreg[u] = u32x4{0, 0, 0, 0};
+      }
+    }
+  };
+  auto store_tile = [&](int buf) {
+    T* ks = smem + buf * (KT + VT);
+    T* vs = ks + KT;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int idx = tid + u * kThreads;
+      const int r = idx / CH, c = idx % CH;
+      lds_write16(ks + r * KS + c * 8, kreg[u]);
+      lds_write16(vs + r * VS + c * 8, vreg[u]);
+    }
+  };
+
+  const int qrow_c = min(qrow, Tq - 1);  // clamped row for mask/score reads
+  const uint8_t* mrow = nullptr;
+  const float* srow = nullptr;
+  if constexpr (MASK) mrow = a.mask + b * a.msb + h * a.msh + (int64_t)qrow_c * a.msq;
+  if constexpr (SCORE) srow = a.score + b * a.ssb + h * a.ssh + (int64_t)qrow_c * a.ssq;
+  const bool mvec = a.mask_vec != 0, svec = a.score_vec != 0;
+  const float c2 = a.scale_log2;
+
+  f32x16 oacc[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) oacc[nb] = f32x16{};
+  float m_run = kNegInf, l_run = 0.f;
+
+  load_tile(0);
+  store_tile(0);
+  __syncthreads();
+
+  for (int j = 0; j < ntiles; ++j) {
+    const int k0 = j * BN;
+    const bool more = j + 1 < ntiles;
+    if (more) load_tile(k0 + BN);
+    const T* ks = smem + (j & 1) * (KT + VT);
+    const T* vs = ks + KT;
+
+    // A wave whose 32 rows all precede the tile's first key has nothing to do.
+    const bool active = !CAUSAL || (k0 <= q0w + 31);
+    if (active) {
+      // ---- S^T = K Q^T ----------------------------------------------------------
+      f32x16 sacc[2];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        sacc[kb] = f32x16{};
+#pragma unroll
+        for (int ds = 0; ds < DS; ++ds) {
+          const u32x4 kx = lds_read16(ks + (kb * 32 + l32) * KS + ds * 16 + hf * 8);
+          sacc[kb] = mfma32(as_vec8<T>(kx), qf[ds], sacc[kb]);
+        }
+      }
+      // lane's entry (kb, i) is key k0 + 32 kb + 8 (i/4) + 4 hf + i%4 of row qrow
+
+      if constexpr (SCORE) {
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int gi = 0; gi < 4; ++gi) {
+            const f32x4 sc = load_score4(srow, k0 + kb * 32 + gi * 8 + hf * 4, Tk, svec);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) sacc[kb][gi * 4 + t] = fmaf(a.qsign, sc[t], sacc[kb][gi * 4 + t]);
+          }
+      }
+
+      const bool edge = MASK || a.zero_scale || (k0 + BN > Tk) || (CAUSAL && k0 + BN - 1 > q0w);
+      if (edge) {
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int gi = 0; gi < 4; ++gi) {
+            const int kk = k0 + kb * 32 + gi * 8 + hf * 4;
+            uint32_t mb = 0x01010101u;
+            if constexpr (MASK) mb = load_mask4(mrow, kk, Tk, mvec);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+              const int key = kk + t;
+              bool keep = key < Tk;
+              if constexpr (CAUSAL) keep = keep && (key <= qrow);
+              if constexpr (MASK) keep = keep && (((mb >> (8 * t)) & 0xffu) != 0);
+              const float s = sacc[kb][gi * 4 + t];
+              sacc[kb][gi * 4 + t] = keep ? (a.zero_scale ? 0.f : s) : kNegInf;
+            }
+          }
+      }
+
+      // ---- online softmax ---------------------------------------------------------
+      float mx = kNegInf;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, sacc[kb][i]);
+      mx = half_max(mx);
+      const float m_tile = mx * c2;
+      if (wave_any(m_tile > m_run + kRescaleLog2)) {
+        const float m_new = fmaxf(m_run, m_tile);
+        const float alpha = (m_run == kNegInf) ? 0.f : exp2_fast(m_run - m_new);
+        l_run *= alpha;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) oacc[nb][i] *= alpha;
+        m_run = m_new;
+      }
+      const float mneg = (m_run == kNegInf) ? 0.f : -m_run;
+      float lsum = 0.f;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const float p = exp2_fast(fmaf(sacc[kb][i], c2, mneg));
+          sacc[kb][i] = p;
+          lsum += p;
+        }
+      l_run += lsum;
+
+      // ---- O^T += V^T P^T -----------------------------------------------------------
+      const int tr_row = 4 * hf + ((lane >> 2) & 3);
+      const int tr_col = ((lane >> 4) & 1) * 16 + (lane & 3) * 4;
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const int kb = kk >> 1, c = kk & 1;
+        const V8 pb = pack8<T>(sacc[kb][8 * c + 0], sacc[kb][8 * c + 1], sacc[kb][8 * c + 2], sacc[kb][8 * c + 3],
+                               sacc[kb][8 * c + 4], sacc[kb][8 * c + 5], sacc[kb][8 * c + 6], sacc[kb][8 * c + 7]);
+        const int row = kb * 32 + 16 * c + tr_row;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+          const int col = nb * 32 + tr_col;
+          const s16x4 lo = lds_read_tr(vs + row * VS + col);
+          const s16x4 hi = lds_read_tr(vs + (row + 8) * VS + col);
+          oacc[nb] = mfma32(cat_tr<T>(lo, hi), pb, oacc[nb]);
+        }
+      }
+    }
+
+    if (more) store_tile((j + 1) & 1);
+    __syncthreads();
+  }
+
+  // ---- epilogue: O = acc / l (NaN for a row with no kept key), LSE ----------------
+  const float l_tot = half_sum(l_run);
+  const float inv = 1.0f / l_tot;
+  T* os = smem + wave * 32 * OS;  // wave-private staging, K/V buffers are free now
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+    for (int gi = 0; gi < 4; ++gi) {
+      const int d = nb * 32 + gi * 8 + hf * 4;
+      lds_write8(os + l32 * OS + d,
+                 pack4<T>(oacc[nb][gi * 4 + 0] * inv, oacc[nb][gi * 4 + 1] * inv, oacc[nb][gi * 4 + 2] * inv,
+                          oacc[nb][gi * 4 + 3] * inv));
+    }
+  __syncthreads();
+  T* op = (T*)a.o + b * a.osb + h * a.osh;
+#pragma unroll
+  for (int u = 0; u < 32 * CH / 64; ++u) {
+    const int idx = lane + u * 64;
+    const int r = idx / CH, c = idx % CH;
+    const int qr = q0w + r;
+    if (qr < Tq) gstore16(op + (int64_t)qr * a.ost + c * 8, lds_read16(os + r * OS + c * 8));
+  }
+  if (hf == 0 && qrow < Tq)
+    a.lse[((int64_t)b * a.Hq + h) * Tq + qrow] = (l_tot > 0.f) ? m_run + log2_fast(l_tot) : kPosInf;
+}
+
+template <typename T, int D, bool CAUSAL>
+hipError_t launch_fwd_t(const FwdArgs& a, hipStream_t s) {
+  const dim3 grid((unsigned)(a.B * a.Hq * a.nqt)), block(kThreads);
+  const bool m = a.mask != nullptr, sc = a.score != nullptr;
+  if (m && sc) hipLaunchKernelGGL((fwd_kernel<T, D, CAUSAL, true, true>), grid, block, 0, s, a);
+  else if (m) hipLaunchKernelGGL((fwd_kernel<T, D, CAUSAL, true, false>), grid, block, 0, s, a);
+  else if (sc) hipLaunchKernelGGL((fwd_kernel<T, D, CAUSAL, false, true>), grid, block, 0, s, a);
+  else hipLaunchKernelGGL((fwd_kernel<T, D, CAUSAL, false, false>), grid, block, 0, s, a);
+  return hipGetLastError();
+}
+
+template <typename T, int D>
+hipError_t launch_fwd_d(const FwdArgs& a, bool causal, hipStream_t s) {
+  return causal ? launch_fwd_t<T, D, true>(a, s) : launch_fwd_t<T, D, false>(a, s);
+}
+
+}  // namespace
+
+int fwd_block_rows() { return kBM; }
+
+hipError_t launch_fwd(const FwdArgs& a, int D, int dtype, bool causal, hipStream_t s) {
+  if (dtype == 0) {
+    if (D == 128) return launch_fwd_d<bf16, 128>(a, causal, s);
+    if (D == 64) return launch_fwd_d<bf16, 64>(a, causal, s);
+  } else {
+    if (D == 128) return launch_fwd_d<f16, 128>(a, causal, s);
+    if (D == 64) return launch_fwd_d<f16, 64>(a, causal, s);
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace fa

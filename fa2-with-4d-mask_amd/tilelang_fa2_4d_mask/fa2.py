@@ -1,0 +1,208 @@
+"""Autograd Function over the gfx950 FlashAttention-2 kernels.
+
+Host-side mirror of the reference's ``_flash_attention_with_4d_mask``
+(python/fa2.py:437-558): same positional signature
+``(Q, K, V, Mask, Score, scale, is_causal, use_atomic_backward, bhsd_input)``,
+same defaults (``scale = D**-0.5``, python/fa2.py:456), same rank assert
+(python/fa2.py:448), output in the input layout (python/fa2.py:488) and
+gradients for Q, K, V only (python/fa2.py:556).
+
+What differs on purpose:
+* no layout copies: the kernels take (batch, time, head) strides, so both a
+  BHSD view over BTHD storage and a BHSD-contiguous tensor are used in place
+  (the reference copies the latter, python/fa2.py:433-435, 449-452);
+* Mask/Score may be broadcast views ([B|1, Hq|1, Tq, Tk] with stride 0);
+* dQ/dK/dV come back in the input dtype directly (the reference returns fp32
+  dQ and lets autograd cast it, python/fa2.py:527,556);
+* ``use_atomic_backward=False`` selects a deterministic dQ kernel (the
+  reference's "reduce" path still adds dQ atomically, python/fa2.py:420-421).
+"""
+
+from __future__ import annotations
+
+import ctypes
+from typing import Optional
+
+import torch
+from torch.autograd.function import once_differentiable
+
+from . import _ext
+
+
+def _norm_strides(x: torch.Tensor) -> tuple:
+    """Strides with size-1 dimensions reported as 0 (never stepped over)."""
+    return tuple(0 if n == 1 else s for n, s in zip(x.shape, x.stride()))
+
+
+def _kernel_operand(x: torch.Tensor) -> torch.Tensor:
+    """A logical [B, T, H, D] operand the kernels can address: head dim
+    contiguous, rows 16-byte aligned.  Copies only when that does not hold."""
+    st = _norm_strides(x)
+    if x.stride(3) != 1 and x.shape[3] > 1:
+        return x.contiguous()
+    if any(s % 8 for s in st[:3]) or x.data_ptr() % 16:
+        return x.contiguous()
+    return x
+
+
+def _bthd_strides(x: torch.Tensor) -> tuple:
+    st = _norm_strides(x)
+    return st[0], st[1], st[2]
+
+
+def _kernel_side(x: Optional[torch.Tensor], dtype: Optional[torch.dtype], B: int, Hq: int, Tq: int, Tk: int,
+                 name: str, device: torch.device):
+    """Mask/Score as a broadcastable [B|1, Hq|1, Tq, Tk] view with a contiguous key axis."""
+    if x is None:
+        return None, (0, 0, 0)
+    if x.dim() != 4:
+        raise ValueError(f"{name} must have shape [B, H or 1, Tq, Tk]")
+    if x.device != device:
+        raise ValueError(f"{name} must be on {device}, got {x.device}")
+    if dtype is not None and x.dtype != dtype:
+        x = x.to(dtype)
+    if tuple(x.shape[-2:]) != (Tq, Tk) or x.shape[0] not in (1, B) or x.shape[1] not in (1, Hq):
+        raise ValueError(f"{name} has shape {tuple(x.shape)}, expected [{B} or 1, {Hq} or 1, {Tq}, {Tk}]")
+    if x.stride(3) != 1 and Tk > 1:
+        x = x.contiguous()
+    st = _norm_strides(x)
+    return x, (st[0], st[1], st[2])
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+class _flash_attention_with_4d_mask(torch.autograd.Function):
+    @staticmethod
+    def forward(
+        ctx,
+        Q: torch.Tensor,
+        K: torch.Tensor,
+        V: torch.Tensor,
+        Mask: Optional[torch.Tensor] = None,
+        Score: Optional[torch.Tensor] = None,
+        scale: Optional[float] = None,
+        is_causal: Optional[bool] = False,
+        use_atomic_backward: Optional[bool] = True,
+        bhsd_input: Optional[bool] = True,
+    ):
+        assert Q.dim() == 4 and K.dim() == 4 and V.dim() == 4
+        q = Q.transpose(1, 2) if bhsd_input else Q
+        k = K.transpose(1, 2) if bhsd_input else K
+        v = V.transpose(1, 2) if bhsd_input else V
+        B, Tq, Hq, D = q.shape
+        _, Tk, Hk, _ = k.shape
+        if scale is None:
+            scale = D ** -0.5
+        scale = float(scale)
+        if not q.is_cuda:
+            raise ValueError("flash_attention_with_4d_mask runs on the GPU: inputs must be HIP/CUDA tensors")
+        if k.device != q.device or v.device != q.device:
+            raise ValueError("query, key and value must be on the same device")
+        if k.dtype != q.dtype or v.dtype != q.dtype:
+            raise ValueError("query, key, and value must have the same dtype")
+        code = _ext.dtype_code(q.dtype)
+
+        mask, mst = _kernel_side(Mask, torch.bool, B, Hq, Tq, Tk, "mask", q.device)
+        score, sst = _kernel_side(Score, torch.float32, B, Hq, Tq, Tk, "score", q.device)
+
+        O = torch.empty((B, Tq, Hq, D), dtype=q.dtype, device=q.device)
+        LSE = torch.empty((B, Hq, Tq), dtype=torch.float32, device=q.device)
+        if B * Tq * Hq > 0:
+            if Tk == 0:
+                O.zero_()
+                LSE.fill_(float("-inf"))
+            else:
+                q = _kernel_operand(q)
+                k = _kernel_operand(k)
+                v = _kernel_operand(v)
+                p = _ext.FaFwdParams()
+                p.q, p.k, p.v, p.o, p.lse = q.data_ptr(), k.data_ptr(), v.data_ptr(), O.data_ptr(), LSE.data_ptr()
+                p.mask, p.score = _ext.ptr(mask), _ext.ptr(score)
+                p.q_stride_b, p.q_stride_t, p.q_stride_h = _bthd_strides(q)
+                p.k_stride_b, p.k_stride_t, p.k_stride_h = _bthd_strides(k)
+                p.v_stride_b, p.v_stride_t, p.v_stride_h = _bthd_strides(v)
+                p.o_stride_b, p.o_stride_t, p.o_stride_h = _bthd_strides(O)
+                p.mask_stride_b, p.mask_stride_h, p.mask_stride_q = mst
+                p.score_stride_b, p.score_stride_h, p.score_stride_q = sst
+                p.batch, p.seqlen_q, p.seqlen_k, p.heads_q, p.heads_k, p.head_dim = B, Tq, Tk, Hq, Hk, D
+                p.scale = scale
+                p.is_causal = 1 if is_causal else 0
+                p.dtype = code
+                p.stream = _stream(q.device)
+                lib = _ext.load_library()
+                _ext.check(lib.fa_fwd(ctypes.byref(p)), "fa_fwd", lib)
+
+        ctx.save_for_backward(q, k, v, O, LSE, mask, score)
+        ctx.scale = scale
+        ctx.is_causal = bool(is_causal)
+        ctx.use_atomic_backward = bool(use_atomic_backward)
+        ctx.mst, ctx.sst = mst, sst
+        ctx.bhsd_input = bool(bhsd_input)
+        return O.transpose(1, 2) if bhsd_input else O
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, dO: torch.Tensor):
+        q, k, v, O, LSE, mask, score = ctx.saved_tensors
+        do = dO.transpose(1, 2) if ctx.bhsd_input else dO
+        B, Tq, Hq, D = q.shape
+        _, Tk, Hk, _ = k.shape
+        dev = q.device
+        dQ = torch.empty((B, Tq, Hq, D), dtype=q.dtype, device=dev)
+        dK = torch.empty((B, Tk, Hk, D), dtype=q.dtype, device=dev)
+        dV = torch.empty((B, Tk, Hk, D), dtype=q.dtype, device=dev)
+        if B * Tq * Hq == 0 or Tk == 0:
+            dQ.zero_()
+            dK.zero_()
+            dV.zero_()
+        else:
+            do = _kernel_operand(do.to(q.dtype))
+            p = _ext.FaBwdParams()
+            p.batch, p.seqlen_q, p.seqlen_k, p.heads_q, p.heads_k, p.head_dim = B, Tq, Tk, Hq, Hk, D
+            p.scale = ctx.scale
+            p.is_causal = 1 if ctx.is_causal else 0
+            p.atomic_dq = 1 if ctx.use_atomic_backward else 0
+            p.kv_split = 0
+            p.dtype = _ext.dtype_code(q.dtype)
+            lib = _ext.load_library()
+            plan = _ext.FaBwdPlan()
+            _ext.check(lib.fa_bwd_plan(ctypes.byref(p), ctypes.byref(plan)), "fa_bwd_plan", lib)
+            p.kv_split = plan.kv_split
+
+            delta = torch.empty((B, Hq, Tq), dtype=torch.float32, device=dev)
+            dead = torch.zeros((B * Hk,), dtype=torch.int32, device=dev)
+            dq_acc = torch.empty((B, Tq, Hq, D), dtype=torch.float32, device=dev) if plan.needs_dq_accum else None
+            dk_acc = dv_acc = None
+            if plan.kv_split > 1:
+                dk_acc = torch.zeros((B, Tk, Hk, D), dtype=torch.float32, device=dev)
+                dv_acc = torch.zeros((B, Tk, Hk, D), dtype=torch.float32, device=dev)
+
+            p.q, p.k, p.v, p.o, p.dout = q.data_ptr(), k.data_ptr(), v.data_ptr(), O.data_ptr(), do.data_ptr()
+            p.lse, p.delta, p.dead_flags = LSE.data_ptr(), delta.data_ptr(), dead.data_ptr()
+            p.mask, p.score = _ext.ptr(mask), _ext.ptr(score)
+            p.dq_accum, p.dk_accum, p.dv_accum = _ext.ptr(dq_acc), _ext.ptr(dk_acc), _ext.ptr(dv_acc)
+            p.dq, p.dk, p.dv = dQ.data_ptr(), dK.data_ptr(), dV.data_ptr()
+            p.q_stride_b, p.q_stride_t, p.q_stride_h = _bthd_strides(q)
+            p.k_stride_b, p.k_stride_t, p.k_stride_h = _bthd_strides(k)
+            p.v_stride_b, p.v_stride_t, p.v_stride_h = _bthd_strides(v)
+            p.o_stride_b, p.o_stride_t, p.o_stride_h = _bthd_strides(O)
+            p.do_stride_b, p.do_stride_t, p.do_stride_h = _bthd_strides(do)
+            p.dq_stride_b, p.dq_stride_t, p.dq_stride_h = _bthd_strides(dQ)
+            p.dk_stride_b, p.dk_stride_t, p.dk_stride_h = _bthd_strides(dK)
+            p.dv_stride_b, p.dv_stride_t, p.dv_stride_h = _bthd_strides(dV)
+            p.mask_stride_b, p.mask_stride_h, p.mask_stride_q = ctx.mst
+            p.score_stride_b, p.score_stride_h, p.score_stride_q = ctx.sst
+            p.stream = _stream(dev)
+            _ext.check(lib.fa_bwd_preprocess(ctypes.byref(p)), "fa_bwd_preprocess", lib)
+            _ext.check(lib.fa_bwd(ctypes.byref(p)), "fa_bwd", lib)
+
+        if ctx.bhsd_input:
+            dQ, dK, dV = dQ.transpose(1, 2), dK.transpose(1, 2), dV.transpose(1, 2)
+        return dQ, dK, dV, None, None, None, None, None, None
+
+
+flash_attention_with_4d_mask = _flash_attention_with_4d_mask.apply
+
+__all__ = ["flash_attention_with_4d_mask"]

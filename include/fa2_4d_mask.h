@@ -1,0 +1,145 @@
+/*
+ * fa2_4d_mask.h -- C ABI of the MI355X (gfx950) FlashAttention-2 forward and
+ * backward with optional 4D bool keep-mask and 4D fp32 score.
+ *
+ * The library (libfa2_4d_mask.so) replaces the four TileLang JIT kernels of
+ * the reference (python/fa2.py) and is called by the host mirror of the
+ * reference's autograd Function (tilelang_fa2_4d_mask/fa2.py in this build).
+ *
+ * Conventions
+ *  - All pointers are device pointers; the caller owns every buffer (outputs
+ *    and workspaces).  Nothing here allocates device memory.
+ *  - Strides are in ELEMENTS.  The head dimension (D) of Q/K/V/O/dO/dQ/dK/dV
+ *    must be contiguous (stride 1); batch/time/head strides are free, so BHSD
+ *    views over BTHD storage and BHSD-contiguous tensors both work uncopied.
+ *  - Mask is bool (1 byte, 0 = drop, nonzero = keep) and Score is fp32, both
+ *    logically [B, Hq, Tq, Tk] with the key dimension contiguous; a batch or
+ *    head stride of 0 broadcasts (e.g. a [B, 1, Tq, Tk] mask).
+ *  - LSE is fp32 [B, Hq, Tq] contiguous, base-2 log-sum-exp of the scaled
+ *    logits; +inf marks a row with no kept key.  Internal fwd->bwd contract.
+ *  - Every entry point validates its arguments before touching the GPU and
+ *    returns 0 when the kernels were enqueued on `stream`, or a nonzero
+ *    FA_ERR_* code with nothing launched; fa_last_error() then describes it.
+ *    Launches are asynchronous, never synchronise, and keep no state between
+ *    calls, so they can be captured into a HIP graph.
+ */
+#ifndef FA2_4D_MASK_H
+#define FA2_4D_MASK_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FA_ABI_VERSION 1
+
+enum FaDtype { FA_DTYPE_BF16 = 0, FA_DTYPE_FP16 = 1 };
+
+enum FaStatus {
+  FA_OK = 0,
+  FA_ERR_NULL = 1,        /* a required pointer is NULL */
+  FA_ERR_SHAPE = 2,       /* non-positive size, Hq % Hk != 0, ... */
+  FA_ERR_HEAD_DIM = 3,    /* head_dim not supported by a kernel instance */
+  FA_ERR_DTYPE = 4,       /* dtype not FA_DTYPE_BF16 / FA_DTYPE_FP16 */
+  FA_ERR_STRIDE = 5,      /* head-dim stride != 1 or misaligned base */
+  FA_ERR_SCALE = 6,       /* scale is NaN or infinite */
+  FA_ERR_LAUNCH = 7,      /* the HIP runtime refused the launch */
+  FA_ERR_WORKSPACE = 8    /* a workspace required by the chosen plan is missing */
+};
+
+/* Forward problem: O = softmax(((Q K^T + Score) * scale) masked) V, plus LSE. */
+typedef struct FaFwdParams {
+  const void* q;                 /* [B, Tq, Hq, D] (by strides), dtype */
+  const void* k;                 /* [B, Tk, Hk, D] */
+  const void* v;                 /* [B, Tk, Hk, D] */
+  void* o;                       /* [B, Tq, Hq, D] output, dtype */
+  float* lse;                    /* [B, Hq, Tq] fp32 output, contiguous */
+  const uint8_t* mask;           /* optional, NULL if absent */
+  const float* score;            /* optional, NULL if absent */
+  int64_t q_stride_b, q_stride_t, q_stride_h;
+  int64_t k_stride_b, k_stride_t, k_stride_h;
+  int64_t v_stride_b, v_stride_t, v_stride_h;
+  int64_t o_stride_b, o_stride_t, o_stride_h;
+  int64_t mask_stride_b, mask_stride_h, mask_stride_q;
+  int64_t score_stride_b, score_stride_h, score_stride_q;
+  int32_t batch, seqlen_q, seqlen_k, heads_q, heads_k, head_dim;
+  float scale;                   /* softmax scale applied after adding Score */
+  int32_t is_causal;             /* keep j <= i (top-left aligned) */
+  int32_t dtype;                 /* enum FaDtype */
+  void* stream;                  /* hipStream_t; NULL = default stream */
+} FaFwdParams;
+
+/* Backward problem.  Reuses the forward's inputs plus O, LSE and dO. */
+typedef struct FaBwdParams {
+  const void* q; const void* k; const void* v;
+  const void* o;                 /* forward output */
+  const void* dout;              /* gradient of O, [B, Tq, Hq, D] by strides */
+  const float* lse;              /* [B, Hq, Tq] from fa_fwd */
+  float* delta;                  /* workspace [B, Hq, Tq] fp32 (written by fa_bwd_preprocess) */
+  int32_t* dead_flags;           /* workspace [B * Hk] int32, zeroed by the caller */
+  const uint8_t* mask; const float* score;
+  float* dq_accum;               /* workspace [B, Tq, Hq, D] fp32 contiguous (atomic dQ) */
+  float* dk_accum;               /* workspace [B, Tk, Hk, D] fp32 zeroed, only when plan.kv_split > 1 */
+  float* dv_accum;               /* idem */
+  void* dq; void* dk; void* dv;  /* outputs, dtype, strided like q/k/v */
+  int64_t q_stride_b, q_stride_t, q_stride_h;
+  int64_t k_stride_b, k_stride_t, k_stride_h;
+  int64_t v_stride_b, v_stride_t, v_stride_h;
+  int64_t o_stride_b, o_stride_t, o_stride_h;
+  int64_t do_stride_b, do_stride_t, do_stride_h;
+  int64_t dq_stride_b, dq_stride_t, dq_stride_h;
+  int64_t dk_stride_b, dk_stride_t, dk_stride_h;
+  int64_t dv_stride_b, dv_stride_t, dv_stride_h;
+  int64_t mask_stride_b, mask_stride_h, mask_stride_q;
+  int64_t score_stride_b, score_stride_h, score_stride_q;
+  int32_t batch, seqlen_q, seqlen_k, heads_q, heads_k, head_dim;
+  float scale;
+  int32_t is_causal;
+  int32_t atomic_dq;             /* 1: fp32 atomic dQ (default); 0: deterministic dQ kernel */
+  int32_t kv_split;              /* query-head-group split of the dK/dV kernel; 0 = let fa_bwd_plan choose */
+  int32_t dtype;
+  void* stream;
+} FaBwdParams;
+
+/* What fa_bwd will do for a problem, so the caller can size workspaces. */
+typedef struct FaBwdPlan {
+  int32_t kv_split;              /* >1: dK/dV accumulate in fp32 dk_accum/dv_accum (zeroed) */
+  int32_t needs_dq_accum;        /* 1 if dq_accum is used */
+  int64_t dq_accum_elems;        /* B*Tq*Hq*D when used, else 0 */
+  int64_t dkv_accum_elems;       /* B*Tk*Hk*D when kv_split > 1, else 0 */
+} FaBwdPlan;
+
+/* Forward.  Replaces the reference's `flash_attention_fwd_with_4d_mask`
+ * (python/fa2.py:22-139) as launched by `_flash_attention_with_4d_mask.forward`
+ * (python/fa2.py:474-478).  Writes O and LSE. */
+int fa_fwd(const FaFwdParams* p);
+
+/* Backward preprocess.  Replaces `bwd_preprocess` (python/fa2.py:142-179, launched at
+ * python/fa2.py:509-513): delta[b,h,i] = sum_d O*dO in fp32; additionally zeroes the
+ * dq_accum rows (when the plan uses it), zeroes delta and raises dead_flags[b*Hk+kvh]
+ * for rows whose LSE is +inf (no kept key). */
+int fa_bwd_preprocess(const FaBwdParams* p);
+
+/* Backward main pass.  Replaces `flash_attention_bwd_with_4d_mask_atomic`
+ * (python/fa2.py:181-302, launched at :530-534) when atomic_dq = 1 and
+ * `flash_attention_bwd_with_4d_mask_reduce` (python/fa2.py:305-426, launched at
+ * :543-547, host reduction :548-549) when atomic_dq = 0, including the fp32 -> dtype
+ * casts of python/fa2.py:535-536 and the engine's dQ cast.  Writes dq, dk, dv in dtype.
+ * Must follow fa_bwd_preprocess on the same stream. */
+int fa_bwd(const FaBwdParams* p);
+
+/* Fills *plan for the problem in *p (no launch, no GPU access). */
+int fa_bwd_plan(const FaBwdParams* p, FaBwdPlan* plan);
+
+/* Human-readable description of the last nonzero status on the calling thread. */
+const char* fa_last_error(void);
+
+/* FA_ABI_VERSION of the library. */
+int fa_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FA2_4D_MASK_H */
