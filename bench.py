@@ -1,0 +1,226 @@
+#!/usr/bin/env python3
+"""Headline benchmark: FA2 fwd and fwd+bwd TFLOPS at B1 T8192 Hq32 Hk8 D128 bf16.
+
+One step = one fwd+bwd pass (non-causal) of ``tilelang_flash_attention`` over
+the BASELINE headline config: Q/K/V/dO ~ N(0,1) bf16, BHSD views
+over BTHD storage, scale D^-0.5 -- exactly what the reference's
+throughput_check.py times (fwd+bwd = zero grads, forward, backward(dO),
+benchmark/throughput_check.py:206-211).  The same run also times fwd and
+fwd+bwd with is_causal=True and fwd non-causal; those go into ``breakdown``.
+
+FLOP convention (benchmark/throughput_check.py:85-92): fwd 4*B*Hq*Tq*Tk*D,
+fwd+bwd 14*..., x0.5 when causal.  Peak: MI355X dense bf16 MFMA 2.5 PFLOP/s.
+
+``roofline`` is for the dominant kernel of the step, the backward kernel
+launched by ``fa_bwd`` (dK/dV + atomic dQ, 10*B*Hq*Tq*Tk*D algorithmic FLOPs
+per launch), timed with HIP events on the launch stream inside the timed
+region.  ``cpu_baseline`` times this repository's eager fp32 oracle on the host
+cores on a bounded sample.
+
+Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (str(ROOT), str(ROOT / "fa2-with-4d-mask_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "fwd and fwd+bwd TFLOPS (and % bf16 MFMA peak) at B1 T8192 Hq32 Hk8 D128"
+PEAK_TFLOPS = 2500.0          # MI355X dense bf16 MFMA
+PUBLISHED_FWD_BWD = 169.43    # reference README.md:136 (TileLang fwd+bwd, non-causal, RTX PRO 5000)
+B, T, HQ, HK, D = 1, 8192, 32, 8, 128
+
+
+def conv_flops(mode: str, causal: bool) -> float:
+    return (4.0 if mode == "fwd" else 14.0) * (0.5 if causal else 1.0) * B * HQ * T * T * D
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def make_inputs(torch, dev):
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    q = torch.randn((B, T, HQ, D), generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
+    k = torch.randn((B, T, HK, D), generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
+    v = torch.randn((B, T, HK, D), generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
+    do = torch.randn((B, T, HQ, D), generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
+    return q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), do.transpose(1, 2)
+
+
+def time_steps(torch, fn, steps: int, warmup: int, record_events):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    with record_events() as ev:
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            fn()
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+    per_kernel = {name: statistics.mean(v) for name, v in ev.elapsed_ms().items()}
+    return (t1 - t0) * 1e3 / steps, per_kernel
+
+
+def cpu_baseline(seconds: float) -> dict:
+    """Eager fp32 oracle (oracle/eager.py) on the host cores, fwd+bwd, on a bounded
+    sample of the headline workload: one kv-head group (Hq=4, Hk=1) at full T."""
+    import torch
+
+    from oracle import eager as E
+
+    hq, hk = 4, 1
+    g = torch.Generator(device="cpu")
+    g.manual_seed(0)
+    q = torch.randn((B, T, hq, D), generator=g).to(torch.bfloat16).transpose(1, 2)
+    k = torch.randn((B, T, hk, D), generator=g).to(torch.bfloat16).transpose(1, 2)
+    v = torch.randn((B, T, hk, D), generator=g).to(torch.bfloat16).transpose(1, 2)
+    do = torch.randn((B, T, hq, D), generator=g).to(torch.bfloat16).transpose(1, 2)
+    flops = 14.0 * B * hq * T * T * D
+    runs, t0 = 0, time.perf_counter()
+    while True:
+        E.eager_fwd_bwd(q, k, v, None, None, do, scale=D ** -0.5, is_causal=False, ref_block=128)
+        runs += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    tflops = flops * runs / el * 1e-12
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except AttributeError:
+        cores = os.cpu_count()
+    return {
+        "value": round(tflops, 4),
+        "unit": "TFLOPS",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"oracle eager fp32 fwd+bwd (ref_block=128) at B1 T8192 Hq4 Hk1 D128 non-causal "
+                   f"(1/8 of the headline heads), {runs} run(s) in {el:.1f} s; host affinity {cores} cores"),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}): this build has no multi-GPU "
+              "path; the op shards over (batch x kv-head) with no communication.", file=sys.stderr)
+        return 2
+
+    import torch
+
+    import tilelang_fa2_4d_mask as api
+    from tilelang_fa2_4d_mask.fa2 import record_kernel_events
+
+    if not torch.cuda.is_available():
+        log("no GPU visible")
+        return 1
+    dev = torch.device("cuda:0")
+    q0, k0, v0, do = make_inputs(torch, dev)
+    q = q0.detach().requires_grad_(True)
+    k = k0.detach().requires_grad_(True)
+    v = v0.detach().requires_grad_(True)
+
+    def fwd(causal):
+        def f():
+            with torch.no_grad():
+                api.tilelang_flash_attention(q0, k0, v0, is_causal=causal)
+        return f
+
+    def fwd_bwd(causal):
+        def f():
+            q.grad = k.grad = v.grad = None
+            out = api.tilelang_flash_attention(q, k, v, is_causal=causal)
+            out.backward(do)
+        return f
+
+    log(f"device: {torch.cuda.get_device_name(dev)}; workload B{B} T{T} Hq{HQ} Hk{HK} D{D} bf16")
+    results = {}
+    for name, fn, mode, causal in (
+        ("fwd_bwd", fwd_bwd(False), "fwd_bwd", False),
+        ("fwd", fwd(False), "fwd", False),
+        ("fwd_causal", fwd(True), "fwd", True),
+        ("fwd_bwd_causal", fwd_bwd(True), "fwd_bwd", True),
+    ):
+        ms, kern = time_steps(torch, fn, args.steps, args.warmup, record_kernel_events)
+        tf = conv_flops(mode, causal) / (ms * 1e-3) * 1e-12
+        results[name] = {"ms": round(ms, 4), "tflops": round(tf, 2), "frac_of_peak": round(tf / PEAK_TFLOPS, 4),
+                         "kernel_ms": {k2: round(v2, 4) for k2, v2 in kern.items()}}
+        log(f"{name:15s} {ms:8.3f} ms  {tf:8.1f} TFLOPS  ({100 * tf / PEAK_TFLOPS:5.1f}% of peak)  kernels {kern}")
+
+    main_res = results["fwd_bwd"]
+    bwd_ms = main_res["kernel_ms"]["fa_bwd"]
+    bwd_flops = 10.0 * B * HQ * T * T * D
+    achieved = bwd_flops / (bwd_ms * 1e-3) * 1e-12
+    fwd_kernel_ms = results["fwd"]["kernel_ms"]["fa_fwd"]
+    fwd_achieved = 4.0 * B * HQ * T * T * D / (fwd_kernel_ms * 1e-3) * 1e-12
+    for name, r in results.items():
+        causal = name.endswith("causal")
+        if "fa_fwd" in r["kernel_ms"]:
+            r["fwd_kernel_tflops"] = round(conv_flops("fwd", causal) / (r["kernel_ms"]["fa_fwd"] * 1e-3) * 1e-12, 2)
+        if "fa_bwd" in r["kernel_ms"]:
+            r["bwd_kernel_tflops"] = round(10.0 * (0.5 if causal else 1.0) * B * HQ * T * T * D
+                                           / (r["kernel_ms"]["fa_bwd"] * 1e-3) * 1e-12, 2)
+
+    line = {
+        "metric": METRIC,
+        "value": main_res["tflops"],
+        "unit": "TFLOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": main_res["ms"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": round(main_res["tflops"] / PUBLISHED_FWD_BWD, 3),
+        "dtype": "bf16",
+        "data": "synthetic: Q/K/V/dO ~ N(0,1) bf16, seeded, BHSD views over BTHD storage",
+        "config": {
+            "workload": "H (BASELINE configs[1]): fwd+bwd non-causal per step",
+            "batch": B, "seq_len_q": T, "seq_len_k": T, "heads_q": HQ, "heads_k": HK, "head_dim": D,
+            "layout": "bhsd", "scale": "D^-0.5", "parallelism": "single GPU",
+        },
+        "breakdown": results,
+        "roofline": {
+            "kernel": "dkdv_kernel<bf16,128> via fa_bwd (dK/dV + fp32-atomic dQ)",
+            "bound": "mfma",
+            "achieved": round(achieved, 2),
+            "peak": PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_TFLOPS, 4),
+            "traffic": None,
+            "avg_launch_ms": round(bwd_ms, 4),
+            "flops_per_launch": bwd_flops,
+            "fwd_kernel": {"achieved": round(fwd_achieved, 2), "frac": round(fwd_achieved / PEAK_TFLOPS, 4),
+                           "avg_launch_ms": round(fwd_kernel_ms, 4)},
+        },
+    }
+    if not args.no_cpu_baseline:
+        log("timing the CPU baseline ...")
+        line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+        log(f"cpu baseline: {line['cpu_baseline']}")
+    else:
+        line["cpu_baseline"] = None
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -173,7 +173,10 @@ int fa_bwd_plan(const FaBwdParams* p, FaBwdPlan* plan) {
   plan->kv_split = split;
   plan->needs_dq_accum = p->atomic_dq ? 1 : 0;
   plan->dq_accum_elems = p->atomic_dq ? (int64_t)p->batch * p->seqlen_q * p->heads_q * p->head_dim : 0;
-  plan->dkv_accum_elems = split > 1 ? (int64_t)p->batch * p->seqlen_k * p->heads_k * p->head_dim : 0;
+  // atomic dQ: one zeroed fp32 accumulator for dK and one for dV; deterministic
+  // path: one slab per split, fully overwritten (no zeroing needed).
+  plan->dkv_accum_elems =
+      split > 1 ? (int64_t)(p->atomic_dq ? 1 : split) * p->batch * p->seqlen_k * p->heads_k * p->head_dim : 0;
   return FA_OK;
 }
 
@@ -226,19 +229,32 @@ int fa_bwd(const FaBwdParams* p) {
   const bool causal = p->is_causal != 0;
 
   if ((st = launch_status(fa::launch_bwd_dkdv(a, p->head_dim, p->dtype, causal, s), "dkdv"))) return st;
-  if (p->atomic_dq) {
-    fa::CvtArgs c{p->dq_accum, p->dq, p->dq_stride_b, p->dq_stride_t, p->dq_stride_h,
-                  p->batch, p->seqlen_q, p->heads_q, p->head_dim};
-    if ((st = launch_status(fa::launch_convert(c, p->dtype, s), "dq convert"))) return st;
-  } else {
+  if (!p->atomic_dq) {
     if ((st = launch_status(fa::launch_bwd_dq(a, p->head_dim, p->dtype, causal, s), "dq"))) return st;
   }
+  return FA_OK;
+}
+
+int fa_bwd_finalize(const FaBwdParams* p) {
+  if (!p) return fail(FA_ERR_NULL, "params is NULL");
+  const int split = choose_split(p);
+  int st = check_bwd(p, split);
+  if (st) return st;
+  const hipStream_t s = (hipStream_t)p->stream;
+  if (p->atomic_dq) {
+    fa::CvtArgs c{p->dq_accum, p->dq, p->dq_stride_b, p->dq_stride_t, p->dq_stride_h,
+                  p->batch, p->seqlen_q, p->heads_q, p->head_dim, 1, 0};
+    if ((st = launch_status(fa::launch_convert(c, p->dtype, s), "dq convert"))) return st;
+  }
   if (split > 1) {
+    // atomic path: one zeroed accumulator; deterministic path: one slab per split.
+    const int nslab = p->atomic_dq ? 1 : split;
+    const int64_t slab = (int64_t)p->batch * p->seqlen_k * p->heads_k * p->head_dim;
     fa::CvtArgs ck{p->dk_accum, p->dk, p->dk_stride_b, p->dk_stride_t, p->dk_stride_h,
-                   p->batch, p->seqlen_k, p->heads_k, p->head_dim};
+                   p->batch, p->seqlen_k, p->heads_k, p->head_dim, nslab, slab};
     if ((st = launch_status(fa::launch_convert(ck, p->dtype, s), "dk convert"))) return st;
     fa::CvtArgs cv{p->dv_accum, p->dv, p->dv_stride_b, p->dv_stride_t, p->dv_stride_h,
-                   p->batch, p->seqlen_k, p->heads_k, p->head_dim};
+                   p->batch, p->seqlen_k, p->heads_k, p->head_dim, nslab, slab};
     if ((st = launch_status(fa::launch_convert(cv, p->dtype, s), "dv convert"))) return st;
   }
   return FA_OK;

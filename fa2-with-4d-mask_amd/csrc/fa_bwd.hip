@@ -359,15 +359,24 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdArgs a) {
         }
       }
   } else {
+    // Head-group split: fp32 partials.  With atomic dQ they are added into one
+    // zeroed accumulator; on the deterministic path every split owns a slab
+    // [split][B, Tk, Hk, D] that the finalize step sums in a fixed order.
+    const int64_t slab = DQ ? 0 : (int64_t)sp * a.B * Tk * a.Hk * D;
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int kr = kw0 + 8 * (i >> 2) + 4 * hf + (i & 3);
         if (kr < Tk) {
-          const int64_t o = (((int64_t)b * Tk + kr) * a.Hk + kvh) * D + nb * 32 + l32;
-          unsafeAtomicAdd(a.dk_accum + o, dk[nb][i]);
-          unsafeAtomicAdd(a.dv_accum + o, dead ? nanv : dv[nb][i]);
+          const int64_t o = slab + (((int64_t)b * Tk + kr) * a.Hk + kvh) * D + nb * 32 + l32;
+          if constexpr (DQ) {
+            unsafeAtomicAdd(a.dk_accum + o, dk[nb][i]);
+            unsafeAtomicAdd(a.dv_accum + o, dead ? nanv : dv[nb][i]);
+          } else {
+            a.dk_accum[o] = dk[nb][i];
+            a.dv_accum[o] = dead ? nanv : dv[nb][i];
+          }
         }
       }
   }
@@ -573,7 +582,11 @@ __global__ __launch_bounds__(256) void convert_kernel(const CvtArgs a) {
     const int t = (int)(rest % a.T);
     const int bb = (int)(rest / a.T);
     const float* s = a.src + i * 8;
-    const f32x4 x0 = *(const f32x4*)s, x1 = *(const f32x4*)(s + 4);
+    f32x4 x0 = *(const f32x4*)s, x1 = *(const f32x4*)(s + 4);
+    for (int k = 1; k < a.nsplit; ++k) {  // fixed summation order: deterministic
+      x0 += *(const f32x4*)(s + k * a.split_stride);
+      x1 += *(const f32x4*)(s + k * a.split_stride + 4);
+    }
     const auto v = pack8<T>(x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]);
     T* d = (T*)a.dst + bb * a.sb + (int64_t)t * a.st + hh * a.sh + c * 8;
     gstore16(d, as_u32x4<T>(v));

@@ -49,10 +49,12 @@ struct BwdArgs {
 };
 
 struct CvtArgs {
-  const float* src;      // [B, T, H, D] fp32 contiguous
+  const float* src;      // nsplit x [B, T, H, D] fp32 contiguous slabs, summed
   void* dst;             // dtype, strided
   int64_t sb, st, sh;
   int B, T, H, D;
+  int nsplit;            // number of slabs (1 = plain conversion)
+  int64_t split_stride;  // elements between slabs
 };
 
 hipError_t launch_fwd(const FwdArgs& a, int D, int dtype, bool causal, hipStream_t s);

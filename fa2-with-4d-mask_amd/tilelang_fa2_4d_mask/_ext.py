@@ -73,7 +73,8 @@ class FaBwdPlan(ctypes.Structure):
     ]
 
 
-EXPORTED = ("fa_fwd", "fa_bwd_preprocess", "fa_bwd", "fa_bwd_plan", "fa_last_error", "fa_abi_version")
+EXPORTED = ("fa_fwd", "fa_bwd_preprocess", "fa_bwd", "fa_bwd_finalize", "fa_bwd_plan", "fa_last_error",
+            "fa_abi_version")
 
 _lib = None
 _lock = threading.Lock()
@@ -100,6 +101,8 @@ def load_library(path: os.PathLike | None = None) -> ctypes.CDLL:
         lib.fa_bwd_preprocess.restype = ctypes.c_int
         lib.fa_bwd.argtypes = [ctypes.POINTER(FaBwdParams)]
         lib.fa_bwd.restype = ctypes.c_int
+        lib.fa_bwd_finalize.argtypes = [ctypes.POINTER(FaBwdParams)]
+        lib.fa_bwd_finalize.restype = ctypes.c_int
         lib.fa_bwd_plan.argtypes = [ctypes.POINTER(FaBwdParams), ctypes.POINTER(FaBwdPlan)]
         lib.fa_bwd_plan.restype = ctypes.c_int
         lib.fa_last_error.argtypes = []

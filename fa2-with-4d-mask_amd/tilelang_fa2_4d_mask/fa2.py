@@ -20,6 +20,7 @@ What differs on purpose:
 
 from __future__ import annotations
 
+import contextlib
 import ctypes
 from typing import Optional
 
@@ -71,6 +72,51 @@ def _kernel_side(x: Optional[torch.Tensor], dtype: Optional[torch.dtype], B: int
 
 def _stream(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
+
+
+class KernelEventLog:
+    """HIP events recorded around every library call, on the stream the
+    kernels are launched on (torch's current stream)."""
+
+    def __init__(self):
+        self.records = []  # (entry point, start event, end event)
+
+    def elapsed_ms(self) -> dict:
+        torch.cuda.synchronize()
+        out: dict = {}
+        for name, s, e in self.records:
+            out.setdefault(name, []).append(s.elapsed_time(e))
+        return out
+
+
+_event_log: Optional[KernelEventLog] = None
+
+
+@contextlib.contextmanager
+def record_kernel_events():
+    """Context manager yielding a :class:`KernelEventLog` of the library calls
+    made inside it (forward and backward)."""
+    global _event_log
+    prev, log = _event_log, KernelEventLog()
+    _event_log = log
+    try:
+        yield log
+    finally:
+        _event_log = prev
+
+
+def _call(lib, entry: str, params) -> None:
+    fn = getattr(lib, entry)
+    log = _event_log
+    if log is None:
+        _ext.check(fn(ctypes.byref(params)), entry, lib)
+        return
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    status = fn(ctypes.byref(params))
+    end.record()
+    log.records.append((entry, start, end))
+    _ext.check(status, entry, lib)
 
 
 class _flash_attention_with_4d_mask(torch.autograd.Function):
@@ -131,8 +177,7 @@ class _flash_attention_with_4d_mask(torch.autograd.Function):
                 p.is_causal = 1 if is_causal else 0
                 p.dtype = code
                 p.stream = _stream(q.device)
-                lib = _ext.load_library()
-                _ext.check(lib.fa_fwd(ctypes.byref(p)), "fa_fwd", lib)
+                _call(_ext.load_library(), "fa_fwd", p)
 
         ctx.save_for_backward(q, k, v, O, LSE, mask, score)
         ctx.scale = scale
@@ -176,8 +221,11 @@ class _flash_attention_with_4d_mask(torch.autograd.Function):
             dq_acc = torch.empty((B, Tq, Hq, D), dtype=torch.float32, device=dev) if plan.needs_dq_accum else None
             dk_acc = dv_acc = None
             if plan.kv_split > 1:
-                dk_acc = torch.zeros((B, Tk, Hk, D), dtype=torch.float32, device=dev)
-                dv_acc = torch.zeros((B, Tk, Hk, D), dtype=torch.float32, device=dev)
+                # atomic path: zeroed accumulators; deterministic path: one fully
+                # overwritten fp32 slab per head-group split.
+                alloc = torch.zeros if ctx.use_atomic_backward else torch.empty
+                dk_acc = alloc((plan.dkv_accum_elems,), dtype=torch.float32, device=dev)
+                dv_acc = alloc((plan.dkv_accum_elems,), dtype=torch.float32, device=dev)
 
             p.q, p.k, p.v, p.o, p.dout = q.data_ptr(), k.data_ptr(), v.data_ptr(), O.data_ptr(), do.data_ptr()
             p.lse, p.delta, p.dead_flags = LSE.data_ptr(), delta.data_ptr(), dead.data_ptr()
@@ -195,8 +243,9 @@ class _flash_attention_with_4d_mask(torch.autograd.Function):
             p.mask_stride_b, p.mask_stride_h, p.mask_stride_q = ctx.mst
             p.score_stride_b, p.score_stride_h, p.score_stride_q = ctx.sst
             p.stream = _stream(dev)
-            _ext.check(lib.fa_bwd_preprocess(ctypes.byref(p)), "fa_bwd_preprocess", lib)
-            _ext.check(lib.fa_bwd(ctypes.byref(p)), "fa_bwd", lib)
+            _call(lib, "fa_bwd_preprocess", p)
+            _call(lib, "fa_bwd", p)
+            _call(lib, "fa_bwd_finalize", p)
 
         if ctx.bhsd_input:
             dQ, dK, dV = dQ.transpose(1, 2), dK.transpose(1, 2), dV.transpose(1, 2)
@@ -205,4 +254,4 @@ class _flash_attention_with_4d_mask(torch.autograd.Function):
 
 flash_attention_with_4d_mask = _flash_attention_with_4d_mask.apply
 
-__all__ = ["flash_attention_with_4d_mask"]
+__all__ = ["flash_attention_with_4d_mask", "record_kernel_events", "KernelEventLog"]

@@ -124,10 +124,18 @@ int fa_bwd_preprocess(const FaBwdParams* p);
 /* Backward main pass.  Replaces `flash_attention_bwd_with_4d_mask_atomic`
  * (python/fa2.py:181-302, launched at :530-534) when atomic_dq = 1 and
  * `flash_attention_bwd_with_4d_mask_reduce` (python/fa2.py:305-426, launched at
- * :543-547, host reduction :548-549) when atomic_dq = 0, including the fp32 -> dtype
- * casts of python/fa2.py:535-536 and the engine's dQ cast.  Writes dq, dk, dv in dtype.
+ * :543-547) when atomic_dq = 0.  atomic_dq = 1: one kernel; dK/dV are written in
+ * dtype (kv_split = 1) or added to dk_accum/dv_accum, dQ is added to dq_accum.
+ * atomic_dq = 0: the dK/dV kernel and a deterministic dQ kernel writing dq in dtype.
  * Must follow fa_bwd_preprocess on the same stream. */
 int fa_bwd(const FaBwdParams* p);
+
+/* Backward finalisation: fp32 accumulators -> dtype outputs (dq from dq_accum when
+ * atomic_dq = 1; dk, dv from dk_accum/dv_accum when kv_split > 1); launches nothing
+ * when neither applies.  Replaces the casts of python/fa2.py:535-536, the group sum
+ * of python/fa2.py:548-549 and autograd's cast of the fp32 dQ the reference
+ * returns (python/fa2.py:527, 556).  Must follow fa_bwd on the same stream. */
+int fa_bwd_finalize(const FaBwdParams* p);
 
 /* Fills *plan for the problem in *p (no launch, no GPU access). */
 int fa_bwd_plan(const FaBwdParams* p, FaBwdPlan* plan);

@@ -74,27 +74,30 @@ def eager_ref(
     scale: float,
     is_causal: bool,
     ref_block: int = 0,
+    compute_dtype: torch.dtype = torch.float32,
 ) -> torch.Tensor:
     """Eager attention in BHSD layout; differentiable w.r.t. q, k, v.
 
     q: [B, Hq, Tq, D]; k, v: [B, Hk, Tk, D]; mask: bool [B|1, Hq|1, Tq, Tk];
     score: float [B|1, Hq|1, Tq, Tk].  Returns [B, Hq, Tq, D] in q.dtype.
-    Follows benchmark/precision_check.py:133-180 step by step.
+    Follows benchmark/precision_check.py:133-180 step by step.  ``compute_dtype``
+    is fp32 as in the reference; tests use float64 to pin the maths.
     """
     B, Hq, Tq, D = q.shape
     _, Hk, Tk, _ = k.shape
     if Hq % Hk != 0:
         raise ValueError(f"Hq={Hq} must be divisible by Hk={Hk}")
     groups = Hq // Hk
-    qf = q.float()
-    kf = _expand_kv(k, groups).float()
-    vf = _expand_kv(v, groups).float()
+    cd = compute_dtype
+    qf = q.to(cd)
+    kf = _expand_kv(k, groups).to(cd)
+    vf = _expand_kv(v, groups).to(cd)
     kt = kf.transpose(-1, -2).contiguous()
 
     def rows(q0: int, q1: int) -> torch.Tensor:
         logits = torch.matmul(qf[:, :, q0:q1, :], kt)
         if score is not None:
-            logits = logits + score[:, :, q0:q1, :].float()
+            logits = logits + score[:, :, q0:q1, :].to(cd)
         logits = logits * scale
         keep = _keep_for_rows(q0, q1, Tk, mask, is_causal, logits.device)
         if keep is not None:
@@ -119,6 +122,7 @@ def eager_fwd_bwd(
     scale: float,
     is_causal: bool,
     ref_block: int = 0,
+    compute_dtype: torch.dtype = torch.float32,
 ):
     """Forward + autograd backward of :func:`eager_ref` on fresh leaf copies.
 
@@ -128,7 +132,8 @@ def eager_fwd_bwd(
     qr = q.detach().clone().requires_grad_(True)
     kr = k.detach().clone().requires_grad_(True)
     vr = v.detach().clone().requires_grad_(True)
-    out = eager_ref(qr, kr, vr, mask, score, scale=scale, is_causal=is_causal, ref_block=ref_block)
+    out = eager_ref(qr, kr, vr, mask, score, scale=scale, is_causal=is_causal, ref_block=ref_block,
+                    compute_dtype=compute_dtype)
     out.backward(grad_out)
     return out.detach(), qr.grad, kr.grad, vr.grad
 
@@ -145,6 +150,7 @@ def eager_grads_chunked(
     is_causal: bool,
     block: int = 128,
     compute_dkdv: bool = True,
+    compute_dtype: torch.dtype = torch.float32,
 ):
     """Closed-form forward + gradients of :func:`eager_ref`, chunked over query rows.
 
@@ -162,22 +168,23 @@ def eager_grads_chunked(
     _, Hk, Tk, _ = k.shape
     groups = Hq // Hk
     dev = q.device
-    qf = q.float()
-    kf = _expand_kv(k, groups).float()
-    vf = _expand_kv(v, groups).float()
+    cd = compute_dtype
+    qf = q.to(cd)
+    kf = _expand_kv(k, groups).to(cd)
+    vf = _expand_kv(v, groups).to(cd)
     kt = kf.transpose(-1, -2).contiguous()
     vt = vf.transpose(-1, -2).contiguous()
-    gf = grad_out.float()
-    out = torch.empty((B, Hq, Tq, D), dtype=torch.float32, device=dev)
-    dq = torch.empty((B, Hq, Tq, D), dtype=torch.float32, device=dev)
-    dk = torch.zeros((B, Hq, Tk, D), dtype=torch.float32, device=dev) if compute_dkdv else None
-    dv = torch.zeros((B, Hq, Tk, D), dtype=torch.float32, device=dev) if compute_dkdv else None
+    gf = grad_out.to(cd)
+    out = torch.empty((B, Hq, Tq, D), dtype=cd, device=dev)
+    dq = torch.empty((B, Hq, Tq, D), dtype=cd, device=dev)
+    dk = torch.zeros((B, Hq, Tk, D), dtype=cd, device=dev) if compute_dkdv else None
+    dv = torch.zeros((B, Hq, Tk, D), dtype=cd, device=dev) if compute_dkdv else None
     for q0 in range(0, Tq, block):
         q1 = min(q0 + block, Tq)
         qc = qf[:, :, q0:q1, :]
         logits = torch.matmul(qc, kt)
         if score is not None:
-            logits = logits + score[:, :, q0:q1, :].float()
+            logits = logits + score[:, :, q0:q1, :].to(cd)
         logits = logits * scale
         keep = _keep_for_rows(q0, q1, Tk, mask, is_causal, dev)
         if keep is not None:

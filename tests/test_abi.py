@@ -1,0 +1,201 @@
+"""C ABI of libfa2_4d_mask.so, without a GPU.
+
+* the library loads and exports every function include/fa2_4d_mask.h declares;
+* the ctypes mirror of the parameter structs has exactly the C layout (a small
+  C program compiled with gcc against the header prints sizeof/offsetof);
+* every validation path returns its FA_ERR_* code before any HIP call;
+* fa_bwd_plan's head-group split and workspace sizes.
+"""
+
+import ctypes
+import math
+import re
+import shutil
+import subprocess
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "fa2_4d_mask.h"
+
+
+def _ext():
+    from tilelang_fa2_4d_mask import _ext
+
+    return _ext
+
+
+@pytest.fixture(scope="module")
+def lib():
+    ext = _ext()
+    if not ext.LIB_PATH.exists():
+        import importlib.util
+
+        spec = importlib.util.spec_from_file_location("fa_build_ext", ROOT / "fa2-with-4d-mask_amd" / "build_ext.py")
+        mod = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(mod)
+        mod.build(jobs=4)
+    return ext.load_library()
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(fa_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_exports_every_declared_function(lib):
+    names = declared_functions()
+    assert {"fa_fwd", "fa_bwd_preprocess", "fa_bwd", "fa_bwd_finalize", "fa_bwd_plan", "fa_last_error",
+            "fa_abi_version"} <= set(names)
+    for n in names:
+        assert hasattr(lib, n), n
+    assert set(_ext().EXPORTED) == set(names)
+    assert lib.fa_abi_version() == _ext().ABI_VERSION
+
+
+def test_struct_layout_matches_header(tmp_path):
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("gcc not available")
+    ext = _ext()
+    lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void) {"]
+    for cname, cls in (("FaFwdParams", ext.FaFwdParams), ("FaBwdParams", ext.FaBwdParams),
+                       ("FaBwdPlan", ext.FaBwdPlan)):
+        lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
+        for fname, _ in cls._fields_:
+            lines.append(f'printf("{cname} {fname} %zu\\n", offsetof({cname}, {fname}));')
+    lines += ["return 0;", "}"]
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run([gcc, "-std=c99", str(src), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split("\n")
+    got = {}
+    for line in out:
+        if line.strip():
+            parts = line.split()
+            got[(parts[0], parts[1])] = int(parts[2])
+    for cname, cls in (("FaFwdParams", ext.FaFwdParams), ("FaBwdParams", ext.FaBwdParams),
+                       ("FaBwdPlan", ext.FaBwdPlan)):
+        assert got[(cname, "size")] == ctypes.sizeof(cls), cname
+        for fname, _ in cls._fields_:
+            assert got[(cname, fname)] == getattr(cls, fname).offset, (cname, fname)
+
+
+FAKE = 0x100000  # 16-byte aligned, never dereferenced: validation fails first
+
+
+def fwd_params(**over):
+    ext = _ext()
+    p = ext.FaFwdParams()
+    p.q = p.k = p.v = p.o = p.lse = FAKE
+    p.q_stride_b, p.q_stride_t, p.q_stride_h = 8192 * 32 * 128, 32 * 128, 128
+    p.k_stride_b, p.k_stride_t, p.k_stride_h = 8192 * 8 * 128, 8 * 128, 128
+    p.v_stride_b, p.v_stride_t, p.v_stride_h = 8192 * 8 * 128, 8 * 128, 128
+    p.o_stride_b, p.o_stride_t, p.o_stride_h = 8192 * 32 * 128, 32 * 128, 128
+    p.batch, p.seqlen_q, p.seqlen_k, p.heads_q, p.heads_k, p.head_dim = 1, 8192, 8192, 32, 8, 128
+    p.scale = 128 ** -0.5
+    p.dtype = 0
+    for k, v in over.items():
+        setattr(p, k, v)
+    return p
+
+
+def bwd_params(**over):
+    ext = _ext()
+    p = ext.FaBwdParams()
+    for n in ("q", "k", "v", "o", "dout", "lse", "delta", "dead_flags", "dq_accum", "dq", "dk", "dv"):
+        setattr(p, n, FAKE)
+    for pre, h in (("q", 32), ("o", 32), ("do", 32), ("dq", 32), ("k", 8), ("v", 8), ("dk", 8), ("dv", 8)):
+        setattr(p, f"{pre}_stride_b", 8192 * h * 128)
+        setattr(p, f"{pre}_stride_t", h * 128)
+        setattr(p, f"{pre}_stride_h", 128)
+    p.batch, p.seqlen_q, p.seqlen_k, p.heads_q, p.heads_k, p.head_dim = 1, 8192, 8192, 32, 8, 128
+    p.scale = 128 ** -0.5
+    p.atomic_dq = 1
+    for k, v in over.items():
+        setattr(p, k, v)
+    return p
+
+
+FWD_ERRORS = [
+    (dict(head_dim=96), 3, "head_dim 96"),
+    (dict(head_dim=256), 3, "head_dim 256"),
+    (dict(dtype=5), 4, "dtype"),
+    (dict(heads_k=5), 2, "divisible"),
+    (dict(batch=0), 2, "sizes must be"),
+    (dict(seqlen_k=0), 2, "sizes must be"),
+    (dict(scale=float("nan")), 6, "finite"),
+    (dict(scale=float("inf")), 6, "finite"),
+    (dict(q=FAKE + 8), 5, "not 16-byte aligned"),
+    (dict(k_stride_t=8 * 128 + 4), 5, "multiples of 8"),
+    (dict(v=None), 1, "v is NULL"),
+    (dict(lse=None), 1, "lse is NULL"),
+    (dict(mask=FAKE, mask_stride_q=-1), 5, "non-negative"),
+    (dict(score=FAKE, score_stride_h=-4), 5, "non-negative"),
+]
+
+
+@pytest.mark.parametrize("over,code,msg", FWD_ERRORS, ids=[e[2] for e in FWD_ERRORS])
+def test_fwd_validation(lib, over, code, msg):
+    assert lib.fa_fwd(ctypes.byref(fwd_params(**over))) == code
+    assert msg in lib.fa_last_error().decode()
+
+
+def test_null_params(lib):
+    assert lib.fa_fwd(None) == 1
+    assert lib.fa_bwd(None) == 1
+    assert lib.fa_bwd_preprocess(None) == 1
+    assert lib.fa_bwd_finalize(None) == 1
+    assert lib.fa_bwd_plan(None, None) == 1
+
+
+BWD_ERRORS = [
+    (dict(dq_accum=None), 8, "needs dq_accum"),
+    (dict(kv_split=3), 2, "must divide"),
+    (dict(kv_split=2), 8, "needs dk_accum"),
+    (dict(dout=None), 1, "dout is NULL"),
+    (dict(delta=None), 1, "delta is NULL"),
+    (dict(dead_flags=None), 1, "dead_flags is NULL"),
+    (dict(dk_stride_h=100), 5, "multiples of 8"),
+    (dict(head_dim=32), 3, "head_dim 32"),
+]
+
+
+@pytest.mark.parametrize("over,code,msg", BWD_ERRORS, ids=[e[2] for e in BWD_ERRORS])
+@pytest.mark.parametrize("entry", ["fa_bwd_preprocess", "fa_bwd", "fa_bwd_finalize"])
+def test_bwd_validation(lib, entry, over, code, msg):
+    assert getattr(lib, entry)(ctypes.byref(bwd_params(**over))) == code
+    assert msg in lib.fa_last_error().decode()
+
+
+def _plan(lib, **over):
+    ext = _ext()
+    plan = ext.FaBwdPlan()
+    assert lib.fa_bwd_plan(ctypes.byref(bwd_params(**over)), ctypes.byref(plan)) == 0
+    return plan
+
+
+def test_plan_headline_needs_no_split(lib):
+    plan = _plan(lib)
+    assert plan.kv_split == 1 and plan.needs_dq_accum == 1
+    assert plan.dq_accum_elems == 8192 * 32 * 128 and plan.dkv_accum_elems == 0
+    plan = _plan(lib, atomic_dq=0)
+    assert plan.needs_dq_accum == 0 and plan.dq_accum_elems == 0
+
+
+def test_plan_mqa_splits_the_group(lib):
+    # BASELINE config M: B1 Tq2048 Tk16384 Hq32 Hk1 D64 -> 128 key tiles; split 4 -> 512 workgroups
+    m = dict(seqlen_q=2048, seqlen_k=16384, heads_q=32, heads_k=1, head_dim=64)
+    plan = _plan(lib, **m)
+    assert plan.kv_split == 4 and plan.dkv_accum_elems == 16384 * 64
+    plan = _plan(lib, atomic_dq=0, **m)
+    assert plan.kv_split == 4 and plan.dkv_accum_elems == 4 * 16384 * 64
+    plan = _plan(lib, kv_split=8, **m)
+    assert plan.kv_split == 8
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    with pytest.raises(RuntimeError, match="not built"):
+        _ext().load_library(tmp_path / "nope.so")

@@ -1,0 +1,296 @@
+"""Pins the oracle (oracle/eager.py) before it is trusted as the parity checker.
+
+The reference holds no golden vectors or known-answer tests for this path
+(its checks are runtime comparisons, benchmark/precision_check.py:209-349), so
+the oracle is pinned by:
+  * a float64 scalar-loop brute force (oracle/bruteforce.py) on tiny inputs,
+    outputs and all three gradients, dead rows included;
+  * torch's own scaled_dot_product_attention (CPU, enable_gqa) for the
+    forward and its autograd gradients;
+  * finite differences (torch.autograd.gradcheck) in float64;
+  * invariants fixed by the maths (causal == tril mask, all-true mask == no
+    mask, zero score == no score, GQA == explicit repeat, rows of P sum to one);
+  * planted mistakes: plausible wrong variants of the maths are shown to FAIL
+    the brute-force comparison, so the comparison has teeth.
+"""
+
+import math
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import bruteforce as BF
+from oracle import eager as E
+from oracle import inputs as I
+
+torch.set_num_threads(min(8, torch.get_num_threads()))
+
+
+def _tiny(seed, B=2, Hq=4, Hk=2, Tq=5, Tk=6, D=4, mask=False, score=False, dead=False):
+    g = I.make_generator(seed)
+    q = torch.randn((B, Hq, Tq, D), generator=g, dtype=torch.float64)
+    k = torch.randn((B, Hk, Tk, D), generator=g, dtype=torch.float64)
+    v = torch.randn((B, Hk, Tk, D), generator=g, dtype=torch.float64)
+    do = torch.randn((B, Hq, Tq, D), generator=g, dtype=torch.float64)
+    m = None
+    if mask:
+        m = torch.rand((B, Hq, Tq, Tk), generator=g) < 0.6
+        m[..., 0] = True
+        if dead:
+            m[0, 1, 2, :] = False
+    s = torch.randn((B, Hq, Tq, Tk), generator=g, dtype=torch.float64) * 0.5 if score else None
+    return q, k, v, m, s, do
+
+
+def _bf(q, k, v, m, s, do, scale, causal):
+    o, dq, dk, dv = BF.attention_bruteforce(
+        q.tolist(), k.tolist(), v.tolist(), None if m is None else m.tolist(),
+        None if s is None else s.tolist(), do.tolist(), scale, causal)
+    return [torch.tensor(x, dtype=torch.float64) for x in (o, dq, dk, dv)]
+
+
+def _close_with_nans(a, b, tol=1e-9):
+    assert torch.equal(torch.isnan(a), torch.isnan(b)), "NaN positions differ"
+    fin = ~torch.isnan(b)
+    assert torch.allclose(a[fin], b[fin], atol=tol, rtol=tol), (a[fin] - b[fin]).abs().max()
+
+
+CASES = [
+    dict(causal=False, mask=False, score=False),
+    dict(causal=True, mask=False, score=False),
+    dict(causal=False, mask=True, score=False),
+    dict(causal=False, mask=False, score=True),
+    dict(causal=True, mask=True, score=True),
+    dict(causal=False, mask=True, score=True, dead=True),
+    dict(causal=True, mask=True, score=False, dead=True),
+]
+
+
+@pytest.mark.parametrize("c", CASES, ids=[str(i) for i in range(len(CASES))])
+def test_eager_matches_bruteforce(c):
+    q, k, v, m, s, do = _tiny(1, mask=c["mask"], score=c["score"], dead=c.get("dead", False))
+    scale = 0.7
+    o, dq, dk, dv = E.eager_fwd_bwd(q, k, v, m, s, do, scale=scale, is_causal=c["causal"],
+                                    compute_dtype=torch.float64)
+    bo, bdq, bdk, bdv = _bf(q, k, v, m, s, do, scale, c["causal"])
+    _close_with_nans(o, bo)
+    _close_with_nans(dq, bdq)
+    _close_with_nans(dk, bdk)
+    _close_with_nans(dv, bdv)
+
+
+@pytest.mark.parametrize("c", CASES, ids=[str(i) for i in range(len(CASES))])
+def test_chunked_closed_form_matches_autograd(c):
+    q, k, v, m, s, do = _tiny(2, Tq=9, Tk=7, mask=c["mask"], score=c["score"], dead=c.get("dead", False))
+    a = E.eager_fwd_bwd(q, k, v, m, s, do, scale=0.5, is_causal=c["causal"], compute_dtype=torch.float64)
+    b = E.eager_grads_chunked(q, k, v, m, s, do, scale=0.5, is_causal=c["causal"], block=4,
+                              compute_dtype=torch.float64)
+    for x, y in zip(a, b):
+        _close_with_nans(y, x)
+
+
+def test_ref_block_chunking_is_exact():
+    q, k, v, m, s, do = _tiny(3, Tq=11, Tk=13, mask=True, score=True)
+    full = E.eager_ref(q, k, v, m, s, scale=0.3, is_causal=True, compute_dtype=torch.float64)
+    chunked = E.eager_ref(q, k, v, m, s, scale=0.3, is_causal=True, ref_block=4, compute_dtype=torch.float64)
+    assert torch.allclose(full, chunked, atol=1e-12, rtol=0)
+
+
+def test_rows_subset_matches_full():
+    q, k, v, m, s, do = _tiny(4, Tq=10, Tk=8, mask=True, score=True)
+    o, dq, _, _ = E.eager_fwd_bwd(q, k, v, m, s, do, scale=0.4, is_causal=True, compute_dtype=torch.float64)
+    rows = torch.tensor([0, 3, 9])
+    o2, dq2 = E.eager_rows(q.float(), k.float(), v.float(), m, s, do.float(), rows, scale=0.4, is_causal=True)
+    assert torch.allclose(o2.double(), o[:, :, rows], atol=1e-5)
+    assert torch.allclose(dq2.double(), dq[:, :, rows], atol=1e-5)
+
+
+def test_eager_matches_torch_sdpa():
+    q, k, v, m, s, do = _tiny(5, Tq=7, Tk=9, D=8, mask=True, score=True)
+    scale = 0.35
+    bias = (s * scale).masked_fill(~m, float("-inf"))
+    qs, ks, vs = (t.clone().requires_grad_(True) for t in (q, k, v))
+    ref = F.scaled_dot_product_attention(qs, ks, vs, attn_mask=bias, scale=scale, enable_gqa=True)
+    ref.backward(do)
+    o, dq, dk, dv = E.eager_fwd_bwd(q, k, v, m, s, do, scale=scale, is_causal=False, compute_dtype=torch.float64)
+    assert torch.allclose(o, ref, atol=1e-10)
+    assert torch.allclose(dq, qs.grad, atol=1e-10)
+    assert torch.allclose(dk, ks.grad, atol=1e-10)
+    assert torch.allclose(dv, vs.grad, atol=1e-10)
+    # causal through SDPA's own flag (top-left aligned for Tq == Tk)
+    q, k, v, _, _, _ = _tiny(6, Tq=8, Tk=8, D=8)
+    ref = F.scaled_dot_product_attention(q, k, v, is_causal=True, scale=scale, enable_gqa=True)
+    o = E.eager_ref(q, k, v, None, None, scale=scale, is_causal=True, compute_dtype=torch.float64)
+    assert torch.allclose(o, ref, atol=1e-10)
+
+
+def test_gradcheck_finite_differences():
+    q, k, v, m, s, _ = _tiny(7, B=1, Hq=2, Hk=1, Tq=4, Tk=5, D=3, mask=True, score=True)
+    qs, ks, vs = (t.clone().requires_grad_(True) for t in (q, k, v))
+
+    def f(a, b, c):
+        return E.eager_ref(a, b, c, m, s, scale=0.6, is_causal=True, compute_dtype=torch.float64)
+
+    assert torch.autograd.gradcheck(f, (qs, ks, vs), eps=1e-6, atol=1e-6)
+
+
+def test_invariants():
+    q, k, v, _, _, _ = _tiny(8, Tq=6, Tk=6, D=5)
+    sc = 0.5
+    base = E.eager_ref(q, k, v, None, None, scale=sc, is_causal=False, compute_dtype=torch.float64)
+    ones_mask = torch.ones((2, 4, 6, 6), dtype=torch.bool)
+    assert torch.equal(base, E.eager_ref(q, k, v, ones_mask, None, scale=sc, is_causal=False,
+                                         compute_dtype=torch.float64))
+    zero_score = torch.zeros((2, 4, 6, 6), dtype=torch.float64)
+    assert torch.allclose(base, E.eager_ref(q, k, v, None, zero_score, scale=sc, is_causal=False,
+                                            compute_dtype=torch.float64), atol=1e-12)
+    tril = torch.ones((6, 6), dtype=torch.bool).tril().expand(2, 4, 6, 6)
+    assert torch.allclose(E.eager_ref(q, k, v, None, None, scale=sc, is_causal=True, compute_dtype=torch.float64),
+                          E.eager_ref(q, k, v, tril, None, scale=sc, is_causal=False, compute_dtype=torch.float64),
+                          atol=1e-12)
+    # GQA equals an explicit repeat of K/V heads (head h uses kv-head h // G)
+    kr, vr = k.repeat_interleave(2, dim=1), v.repeat_interleave(2, dim=1)
+    assert torch.allclose(base, E.eager_ref(q, kr, vr, None, None, scale=sc, is_causal=False,
+                                            compute_dtype=torch.float64), atol=1e-12)
+    # rows of P sum to one: V = 1 gives O = 1; O is a convex combination of V
+    ones_v = torch.ones_like(v)
+    assert torch.allclose(E.eager_ref(q, k, ones_v, None, None, scale=sc, is_causal=True,
+                                      compute_dtype=torch.float64), torch.ones_like(base), atol=1e-12)
+    vexp = v.repeat_interleave(2, dim=1)
+    assert (base <= vexp.max(dim=2, keepdim=True).values + 1e-12).all()
+    assert (base >= vexp.min(dim=2, keepdim=True).values - 1e-12).all()
+    # causal row 0 attends to key 0 only
+    oc = E.eager_ref(q, k, v, None, None, scale=sc, is_causal=True, compute_dtype=torch.float64)
+    assert torch.allclose(oc[:, :, 0], vexp[:, :, 0], atol=1e-12)
+
+
+def test_dead_row_policy_3x3():
+    """3x3 example: row 1 keeps nothing.  O row NaN, dQ row exactly 0, dV NaN for
+    every key of the head, dK finite."""
+    q = torch.tensor([[[[1.0, 0.0], [0.5, 0.5], [0.0, 1.0]]]], dtype=torch.float64)
+    k = torch.tensor([[[[1.0, 1.0], [0.0, 1.0], [1.0, 0.0]]]], dtype=torch.float64)
+    v = torch.tensor([[[[1.0, 2.0], [3.0, 4.0], [5.0, 6.0]]]], dtype=torch.float64)
+    m = torch.tensor([[[[True, True, False], [False, False, False], [True, True, True]]]])
+    do = torch.ones((1, 1, 3, 2), dtype=torch.float64)
+    o, dq, dk, dv = E.eager_fwd_bwd(q, k, v, m, None, do, scale=1.0, is_causal=False, compute_dtype=torch.float64)
+    assert torch.isnan(o[0, 0, 1]).all() and torch.isfinite(o[0, 0, [0, 2]]).all()
+    assert (dq[0, 0, 1] == 0).all()
+    assert torch.isnan(dv).all()
+    assert torch.isfinite(dk).all()
+    bo, bdq, bdk, bdv = _bf(q, k, v, m, None, do, 1.0, False)
+    _close_with_nans(o, bo)
+    _close_with_nans(dq, bdq)
+    _close_with_nans(dk, bdk)
+
+
+def test_lse2_reference():
+    q, k, v, m, s, _ = _tiny(9, mask=True, score=True, dead=True)
+    lse = E.lse2_reference(q, k, m, s, scale=0.7, is_causal=True)
+    qe = q
+    ke = k.repeat_interleave(2, dim=1)
+    for b, h, i in [(0, 0, 0), (1, 3, 4), (0, 2, 3)]:
+        vals = [((qe[b, h, i] * ke[b, h, j]).sum() + s[b, h, i, j]).item() * 0.7
+                for j in range(6) if j <= i and m[b, h, i, j]]
+        want = math.log2(sum(math.exp(x) for x in vals))
+        assert abs(lse[b, h, i].item() - want) < 1e-5
+    assert lse[0, 1, 2].item() == float("inf")  # dead row
+
+
+# ---------------------------------------------------------------------------
+# planted mistakes: each wrong variant must fail the brute-force comparison
+# ---------------------------------------------------------------------------
+
+def _variant(q, k, v, m, s, scale, causal, mistake):
+    G = q.shape[1] // k.shape[1]
+    if mistake == "gqa_tile":          # head h -> kv-head h % Hk instead of h // G
+        ke, ve = k.repeat(1, G, 1, 1), v.repeat(1, G, 1, 1)
+    else:
+        ke, ve = k.repeat_interleave(G, dim=1), v.repeat_interleave(G, dim=1)
+    logits = q @ ke.transpose(-1, -2)
+    if mistake == "score_after_scale":
+        logits = logits * scale + s
+    else:
+        logits = (logits + s) * scale
+    Tq, Tk = q.shape[2], k.shape[2]
+    i = torch.arange(Tq)[:, None]
+    j = torch.arange(Tk)[None, :]
+    keep = (i > j) if mistake == "strict_causal" else (i >= j)
+    if mistake == "bottom_right_causal":
+        keep = (i + (Tk - Tq)) >= j
+    keep = keep & m if causal else m
+    logits = logits.masked_fill(~keep, float("-inf"))
+    if mistake == "softmax_wrong_axis":
+        p = torch.softmax(logits.masked_fill(~keep, -1e30), dim=-2)
+    else:
+        p = torch.softmax(logits, dim=-1)
+    vv = ve.flip(-2) if mistake == "reversed_keys_of_v" else ve
+    return p @ vv
+
+
+@pytest.mark.parametrize("mistake", ["gqa_tile", "score_after_scale", "strict_causal", "bottom_right_causal",
+                                     "softmax_wrong_axis", "reversed_keys_of_v", "none"])
+def test_planted_mistakes_are_caught(mistake):
+    q, k, v, m, s, do = _tiny(10, Tq=5, Tk=7, mask=True, score=True)
+    bo = _bf(q, k, v, m, s, do, 0.7, True)[0]
+    o = _variant(q, k, v, m, s, 0.7, True, mistake)
+    fin = torch.isfinite(bo)
+    same = torch.allclose(o[fin], bo[fin], atol=1e-9)
+    assert same == (mistake == "none"), mistake
+
+
+# ---------------------------------------------------------------------------
+# statistics, pass rules, FLOP convention, generators
+# ---------------------------------------------------------------------------
+
+def test_diff_stats_and_rules():
+    a = torch.tensor([1.0, 2.0, 3.0])
+    b = torch.tensor([1.0, 2.5, 2.0])
+    st = E.diff_stats(a, b)
+    assert st["max_abs"] == pytest.approx(1.0) and st["mean_abs"] == pytest.approx(0.5)
+    assert st["max_rel"] == pytest.approx(0.5) and st["mean_rel"] == pytest.approx((0 + 0.2 + 0.5) / 3)
+    assert E.case_passed({"max_abs": 0.06, "mean_rel": 0.04}) and not E.case_passed({"max_abs": 0.06, "mean_rel": 0.06})
+    assert E.north_star_passed({"max_abs": 0.02, "mean_abs": 1e-4})
+    assert not E.north_star_passed({"max_abs": 0.021, "mean_abs": 1e-5})
+    nan_st = E.finite_diff_stats(torch.tensor([float("nan"), 1.0]), torch.tensor([float("nan"), 1.5]))
+    assert nan_st["nan_match"] and nan_st["max_abs"] == pytest.approx(0.5)
+    assert not E.finite_diff_stats(torch.tensor([0.0, 1.0]), torch.tensor([float("nan"), 1.0]))["nan_match"]
+
+
+def test_flop_convention():
+    assert E.conv_flops(1, 8192, 8192, 32, 128, False, "fwd") == 2.0 ** 40
+    assert E.conv_flops(1, 8192, 8192, 32, 128, True, "fwd") == 2.0 ** 39
+    assert E.conv_flops(1, 8192, 8192, 32, 128, False, "fwd_bwd") == 14 * 2.0 ** 38
+    assert E.estimate_tflops(1, 8192, 8192, 32, 128, False, 1.0, "fwd") == pytest.approx(2.0 ** 40 * 1e-9)
+
+
+def test_generators():
+    pm = I.packed_docs_mask(2, 600, I.make_generator(0), lo=40, hi=120)
+    assert pm.shape == (2, 1, 600, 600) and pm.dtype == torch.bool
+    assert torch.equal(pm, pm & torch.ones(600, 600, dtype=torch.bool).tril())
+    assert pm.diagonal(dim1=-2, dim2=-1).all()
+    # block-diagonal: keep(i,j) for j <= i iff same segment -> segments are contiguous
+    for b in range(2):
+        row_start = [int(pm[b, 0, i].nonzero()[0]) for i in range(600)]
+        seg_len = torch.tensor(row_start).unique(return_counts=True)[1]
+        assert (seg_len[:-1] >= 40).all() and (seg_len <= 120).all()
+    sm = I.sparse_diag_mask(1, 2, 50, 60, 0.1, I.make_generator(1))
+    assert sm[:, :, torch.arange(50), torch.arange(50)].all()
+    g = I.make_generator(2)
+    a = I.alibi_noise_score(1, 4, 6, 6, g, noise_std=0.0)
+    for h in range(4):
+        slope = 2.0 ** (-8.0 * (h + 1) / 4)
+        assert a[0, h, 5, 1].item() == pytest.approx(-slope * 4)
+    bm = I.bernoulli_mask(1, 2, 10, 7, 0.3, I.make_generator(3))
+    assert bm[:, :, torch.arange(10), torch.clamp(torch.arange(10), max=6)].all()
+
+
+def test_make_case_layouts_are_bthd_backed():
+    cfg = I.AttnConfig("x", 2, 16, 24, 4, 2, 64)
+    c = I.make_case(cfg, seed=0)
+    q = c["q"]
+    assert q.shape == (2, 4, 16, 64) and q.transpose(1, 2).is_contiguous()
+    cfg2 = cfg.scaled(layout="bshd")
+    c2 = I.make_case(cfg2, seed=0)
+    assert c2["q"].shape == (2, 16, 4, 64) and c2["q"].is_contiguous()
+    assert torch.equal(c2["q"].transpose(1, 2), c["q"])
