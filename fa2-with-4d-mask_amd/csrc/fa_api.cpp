@@ -10,7 +10,7 @@
 #include <cstdio>
 #include <cstring>
 
-#include "../../include/fa2_4d_mask.h"
+#include "fa2_4d_mask.h"
 #include "fa_kernels.h"
 
 namespace fa {
@@ -242,19 +242,22 @@ int fa_bwd_finalize(const FaBwdParams* p) {
   if (st) return st;
   const hipStream_t s = (hipStream_t)p->stream;
   if (p->atomic_dq) {
+    // dq_accum is head-major [B, Hq, Tq, D]
+    const int64_t D = p->head_dim, Tq = p->seqlen_q, Hq = p->heads_q;
     fa::CvtArgs c{p->dq_accum, p->dq, p->dq_stride_b, p->dq_stride_t, p->dq_stride_h,
-                  p->batch, p->seqlen_q, p->heads_q, p->head_dim, 1, 0};
+                  p->batch, p->seqlen_q, p->heads_q, p->head_dim, 1, 0, Hq * Tq * D, D, Tq * D};
     if ((st = launch_status(fa::launch_convert(c, p->dtype, s), "dq convert"))) return st;
   }
   if (split > 1) {
     // atomic path: one zeroed accumulator; deterministic path: one slab per split.
     const int nslab = p->atomic_dq ? 1 : split;
     const int64_t slab = (int64_t)p->batch * p->seqlen_k * p->heads_k * p->head_dim;
+    const int64_t D = p->head_dim, Tk = p->seqlen_k, Hk = p->heads_k;
     fa::CvtArgs ck{p->dk_accum, p->dk, p->dk_stride_b, p->dk_stride_t, p->dk_stride_h,
-                   p->batch, p->seqlen_k, p->heads_k, p->head_dim, nslab, slab};
+                   p->batch, p->seqlen_k, p->heads_k, p->head_dim, nslab, slab, Tk * Hk * D, Hk * D, D};
     if ((st = launch_status(fa::launch_convert(ck, p->dtype, s), "dk convert"))) return st;
     fa::CvtArgs cv{p->dv_accum, p->dv, p->dv_stride_b, p->dv_stride_t, p->dv_stride_h,
-                   p->batch, p->seqlen_k, p->heads_k, p->head_dim, nslab, slab};
+                   p->batch, p->seqlen_k, p->heads_k, p->head_dim, nslab, slab, Tk * Hk * D, Hk * D, D};
     if ((st = launch_status(fa::launch_convert(cv, p->dtype, s), "dv convert"))) return st;
   }
   return FA_OK;

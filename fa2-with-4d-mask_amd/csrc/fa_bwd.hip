@@ -65,7 +65,7 @@ __global__ __launch_bounds__(256) void preprocess_kernel(const PreArgs a) {
   acc += __shfl_xor(acc, 2);
   if (q < a.Tq) {
     if (a.dq_accum) {
-      float* z = a.dq_accum + (((int64_t)b * a.Tq + q) * a.Hq + h) * D + part * (D / 4);
+      float* z = a.dq_accum + (((int64_t)b * a.Hq + h) * a.Tq + q) * D + part * (D / 4);
 #pragma unroll
       for (int u = 0; u < D / 16; ++u) *(f32x4*)(z + 4 * u) = f32x4{0.f, 0.f, 0.f, 0.f};
     }
@@ -127,6 +127,8 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdArgs a) {
   const T* __restrict__ vp = (const T*)a.v + b * a.vsb + kvh * a.vsh;
 
   // K, V fragments: B operands of S = Q K^T and dP = dO V^T.
+  // Keys past Tk are zero: their dK/dV rows are never stored and, with K = 0,
+  // their dS contributes nothing to dQ.
   V8 kf[DS], vf[DS];
   if (key < Tk) {
 #pragma unroll
@@ -172,32 +174,45 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdArgs a) {
   const int nq = max(0, nqt - qt_first);
   const int iters = gsz * nq;
 
+  // Query tiles are visited in a per-block rotated order so that the key
+  // blocks of one kv-head add their dQ partials to different rows at any time
+  // (the atomics would otherwise all target the same cache lines).
+  const int qrot = nq > 0 ? (int)(((int64_t)kt * nq) / a.nkt) % nq : 0;
+  auto tile_of = [&](int it, int& g, int& qt) {
+    const int gi = it / nq;
+    int r = it - gi * nq + qrot;
+    if (r >= nq) r -= nq;
+    g = g0 + gi;
+    qt = qt_first + r;
+  };
+
   u32x4 qreg[UQ], dreg[UQ];
-  float lreg = 0.f;
+  float lreg = 0.f, dlreg = 0.f;
+  bool lrow_ok = true;
+  const float* __restrict__ lse_p = a.lse;
+  const float* __restrict__ delta_p = a.delta;
   auto load_q = [&](int it) {
-    const int g = g0 + it / nq, qt = qt_first + it % nq;
+    int g, qt;
+    tile_of(it, g, qt);
     const int h = kvh * a.G + g, qs = qt * BM;
     const T* qp = (const T*)a.q + b * a.qsb + h * a.qsh;
     const T* dp = (const T*)a.dout + b * a.dsb + h * a.dsh;
+    // Rows past Tq are loaded from row Tq-1 (unconditional loads, no zero
+    // fill): their LSE is set to +inf, so P = dS = 0 and they add nothing.
 #pragma unroll
     for (int u = 0; u < UQ; ++u) {
       const int idx = tid + u * 256;
       const int r = idx / CH, c = idx % CH;
-      const int row = qs + r;
-      if (row < Tq) {
-        qreg[u] = gload16(qp + (int64_t)row * a.qst + c * 8);
-        dreg[u] = gload16(dp + (int64_t)row * a.dst + c * 8);
-      } else {
-        qreg[u] = u32x4{0, 0, 0, 0};
-        dreg[u] = u32x4{0, 0, 0, 0};
-      }
+      const int row = min(qs + r, Tq - 1);
+      qreg[u] = gload16(qp + (int64_t)row * a.qst + c * 8);
+      dreg[u] = gload16(dp + (int64_t)row * a.dst + c * 8);
     }
-    if (tid < BM) {
-      const int row = qs + tid;
-      lreg = row < Tq ? a.lse[((int64_t)b * a.Hq + h) * Tq + row] : kPosInf;
-    } else if (tid < 2 * BM) {
-      const int row = qs + tid - BM;
-      lreg = row < Tq ? a.delta[((int64_t)b * a.Hq + h) * Tq + row] : 0.f;
+    {
+      const int row = qs + (tid & (BM - 1));
+      const int64_t ri = ((int64_t)b * a.Hq + h) * Tq + min(row, Tq - 1);
+      lreg = lse_p[ri];
+      dlreg = delta_p[ri];
+      lrow_ok = row < Tq;  // applied at store time, when the loads have landed
     }
   };
   auto store_q = [&](int buf) {
@@ -208,8 +223,10 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdArgs a) {
       lds_write16(sQ + buf * QT + r * QS + c * 8, qreg[u]);
       lds_write16(sdO + buf * QT + r * QS + c * 8, dreg[u]);
     }
-    if (tid < BM) sL[buf * BM + tid] = lreg;
-    else if (tid < 2 * BM) sDl[buf * BM + tid - BM] = lreg;
+    if (tid < BM) {
+      sL[buf * BM + tid] = lrow_ok ? lreg : kPosInf;
+      sDl[buf * BM + tid] = lrow_ok ? dlreg : 0.f;
+    }
   };
 
   f32x16 dk[NB], dv[NB];
@@ -224,34 +241,32 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdArgs a) {
 
   for (int it = 0; it < iters; ++it) {
     const int buf = it & 1;
-    const int g = g0 + it / nq, qt = qt_first + it % nq;
+    int g, qt;
+    tile_of(it, g, qt);
     const int h = kvh * a.G + g, qs = qt * BM;
     if (it + 1 < iters) load_q(it + 1);
     const T* Qs = sQ + buf * QT;
     const T* dOs = sdO + buf * QT;
     const bool active = !CAUSAL || (qs + BM - 1 >= kw0);
     if (active) {
-      // ---- S = Q K^T, dP = dO V^T ----------------------------------------------
-      f32x16 sacc[2], pacc[2];
+      const bool edge = MASK || (CAUSAL && kw0 + 31 > qs);
+      const int kc = min(key, Tk - 1);
+      // The 64-row tile is processed as two 32-row halves to keep the S / dP
+      // accumulators at 32 registers.
 #pragma unroll
       for (int qb = 0; qb < 2; ++qb) {
-        sacc[qb] = f32x16{};
-        pacc[qb] = f32x16{};
+        // ---- S = Q K^T, dP = dO V^T for rows 32 qb .. 32 qb + 31 -----------------
+        f32x16 sacc = f32x16{}, pacc = f32x16{};
 #pragma unroll
         for (int ds = 0; ds < DS; ++ds) {
           const u32x4 xq = lds_read16(Qs + (qb * 32 + l32) * QS + ds * 16 + hf * 8);
-          sacc[qb] = mfma32(as_vec8<T>(xq), kf[ds], sacc[qb]);
           const u32x4 xd = lds_read16(dOs + (qb * 32 + l32) * QS + ds * 16 + hf * 8);
-          pacc[qb] = mfma32(as_vec8<T>(xd), vf[ds], pacc[qb]);
+          sacc = mfma32(as_vec8<T>(xq), kf[ds], sacc);
+          pacc = mfma32(as_vec8<T>(xd), vf[ds], pacc);
         }
-      }
-      // lane's entry (qb, i) is query qs + 32 qb + 8 (i/4) + 4 hf + i%4, key `key`
+        // lane's entry i is query qs + 32 qb + 8 (i/4) + 4 hf + i%4, key `key`
 
-      // ---- P and dS ------------------------------------------------------------
-      const bool edge = MASK || (CAUSAL && kw0 + 31 > qs);
-      const int kc = min(key, Tk - 1);
-#pragma unroll
-      for (int qb = 0; qb < 2; ++qb)
+        // ---- P and dS ----------------------------------------------------------
 #pragma unroll
         for (int gi = 0; gi < 4; ++gi) {
           const int qr0 = qb * 32 + gi * 8 + hf * 4;
@@ -262,50 +277,47 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdArgs a) {
             const int i = gi * 4 + t;
             const int q = qs + qr0 + t;
             const int qc = min(q, Tq - 1);
-            float s = sacc[qb][i];
+            float sv = sacc[i];
             if constexpr (SCORE) {
               const float sc = a.score[b * a.ssb + h * a.ssh + (int64_t)qc * a.ssq + kc];
-              s += key < Tk ? sc : 0.f;
+              sv += key < Tk ? sc : 0.f;
             }
-            if (a.zero_scale) s = 0.f;
-            float p = exp2_fast(fmaf(s, c2, -L4[t]));
+            if (a.zero_scale) sv = 0.f;
+            float p = exp2_fast(fmaf(sv, c2, -L4[t]));
             if (edge) {
               bool keep = true;
               if constexpr (CAUSAL) keep = key <= q;
               if constexpr (MASK) keep = keep && key < Tk && a.mask[b * a.msb + h * a.msh + (int64_t)qc * a.msq + kc] != 0;
               p = keep ? p : 0.f;
             }
-            sacc[qb][i] = p;
-            pacc[qb][i] = p * (pacc[qb][i] - D4[t]) * scale;
+            sacc[i] = p;
+            pacc[i] = p * (pacc[i] - D4[t]) * scale;
           }
         }
 
-      // ---- dV += P^T dO, dK += dS^T Q --------------------------------------------
-#pragma unroll
-      for (int qb = 0; qb < 2; ++qb)
+        // ---- dV += P^T dO, dK += dS^T Q ------------------------------------------
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
-          const V8 pa = pack8<T>(sacc[qb][8 * c + 0], sacc[qb][8 * c + 1], sacc[qb][8 * c + 2], sacc[qb][8 * c + 3],
-                                 sacc[qb][8 * c + 4], sacc[qb][8 * c + 5], sacc[qb][8 * c + 6], sacc[qb][8 * c + 7]);
-          const V8 dsa = pack8<T>(pacc[qb][8 * c + 0], pacc[qb][8 * c + 1], pacc[qb][8 * c + 2], pacc[qb][8 * c + 3],
-                                  pacc[qb][8 * c + 4], pacc[qb][8 * c + 5], pacc[qb][8 * c + 6], pacc[qb][8 * c + 7]);
+          const V8 pa = pack8<T>(sacc[8 * c + 0], sacc[8 * c + 1], sacc[8 * c + 2], sacc[8 * c + 3],
+                                 sacc[8 * c + 4], sacc[8 * c + 5], sacc[8 * c + 6], sacc[8 * c + 7]);
+          const V8 dsa = pack8<T>(pacc[8 * c + 0], pacc[8 * c + 1], pacc[8 * c + 2], pacc[8 * c + 3],
+                                  pacc[8 * c + 4], pacc[8 * c + 5], pacc[8 * c + 6], pacc[8 * c + 7]);
           const int row = qb * 32 + 16 * c + 4 * hf + tr_row;
 #pragma unroll
           for (int nb = 0; nb < NB; ++nb) {
             const int col = nb * 32 + tr_col;
             const V8 bo = cat_tr<T>(lds_read_tr(dOs + row * QS + col), lds_read_tr(dOs + (row + 8) * QS + col));
-            dv[nb] = mfma32(pa, bo, dv[nb]);
             const V8 bq = cat_tr<T>(lds_read_tr(Qs + row * QS + col), lds_read_tr(Qs + (row + 8) * QS + col));
+            dv[nb] = mfma32(pa, bo, dv[nb]);
             dk[nb] = mfma32(dsa, bq, dk[nb]);
           }
         }
-      if constexpr (DQ) {
-#pragma unroll
-        for (int qb = 0; qb < 2; ++qb)
+        if constexpr (DQ) {
 #pragma unroll
           for (int gi = 0; gi < 4; ++gi)
             lds_write8(sdS + (wave * 32 + l32) * SS + qb * 32 + gi * 8 + hf * 4,
-                       pack4<T>(pacc[qb][gi * 4 + 0], pacc[qb][gi * 4 + 1], pacc[qb][gi * 4 + 2], pacc[qb][gi * 4 + 3]));
+                       pack4<T>(pacc[gi * 4 + 0], pacc[gi * 4 + 1], pacc[gi * 4 + 2], pacc[gi * 4 + 3]));
+        }
       }
     } else if constexpr (DQ) {
 #pragma unroll
@@ -318,27 +330,44 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdArgs a) {
     if constexpr (DQ) {
       __syncthreads();  // every wave's dS is in LDS
       // ---- dQ = dS K over the workgroup's 128 keys, atomically added -----------
+      f32x16 acc[NPAIR];
 #pragma unroll
       for (int pp = 0; pp < NPAIR; ++pp) {
         const int qb = (wave * NPAIR + pp) & 1;
-        f32x16 acc = f32x16{};
+        acc[pp] = f32x16{};
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
           const int row = s * 16 + 8 * hf + tr_row;
           const int col = qb * 32 + tr_col;
           const V8 av = cat_tr<T>(lds_read_tr(sdS + row * SS + col), lds_read_tr(sdS + (row + 4) * SS + col));
-          acc = mfma32(av, ktf[s], acc);
-        }
-        float* dqp = a.dq_accum + (int64_t)h * D + db * 32 + l32;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int q = qs + qb * 32 + 8 * (i >> 2) + 4 * hf + (i & 3);
-          if (q < Tq) unsafeAtomicAdd(dqp + ((int64_t)b * Tq + q) * a.Hq * D, acc[i]);
+          acc[pp] = mfma32(av, ktf[s], acc[pp]);
         }
       }
+      // Stage the next tile before issuing the atomics: its wait on the
+      // prefetch loads then does not also wait for this tile's atomics.
+      if (it + 1 < iters) store_q(buf ^ 1);
+      // dq_accum is head-major [B, Hq, Tq, D]: consecutive query rows are D floats
+      // apart, so one wave's 16 row-segments spread over many L2 channels (a
+      // [B, Tq, Hq, D] layout puts them Hq*D*4 bytes apart, all aliasing).
+      const int64_t rs = D;
+#pragma unroll
+      for (int pp = 0; pp < NPAIR; ++pp) {
+        const int qb = (wave * NPAIR + pp) & 1;
+        float* dqp = a.dq_accum + (((int64_t)b * a.Hq + h) * Tq + qs + qb * 32 + 4 * hf) * D + db * 32 + l32;
+        if (qs + BM <= Tq) {
+#pragma unroll
+          for (int i = 0; i < 16; ++i) unsafeAtomicAdd(dqp + (8 * (i >> 2) + (i & 3)) * rs, acc[pp][i]);
+        } else {
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int q = qs + qb * 32 + 8 * (i >> 2) + 4 * hf + (i & 3);
+            if (q < Tq) unsafeAtomicAdd(dqp + (8 * (i >> 2) + (i & 3)) * rs, acc[pp][i]);
+          }
+        }
+      }
+    } else {
+      if (it + 1 < iters) store_q(buf ^ 1);
     }
-
-    if (it + 1 < iters) store_q(buf ^ 1);
     __syncthreads();
   }
 
@@ -451,19 +480,16 @@ __global__ __launch_bounds__(256, 1) void dq_kernel(const BwdArgs a) {
   const int ntiles = (kv_end + BN - 1) / BN;
 
   u32x4 kreg[U], vreg[U];
+  // Keys past Tk are loaded from key Tk-1 (unconditional loads): their P is
+  // masked to 0, so they contribute nothing.
   auto load_tile = [&](int k0) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int idx = tid + u * 256;
       const int r = idx / CH, c = idx % CH;
-      const int kk = k0 + r;
-      if (kk < Tk) {
-        kreg[u] = gload16(kp + (int64_t)kk * a.kst + c * 8);
-        vreg[u] = gload16(vp + (int64_t)kk * a.vst + c * 8);
-      } else {
-        kreg[u] = u32x4{0, 0, 0, 0};
-        vreg[u] = u32x4{0, 0, 0, 0};
-      }
+      const int kk = min(k0 + r, Tk - 1);
+      kreg[u] = gload16(kp + (int64_t)kk * a.kst + c * 8);
+      vreg[u] = gload16(vp + (int64_t)kk * a.vst + c * 8);
     }
   };
   auto store_tile = [&](int buf) {
@@ -581,7 +607,7 @@ __global__ __launch_bounds__(256) void convert_kernel(const CvtArgs a) {
     const int hh = (int)(rest % a.H); rest /= a.H;
     const int t = (int)(rest % a.T);
     const int bb = (int)(rest / a.T);
-    const float* s = a.src + i * 8;
+    const float* s = a.src + bb * a.src_sb + (int64_t)t * a.src_st + (int64_t)hh * a.src_sh + c * 8;
     f32x4 x0 = *(const f32x4*)s, x1 = *(const f32x4*)(s + 4);
     for (int k = 1; k < a.nsplit; ++k) {  // fixed summation order: deterministic
       x0 += *(const f32x4*)(s + k * a.split_stride);

@@ -116,20 +116,17 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_kernel(const FwdArgs a) {
   const int kv_end = CAUSAL ? min(Tk, q0 + BM) : Tk;
   const int ntiles = (kv_end + BN - 1) / BN;
 
+  // Keys past Tk are loaded from key Tk-1 (unconditional loads, no zero fill):
+  // the edge path masks them to -inf, so P = 0 there and V stays finite.
   u32x4 kreg[U], vreg[U];
   auto load_tile = [&](int k0) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int idx = tid + u * kThreads;
       const int r = idx / CH, c = idx % CH;
-      const int key = k0 + r;
-      if (key < Tk) {
-        kreg[u] = gload16(kp + (int64_t)key * a.kst + c * 8);
-        vreg[u] = gload16(vp + (int64_t)key * a.vst + c * 8);
-      } else {
-        kreg[u] = u32x4{0, 0, 0, 0};
-        vreg[u] = u32x4{0, 0, 0, 0};
-      }
+      const int key = min(k0 + r, Tk - 1);
+      kreg[u] = gload16(kp + (int64_t)key * a.kst + c * 8);
+      vreg[u] = gload16(vp + (int64_t)key * a.vst + c * 8);
     }
   };
   auto store_tile = [&](int buf) {

@@ -49,12 +49,13 @@ struct BwdArgs {
 };
 
 struct CvtArgs {
-  const float* src;      // nsplit x [B, T, H, D] fp32 contiguous slabs, summed
+  const float* src;      // nsplit fp32 slabs, element (b, t, h, d) at b*src_sb + t*src_st + h*src_sh + d
   void* dst;             // dtype, strided
   int64_t sb, st, sh;
   int B, T, H, D;
-  int nsplit;            // number of slabs (1 = plain conversion)
+  int nsplit;            // number of slabs summed (1 = plain conversion)
   int64_t split_stride;  // elements between slabs
+  int64_t src_sb, src_st, src_sh;
 };
 
 hipError_t launch_fwd(const FwdArgs& a, int D, int dtype, bool causal, hipStream_t s);

@@ -79,7 +79,7 @@ typedef struct FaBwdParams {
   float* delta;                  /* workspace [B, Hq, Tq] fp32 (written by fa_bwd_preprocess) */
   int32_t* dead_flags;           /* workspace [B * Hk] int32, zeroed by the caller */
   const uint8_t* mask; const float* score;
-  float* dq_accum;               /* workspace [B, Tq, Hq, D] fp32 contiguous (atomic dQ) */
+  float* dq_accum;               /* workspace [B, Hq, Tq, D] fp32 contiguous, head-major (atomic dQ) */
   float* dk_accum;               /* workspace [B, Tk, Hk, D] fp32 zeroed, only when plan.kv_split > 1 */
   float* dv_accum;               /* idem */
   void* dq; void* dk; void* dv;  /* outputs, dtype, strided like q/k/v */
