@@ -118,6 +118,11 @@ int fa_fwd(const FaFwdParams* p) {
                              p->score_stride_b, p->score_stride_h, p->score_stride_q)))
     return st;
 
+  // The forward stages K/V tiles with 32-bit buffer offsets (64 rows of a tile).
+  if (p->k_stride_t < 0 || p->k_stride_t >= (1LL << 24) || p->v_stride_t < 0 || p->v_stride_t >= (1LL << 24))
+    return fail(FA_ERR_STRIDE, "k/v time strides (%lld, %lld) must lie in [0, 2^24) elements",
+                (long long)p->k_stride_t, (long long)p->v_stride_t);
+
   fa::FwdArgs a{};
   a.q = p->q; a.k = p->k; a.v = p->v; a.o = p->o; a.lse = p->lse;
   a.mask = p->mask; a.score = p->score;

@@ -16,16 +16,27 @@
 // Softmax costs about as many VALU cycles as the two GEMMs cost MFMA cycles,
 // so the two must overlap.  The waves form two groups (0-3, 4-7) that run the
 // same step sequence one phase apart:
-//   M(i): S(i) = K(i) Q^T and O += V(i-1)^T P(i-1)      (MFMA phase)
-//   V(i): softmax of S(i) -> P(i), lazy rescale of O    (VALU phase)
+//   M(p): S(p) = K(p) Q^T and O += V(p-1)^T P(p-1)      (MFMA phase)
+//   V(p): softmax of S(p) -> P(p)                        (VALU phase)
 // Waves w and w+4 share a SIMD, so while one issues MFMAs the other issues
-// VALU work; a workgroup barrier separates the phases.  K/V tiles are
-// double-buffered in LDS and prefetched into registers two phases ahead; the
-// barrier waits only for LDS traffic, never for those loads.
+// VALU work; a workgroup barrier separates the phases.  The MFMA wave runs at
+// a raised issue priority so that the softmax wave fills the gaps.
 //
-// The running maximum is only moved when a tile's maximum exceeds it by more
-// than 2^8 (exact: O and l are rescaled consistently; p <= 256), which removes
-// the accumulator rescale from almost every tile.
+// K/V staging: tiles go from global memory straight into LDS with
+// buffer_load ... lds (no VGPR staging, no LDS stores): three buffers each for
+// K and V, a tile's loads issued three or four phases before its first use and
+// waited for (vmcnt) only at the barrier just before that use.  Rows are stored
+// unpadded with an XOR swizzle of their 16-byte chunks, chosen per tile kind
+// so that the K reads (ds_read_b128, 16 rows per bank cycle) and the V reads
+// (ds_read_b64_tr_b16, 4 rows x 4 chunks per bank cycle) are conflict-free.
+// Rows past the end of the keys are zero-filled by the buffer range check.
+//
+// Softmax fast path: p = exp2(s c - m_run) with the running maximum m_run
+// left unchanged, and the row sum taken over the packed P with v_dot2.  Only
+// when some p exceeds 2^8 (the lane's partial sum tells, conservatively) or
+// m_run is still -inf does the slow path compute the tile maximum, rescale
+// O and l, and redo P.  That is exact (O and l always share one reference)
+// and removes the max reduction and the rescale from almost every tile.
 #include "fa_common.h"
 #include "fa_kernels.h"
 
@@ -36,14 +47,28 @@ constexpr int kWaves = 8;               // two groups of four
 constexpr int kBM = kWaves * 32;        // query rows per workgroup
 constexpr int kBN = 64;                 // keys per tile
 constexpr int kThreads = kWaves * 64;
-constexpr float kRescaleLog2 = 8.0f;
+constexpr int kNBuf = 3;                // LDS buffers per tile kind
+constexpr float kFastSumMax = 256.0f;   // lane partial sum bound of the fast path
+
+template <int N> struct IC { static constexpr int value = N; };
+
+// Chunk swizzles (16-byte chunks of a 2*D-byte tile row).
+//  K: 16 lanes read one chunk of 16 consecutive rows -> 16 distinct bank groups.
+//  V: 32 lanes read 4 chunks (4 m .. 4 m + 3) of 4 rows (4 r0 .. 4 r0 + 3).
+template <int D> __device__ __forceinline__ int swz_k(int r) {
+  return D == 128 ? (r & 15) : ((r >> 1) & 7);
+}
+template <int D> __device__ __forceinline__ int swz_v(int r) {
+  return D == 128 ? ((r & 3) << 2) : (((r >> 1) & 1) << 2);
+}
 
 __device__ __forceinline__ uint32_t load_mask4(const uint8_t* row, int kk, int Tk, bool vec) {
+  // Unconditional loads (addresses clamped into the row): the caller masks
+  // keys >= Tk itself, and the number of memory instructions stays fixed.
   if (vec && kk + 4 <= Tk) return *(const uint32_t*)(row + kk);
   uint32_t r = 0;
 #pragma unroll
-  for (int t = 0; t < 4; ++t)
-    if (kk + t < Tk) r |= (uint32_t)(row[kk + t] != 0) << (8 * t);
+  for (int t = 0; t < 4; ++t) r |= (uint32_t)(row[min(kk + t, Tk - 1)] != 0) << (8 * t);
   return r;
 }
 
@@ -51,7 +76,7 @@ __device__ __forceinline__ f32x4 load_score4(const float* row, int kk, int Tk, b
   if (vec && kk + 4 <= Tk) return *(const f32x4*)(row + kk);
   f32x4 r;
 #pragma unroll
-  for (int t = 0; t < 4; ++t) r[t] = (kk + t < Tk) ? row[kk + t] : 0.f;
+  for (int t = 0; t < 4; ++t) r[t] = row[min(kk + t, Tk - 1)];
   return r;
 }
 
@@ -63,11 +88,57 @@ __device__ __forceinline__ u32x2 pack4(float x0, float x1, float x2, float x3) {
   return __builtin_bit_cast(u32x2, v);
 }
 
-// Workgroup barrier that waits for this wave's LDS traffic only: prefetch loads
-// to registers stay in flight across it.
+// Sum of the 8 packed values of x (fp32 accumulate), one v_dot2 per pair.
+__device__ __forceinline__ float dot_ones(bf16x8 x, float acc) {
+  typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+  const b2 one = {(__bf16)1.0f, (__bf16)1.0f};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) acc = __builtin_amdgcn_fdot2_f32_bf16(b2{x[2 * j], x[2 * j + 1]}, one, acc, false);
+  return acc;
+}
+__device__ __forceinline__ float dot_ones(f16x8 x, float acc) {
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  const h2 one = {(_Float16)1.0f, (_Float16)1.0f};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) acc = __builtin_amdgcn_fdot2(h2{x[2 * j], x[2 * j + 1]}, one, acc, false);
+  return acc;
+}
+
+// Hides x's value from the optimiser (keeps an address in one register).
+__device__ __forceinline__ uint32_t opaque(uint32_t x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+__device__ __forceinline__ u32x4 lds_read16_at(uint32_t addr) {
+  return *(const FA_LDS u32x4*)(uintptr_t)addr;
+}
+__device__ __forceinline__ s16x4 lds_read_tr_at(uint32_t addr) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((FA_LDS s16x4*)(uintptr_t)addr);
+}
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+// One 16-byte-per-lane buffer load into LDS: lane l's 16 bytes from
+// rsrc.base + voff land at LDS byte lds_addr + 16 l (lds_addr wave-uniform).
+// Issued as inline asm so that the compiler neither orders LDS reads behind
+// it nor counts it: every use is covered by an explicit vm_wait + barrier.
+__device__ __forceinline__ void dma16(i32x4 rsrc, uint32_t lds_addr, uint32_t voff) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :: "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(voff), "s"(rsrc) : "memory", "m0");
+}
+
+// Workgroup barrier that waits for this wave's LDS traffic only.
 __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_sched_barrier(0);
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+// Wait until at most N of this wave's vector-memory loads are outstanding
+// (loads complete in issue order, LDS-DMA loads included).
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
   __builtin_amdgcn_sched_barrier(0);
 }
 
@@ -78,19 +149,19 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
   constexpr int DS = D / 16;            // k-steps of S^T
   constexpr int NB = D / 32;            // 32-wide d blocks of O^T
   constexpr int CH = D / 8;             // 16-byte chunks per row
-  // Padded row strides (elements): K rows are read 16 rows x 16 B at a time
-  // (stride = 4 dwords mod 64 banks), V rows by the transpose read 4 rows x
-  // 64 B at a time (stride = 16 dwords mod 64 banks): both conflict-free, and
-  // every LDS address is a per-lane base plus an immediate offset.
-  constexpr int KS = D + 8, VS = D + 32;
-  constexpr int KT = BN * KS, VT = BN * VS;  // elements of one K / V tile
-  constexpr int U = BN * CH / kThreads;      // 16-byte chunks per thread per tile
-  static_assert(U >= 1 && BN * CH % kThreads == 0, "tile split");
-  constexpr int OS = D + 8;                  // epilogue O staging stride
-  static_assert(kWaves * 32 * OS <= 2 * (KT + VT), "O staging fits in the K/V buffers");
-  __shared__ __attribute__((aligned(16))) T smem[2 * (KT + VT)];
-  T* const kbuf = smem;           // [2][KT]
-  T* const vbuf = smem + 2 * KT;  // [2][VT]
+  constexpr int ROWB = 2 * D;           // bytes per tile row
+  constexpr int TILEB = BN * ROWB;      // bytes per K or V tile
+  constexpr int NI = TILEB / 1024;      // 1 KB DMA instructions per tile
+  constexpr int IPW = NI / kWaves;      // ... per wave
+  constexpr int RPI = 1024 / ROWB;      // tile rows per DMA instruction
+  constexpr int NDMA = 2 * IPW;         // DMA instructions per wave per batch (K + V tile)
+  constexpr int XMIN = 8 * ((MASK ? 1 : 0) + (SCORE ? 1 : 0));  // >= mask/score loads per M step
+  constexpr int KOFF = 0, VOFF = kNBuf * TILEB;
+  static_assert(NI % kWaves == 0 && IPW >= 1, "DMA split");
+  static_assert(kNBuf * TILEB <= 65536, "buffer + row offsets fit the 16-bit DS immediate");
+  constexpr int OS = D + 8;             // epilogue O staging stride (elements)
+  static_assert(kWaves * 32 * OS * 2 <= 2 * kNBuf * TILEB, "O staging fits in the K/V buffers");
+  __shared__ __attribute__((aligned(1024))) char smem[2 * kNBuf * TILEB];
 
   // ---- which (batch, head, query tile) -------------------------------------
   // Logical order (b, kv-head, [query tile descending, head in group]); with
@@ -120,7 +191,7 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
 
   // ---- Q fragment: lane holds Q[qrow][16 ds + 8 hf + 0..7] -------------------
   V8 qf[DS];
-  {
+  auto load_q = [&]() __attribute__((always_inline)) {
     const uint32_t neg = a.qsign < 0.f ? 0x80008000u : 0u;
     const T* src = qp + (int64_t)min(qrow, Tq - 1) * a.qst + hf * 8;
 #pragma unroll
@@ -129,63 +200,65 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
       x ^= neg;
       qf[ds] = as_vec8<T>(x);
     }
-  }
+  };
 
   const int kv_end = CAUSAL ? min(Tk, q0 + BM) : Tk;
   const int nt = (kv_end + BN - 1) / BN;                       // tiles of the workgroup
-  const int nt_w = CAUSAL ? min(nt, (min(Tk, q0w + 32) + BN - 1) / BN) : nt;  // tiles of this wave
+  // tiles of this wave (opaque: keeps the per-pair guards dynamic, so that
+  // every instantiation gets the same control flow and register assignment)
+  const int nt_w = (int)opaque((uint32_t)(CAUSAL ? min(nt, (min(Tk, q0w + 32) + BN - 1) / BN) : nt));
 
-  // Keys past Tk are loaded from key Tk-1 (unconditional loads, no zero fill):
-  // the edge path masks them to -inf, so P = 0 there and V stays finite.
-  // Full tiles use per-thread row pointers advanced by a uniform tile offset.
-  u32x4 kreg[U], vreg[U];
-  static_assert(kThreads % CH == 0, "chunk u of a thread is kThreads/CH rows below chunk 0");
-  const T* const kthr = kp + (int64_t)(tid / CH) * a.kst + (tid % CH) * 8;
-  const T* const vthr = vp + (int64_t)(tid / CH) * a.vst + (tid % CH) * 8;
-  const int64_t ktile = (int64_t)BN * a.kst, vtile = (int64_t)BN * a.vst;
-  const int64_t kstep = (int64_t)(kThreads / CH) * a.kst, vstep = (int64_t)(kThreads / CH) * a.vst;
-  auto load_k = [&](int j) {
-    if ((j + 1) * BN <= Tk) {
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(FA_LDS char*)smem;
+
+  // ---- LDS-DMA of K/V tiles ---------------------------------------------------
+  // DMA instruction n of a tile writes LDS bytes [1024 n, 1024 n + 1024): lane
+  // l -> tile row r = n RPI + l / CH, physical chunk l % CH, which holds the
+  // row's logical chunk (l % CH) ^ swz(r).  Wave w issues n = w IPW .. + IPW-1.
+  uint32_t voff_k[IPW], voff_v[IPW];
 #pragma unroll
-      for (int u = 0; u < U; ++u) kreg[u] = gload16(kthr + (j * ktile + u * kstep));
-    } else {
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int idx = tid + u * kThreads;
-        const int key = min(j * BN + idx / CH, Tk - 1);
-        kreg[u] = gload16(kp + (int64_t)key * a.kst + (idx % CH) * 8);
-      }
+  for (int u = 0; u < IPW; ++u) {
+    const int r = (wave * IPW + u) * RPI + lane / CH, pc = lane % CH;
+    voff_k[u] = (uint32_t)(r * a.kst * 2) + (uint32_t)((pc ^ swz_k<D>(r)) * 16);
+    voff_v[u] = (uint32_t)(r * a.vst * 2) + (uint32_t)((pc ^ swz_v<D>(r)) * 16);
+  }
+  // Tile t's rows [t BN, min(Tk, t BN + BN)); t >= nt gives an empty range, so
+  // the instructions still issue (fixed vmcnt accounting) but only write zeros.
+  auto dma = [&](const T* base, int64_t st, const uint32_t (&voff)[IPW], int t, int lds_off) __attribute__((always_inline)) {
+    uint32_t nrec = 0;
+    if (t < nt) {
+      const int64_t rows = min(Tk - t * BN, BN);
+      nrec = (uint32_t)min((rows - 1) * st * 2 + ROWB, (int64_t)0xfffffff0);
     }
-  };
-  auto load_v = [&](int j) {
-    if ((j + 1) * BN <= Tk) {
+    const uint64_t tb = (uint64_t)(base + (int64_t)t * BN * st);
+    const i32x4 rs = {(int)(uint32_t)tb, (int)((uint32_t)(tb >> 32) & 0xffffu), (int)nrec, 0x00020000};
 #pragma unroll
-      for (int u = 0; u < U; ++u) vreg[u] = gload16(vthr + (j * vtile + u * vstep));
-    } else {
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int idx = tid + u * kThreads;
-        const int key = min(j * BN + idx / CH, Tk - 1);
-        vreg[u] = gload16(vp + (int64_t)key * a.vst + (idx % CH) * 8);
-      }
-    }
+    for (int u = 0; u < IPW; ++u) dma16(rs, lds0 + lds_off + (wave * IPW + u) * 1024, voff[u]);
   };
-  auto store_k = [&](int j) {
-    T* ks = kbuf + (j & 1) * KT;
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int idx = tid + u * kThreads;
-      lds_write16(ks + (idx / CH) * KS + (idx % CH) * 8, kreg[u]);
-    }
+  // Batch of pair p: K(p+2) -> K buffer (p+2)%3, V(p+1) -> V buffer (p+1)%3.
+  auto dma_batch = [&](int p, int kbuf, int vbuf) __attribute__((always_inline)) {
+    dma(kp, a.kst, voff_k, p + 2, KOFF + kbuf * TILEB);
+    dma(vp, a.vst, voff_v, p + 1, VOFF + vbuf * TILEB);
   };
-  auto store_v = [&](int j) {
-    T* vs = vbuf + (j & 1) * VT;
+
+  // ---- per-lane LDS read addresses -------------------------------------------
+  // Byte addresses of buffer 0 of each kind; the buffer, k-block and key-row
+  // offsets are compile-time immediates (< 64 KB) added per read.  opaque()
+  // keeps the compiler from moving the region base into those immediates.
+  // K (A operand of S^T): lane reads row 32 kb + l32, logical chunk 2 ds + hf.
+  uint32_t kaddr[DS];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int idx = tid + u * kThreads;
-      lds_write16(vs + (idx / CH) * VS + (idx % CH) * 8, vreg[u]);
-    }
-  };
+  for (int ds = 0; ds < DS; ++ds)
+    kaddr[ds] = opaque(lds0 + KOFF + l32 * ROWB + (((2 * ds + hf) ^ swz_k<D>(l32)) * 16));
+  // V (A operand of O^T via the transpose read): lane addresses key row
+  // 32 (kk/2) + 16 (kk%2) + tr_row (+8), columns 32 nb + tr_col .. +3.
+  const int tr_row = 4 * hf + ((lane >> 2) & 3);
+  const int tr_col = ((lane >> 4) & 1) * 16 + (lane & 3) * 4;
+  uint32_t vaddr[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    const int c = nb * 32 + tr_col;
+    vaddr[nb] = opaque(lds0 + VOFF + tr_row * ROWB + ((((c >> 3) ^ swz_v<D>(tr_row))) * 16) + (c & 7) * 2);
+  }
 
   const int qrow_c = min(qrow, Tq - 1);  // clamped row for mask/score reads
   const uint8_t* mrow = nullptr;
@@ -194,191 +267,210 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
   if constexpr (SCORE) srow = a.score + b * a.ssb + h * a.ssh + (int64_t)qrow_c * a.ssq;
   const bool mvec = a.mask_vec != 0, svec = a.score_vec != 0;
   const float c2 = a.scale_log2;
-  const int tr_row = 4 * hf + ((lane >> 2) & 3);
-  const int tr_col = ((lane >> 4) & 1) * 16 + (lane & 3) * 4;
 
   f32x16 oacc[NB];
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) oacc[nb] = f32x16{};
   f32x16 sacc[2] = {f32x16{}, f32x16{}};
-  V8 pk[4];                        // P(i) packed for the next M step
+  V8 pk[4];                        // P(p) packed, B operand of the next M step
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) pk[kk] = V8{};
   uint32_t mreg[MASK ? 8 : 1];     // mask bytes of the tile in flight
   f32x4 sreg[SCORE ? 8 : 1];       // score of the tile in flight
   float m_run = kNegInf, l_run = 0.f;
 
-  // prologue: K(0) in LDS, K(1) and V(0) in flight
-  load_k(0);
-  store_k(0);
-  if (nt > 1) load_k(1);
-  load_v(0);
-  lds_barrier();
-
-  const int nph = 2 * nt + 2;
-  for (int ph = 0; ph < nph; ++ph) {
-    const int st = ph - grp;  // this wave's step
-    if (st >= 0 && st <= 2 * nt) {
-      const int i = st >> 1;
-      if ((st & 1) == 0) {
-        // ---- M(i): S(i) = K(i) Q^T and O += V(i-1)^T P(i-1) ----------------------
-        const bool do_s = i < nt_w;
-        const bool do_pv = i >= 1 && i - 1 < nt_w;
-        const T* ks = kbuf + (i & 1) * KT;
-        const T* vs = vbuf + ((i - 1) & 1) * VT;
-        if (do_s) {
-          if constexpr (MASK || SCORE) {
-            const int k0 = i * BN;
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-              for (int gi = 0; gi < 4; ++gi) {
-                const int kk = k0 + kb * 32 + gi * 8 + hf * 4;
-                if constexpr (MASK) mreg[kb * 4 + gi] = load_mask4(mrow, kk, Tk, mvec);
-                if constexpr (SCORE) sreg[kb * 4 + gi] = load_score4(srow, kk, Tk, svec);
-              }
-          }
-          sacc[0] = f32x16{};
-          sacc[1] = f32x16{};
-        }
-        if (do_s && do_pv) {
-          // The two independent chains interleaved, S op t = (kb = t%2, ds = t/2),
-          // PV op t = (kk = t/NB, nb = t%NB); operands are read from LDS three
-          // op-pairs ahead of their MFMAs so the LDS latency hides behind them.
-          constexpr int NOP = 2 * DS;   // == 4 * NB
-          constexpr int AHEAD = 3;
-          auto rd_s = [&](int t) -> u32x4 {
-            return lds_read16(ks + ((t & 1) * 32 + l32) * KS + (t >> 1) * 16 + hf * 8);
-          };
-          auto rd_pv = [&](int t) -> V8 {
-            const int kk = t / NB, nb = t % NB;
-            const int row = (kk >> 1) * 32 + 16 * (kk & 1) + tr_row;
-            const int col = nb * 32 + tr_col;
-            return cat_tr<T>(lds_read_tr(vs + row * VS + col), lds_read_tr(vs + (row + 8) * VS + col));
-          };
-          u32x4 kq[AHEAD];
-          V8 vq[AHEAD];
-#pragma unroll
-          for (int t = 0; t < AHEAD; ++t) {
-            kq[t] = rd_s(t);
-            vq[t] = rd_pv(t);
-          }
-          __builtin_amdgcn_sched_group_barrier(0x100, 3 * AHEAD, 0);
-#pragma unroll
-          for (int t = 0; t < NOP; ++t) {
-            sacc[t & 1] = mfma32(as_vec8<T>(kq[t % AHEAD]), qf[t >> 1], sacc[t & 1]);
-            oacc[t % NB] = mfma32(vq[t % AHEAD], pk[t / NB], oacc[t % NB]);
-            if (t + AHEAD < NOP) {
-              kq[t % AHEAD] = rd_s(t + AHEAD);
-              vq[t % AHEAD] = rd_pv(t + AHEAD);
-            }
-            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-            if (t + AHEAD < NOP) __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
-          }
-        } else if (do_s) {
-#pragma unroll
-          for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-            for (int ds = 0; ds < DS; ++ds) {
-              const u32x4 kx = lds_read16(ks + (kb * 32 + l32) * KS + ds * 16 + hf * 8);
-              sacc[kb] = mfma32(as_vec8<T>(kx), qf[ds], sacc[kb]);
-            }
-        } else if (do_pv) {
-#pragma unroll
-          for (int kk = 0; kk < 4; ++kk) {
-            const int row = (kk >> 1) * 32 + 16 * (kk & 1) + tr_row;
-#pragma unroll
-            for (int nb = 0; nb < NB; ++nb) {
-              const int col = nb * 32 + tr_col;
-              const s16x4 lo = lds_read_tr(vs + row * VS + col);
-              const s16x4 hi = lds_read_tr(vs + (row + 8) * VS + col);
-              oacc[nb] = mfma32(cat_tr<T>(lo, hi), pk[kk], oacc[nb]);
-            }
-          }
-        }
-      } else if (i < nt_w) {
-        // ---- V(i): softmax of S(i) -> P(i) -----------------------------------------
-        // lane's entry (kb, e) is key 64 i + 32 kb + 8 (e/4) + 4 hf + e%4 of row qrow
-        const int k0 = i * BN;
-        if constexpr (SCORE) {
-#pragma unroll
-          for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-            for (int gi = 0; gi < 4; ++gi)
-#pragma unroll
-              for (int t = 0; t < 4; ++t)
-                sacc[kb][gi * 4 + t] = fmaf(a.qsign, sreg[kb * 4 + gi][t], sacc[kb][gi * 4 + t]);
-        }
-        const bool edge = MASK || a.zero_scale || (k0 + BN > Tk) || (CAUSAL && k0 + BN - 1 > q0w);
-        if (edge) {
-#pragma unroll
-          for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-            for (int gi = 0; gi < 4; ++gi) {
-              const int kk = k0 + kb * 32 + gi * 8 + hf * 4;
-              uint32_t mb = 0x01010101u;
-              if constexpr (MASK) mb = mreg[kb * 4 + gi];
-#pragma unroll
-              for (int t = 0; t < 4; ++t) {
-                const int key = kk + t;
-                bool keep = key < Tk;
-                if constexpr (CAUSAL) keep = keep && (key <= qrow);
-                if constexpr (MASK) keep = keep && (((mb >> (8 * t)) & 0xffu) != 0);
-                const float sv = sacc[kb][gi * 4 + t];
-                sacc[kb][gi * 4 + t] = keep ? (a.zero_scale ? 0.f : sv) : kNegInf;
-              }
-            }
-        }
-        float mx = kNegInf;
+  // ---- M(p): S(p) = K(p) Q^T and O += V(p-1)^T P(p-1) ---------------------------
+  // S(p) is computed (and later discarded) also when p >= nt_w, and PV(p-1)
+  // also when p == 0 (P = 0 against a zeroed V buffer): one straight-line body.
+  auto m_step = [&](auto KBc, int p) __attribute__((always_inline)) {
+    constexpr int KB = decltype(KBc)::value;
+    constexpr uint32_t kb_lds = KB * TILEB;                      // K(p), relative to K buffer 0
+    constexpr uint32_t vb_lds = ((KB + 2) % kNBuf) * TILEB;      // V(p-1), relative to V buffer 0
+    if constexpr (MASK || SCORE) {
+      if (p < nt_w) {
+        const int k0 = p * BN;
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-          for (int e = 0; e < 16; ++e) mx = fmaxf(mx, sacc[kb][e]);
-        mx = half_max(mx);
-        const float m_tile = mx * c2;
-        if (wave_any(m_tile > m_run + kRescaleLog2)) {
-          const float m_new = fmaxf(m_run, m_tile);
-          const float alpha = (m_run == kNegInf) ? 0.f : exp2_fast(m_run - m_new);
-          l_run *= alpha;
-#pragma unroll
-          for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-            for (int e = 0; e < 16; ++e) oacc[nb][e] *= alpha;
-          m_run = m_new;
-        }
-        const float mneg = (m_run == kNegInf) ? 0.f : -m_run;
-        float lsum = 0.f;
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int e = 0; e < 16; ++e) {
-            const float p = exp2_fast(fmaf(sacc[kb][e], c2, mneg));
-            sacc[kb][e] = p;
-            lsum += p;
+          for (int gi = 0; gi < 4; ++gi) {
+            const int kk = k0 + kb * 32 + gi * 8 + hf * 4;
+            if constexpr (MASK) mreg[kb * 4 + gi] = load_mask4(mrow, kk, Tk, mvec);
+            if constexpr (SCORE) sreg[kb * 4 + gi] = load_score4(srow, kk, Tk, svec);
           }
-        l_run += lsum;
-        // key slot t of k-step kk (= 2 kb + c) <-> key 32 kb + 16 c + 4 hf + t%4 + 8 (t/4)
-#pragma unroll
-        for (int kk = 0; kk < 4; ++kk) {
-          const int kb = kk >> 1, c = kk & 1;
-          pk[kk] = pack8<T>(sacc[kb][8 * c + 0], sacc[kb][8 * c + 1], sacc[kb][8 * c + 2], sacc[kb][8 * c + 3],
-                            sacc[kb][8 * c + 4], sacc[kb][8 * c + 5], sacc[kb][8 * c + 6], sacc[kb][8 * c + 7]);
-        }
       }
     }
-    if (ph & 1) {
-      // odd phase 2j+1: K(j+1) and V(j) to LDS, then prefetch K(j+2) and V(j+1)
-      const int j = ph >> 1;
-      if (j + 1 < nt) store_k(j + 1);
-      if (j < nt) store_v(j);
-      if (j + 2 < nt) load_k(j + 2);
-      if (j + 1 < nt) load_v(j + 1);
+    __builtin_amdgcn_s_setprio(2);
+    // The two independent chains interleaved, S op t = (kb = t%2, ds = t/2),
+    // PV op t = (kk = t/NB, nb = t%NB); operands are read from LDS AHEAD op
+    // pairs before their MFMAs.
+    constexpr int NOP = 2 * DS;   // == 4 * NB
+    constexpr int AHEAD = 3;
+    auto rd_s = [&](int t) __attribute__((always_inline)) -> u32x4 {
+      return lds_read16_at(kaddr[t >> 1] + kb_lds + (uint32_t)((t & 1) * 32 * ROWB));
+    };
+    auto rd_pv = [&](int t) __attribute__((always_inline)) -> V8 {
+      const int kk = t / NB, nb = t % NB;
+      const uint32_t row = (kk >> 1) * 32 + 16 * (kk & 1);
+      const uint32_t base = vaddr[nb] + vb_lds + row * ROWB;
+      return cat_tr<T>(lds_read_tr_at(base), lds_read_tr_at(base + 8 * ROWB));
+    };
+    u32x4 kq[AHEAD];
+    V8 vq[AHEAD];
+#pragma unroll
+    for (int t = 0; t < AHEAD; ++t) {
+      kq[t] = rd_s(t);
+      vq[t] = rd_pv(t);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x100, 3 * AHEAD, 0);
+#pragma unroll
+    for (int t = 0; t < NOP; ++t) {
+      const int kb = t & 1, ds = t >> 1;
+      sacc[kb] = mfma32(as_vec8<T>(kq[t % AHEAD]), qf[ds], ds == 0 ? f32x16{} : sacc[kb]);
+      oacc[t % NB] = mfma32(vq[t % AHEAD], pk[t / NB], oacc[t % NB]);
+      if (t + AHEAD < NOP) {
+        kq[t % AHEAD] = rd_s(t + AHEAD);
+        vq[t % AHEAD] = rd_pv(t + AHEAD);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+      if (t + AHEAD < NOP) __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
+    }
+    __builtin_amdgcn_s_setprio(0);
+  };
+
+  // P = exp2(S c - m) packed into pk; returns the lane's partial row sum.
+  auto make_p = [&](float mneg) __attribute__((always_inline)) -> float {
+    float lsum = 0.f;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const int kb = kk >> 1, c = kk & 1;
+      float x[8];
+#pragma unroll
+      for (int t = 0; t < 8; ++t) x[t] = exp2_fast(fmaf(sacc[kb][8 * c + t], c2, mneg));
+      pk[kk] = pack8<T>(x[0], x[1], x[2], x[3], x[4], x[5], x[6], x[7]);
+      lsum = dot_ones(pk[kk], lsum);
+    }
+    return lsum;
+  };
+
+  // ---- V(p): softmax of S(p) -> P(p) ----------------------------------------------
+  // lane's entry (kb, e) is key 64 p + 32 kb + 8 (e/4) + 4 hf + e%4 of row qrow;
+  // key slot t of k-step kk (= 2 kb + c) <-> key 32 kb + 16 c + 4 hf + t%4 + 8 (t/4)
+  auto v_step = [&](int p, auto&& issue_dma) __attribute__((always_inline)) {
+    const int k0 = p * BN;
+    if constexpr (SCORE) {
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int gi = 0; gi < 4; ++gi)
+#pragma unroll
+          for (int t = 0; t < 4; ++t)
+            sacc[kb][gi * 4 + t] = fmaf(a.qsign, sreg[kb * 4 + gi][t], sacc[kb][gi * 4 + t]);
+    }
+    const bool edge = MASK || a.zero_scale || (k0 + BN > Tk) || (CAUSAL && k0 + BN - 1 > q0w);
+    if (edge) {
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int gi = 0; gi < 4; ++gi) {
+          const int kk = k0 + kb * 32 + gi * 8 + hf * 4;
+          uint32_t mb = 0x01010101u;
+          if constexpr (MASK) mb = mreg[kb * 4 + gi];
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const int key = kk + t;
+            bool keep = key < Tk;
+            if constexpr (CAUSAL) keep = keep && (key <= qrow);
+            if constexpr (MASK) keep = keep && (((mb >> (8 * t)) & 0xffu) != 0);
+            const float sv = sacc[kb][gi * 4 + t];
+            sacc[kb][gi * 4 + t] = keep ? (a.zero_scale ? 0.f : sv) : kNegInf;
+          }
+        }
+    }
+    // The mask/score registers are consumed: loads issued from here on do not
+    // delay this wave's next wait for them.
+    issue_dma();
+    // Fast path against the current m_run (+inf offset while m_run is -inf,
+    // which makes the sum inf or NaN and forces the slow path).
+    float lsum = make_p(-m_run);
+    if (wave_any(!(lsum <= kFastSumMax))) {
+      float mx = kNegInf;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) mx = fmaxf(mx, sacc[kb][e]);
+      mx = half_max(mx);
+      const float m_new = fmaxf(m_run, mx * c2);
+      const float alpha = (m_run == kNegInf) ? 0.f : exp2_fast(m_run - m_new);
+      l_run *= alpha;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) oacc[nb][e] *= alpha;
+      m_run = m_new;
+      lsum = make_p(m_run == kNegInf ? 0.f : -m_run);
+    }
+    l_run += lsum;
+  };
+
+  // ---- prologue: zero V buffer 2 (read as V(-1) with P = 0), DMA K(0), K(1), V(0)
+  {
+    char* z = smem + VOFF + 2 * TILEB;
+#pragma unroll
+    for (int u = 0; u < TILEB / (kThreads * 16); ++u) lds_write16(z + (tid + u * kThreads) * 16, u32x4{0, 0, 0, 0});
+  }
+  dma(kp, a.kst, voff_k, 0, KOFF + 0 * TILEB);
+  load_q();
+  // The compiler waits for Q here (vmcnt(0)), which also covers K(0).
+#pragma unroll
+  for (int ds = 0; ds < DS; ++ds) asm volatile("" ::"v"(qf[ds]));
+  dma(kp, a.kst, voff_k, 1, KOFF + 1 * TILEB);
+  dma(vp, a.vst, voff_v, 0, VOFF + 0 * TILEB);
+  lds_barrier();
+
+  // ---- main loop over phase pairs p = 0 .. nt ------------------------------------
+  // pair p: phase 2p   group 0: M(p)            group 1: V(p-1) + DMA batch p
+  //         phase 2p+1 group 0: V(p) + batch p  group 1: M(p)
+  // Each wave issues its share of batch p (K(p+2), V(p+1)) in its softmax
+  // phase, after the mask/score registers are consumed.  End of phase 2p+1:
+  // batch p-1 (K(p+1), V(p), needed from phase 2p+2 on) must have landed.  Of
+  // this wave's loads issued after it, the newest are batch p (group 0), or
+  // batch p followed by the mask/score loads of M(p) when that ran (group 1).
+  auto pair = [&](auto KBc, int p) __attribute__((always_inline)) {
+    constexpr int KB = decltype(KBc)::value;
+    auto batch = [&]() __attribute__((always_inline)) { dma_batch(p, (KB + 2) % kNBuf, (KB + 1) % kNBuf); };
+    const bool m_act = p <= nt_w;
+    if (grp == 0) {
+      if (m_act) m_step(KBc, p);
+    } else {
+      if (p >= 1 && p - 1 < nt_w) v_step(p - 1, batch);
+      else batch();
     }
     lds_barrier();
+    if (grp == 0) {
+      if (p < nt_w) v_step(p, batch);
+      else batch();
+      vm_wait<NDMA>();
+    } else {
+      if (m_act) m_step(KBc, p);
+      if (XMIN > 0 && p < nt_w) vm_wait<NDMA + XMIN>();
+      else vm_wait<NDMA>();
+    }
+    lds_barrier();
+  };
+  for (int p = 0; p <= nt; p += 3) {
+    pair(IC<0>{}, p);
+    if (p + 1 > nt) break;
+    pair(IC<1>{}, p + 1);
+    if (p + 2 > nt) break;
+    pair(IC<2>{}, p + 2);
   }
 
   // ---- epilogue: O = acc / l (NaN for a row with no kept key), LSE ----------------
+  vm_wait<0>();   // the last (zero-filling) DMA batch must not land on the staging area
+  lds_barrier();
   const float l_tot = half_sum(l_run);
   const float inv = 1.0f / l_tot;
-  T* os = smem + wave * 32 * OS;  // wave-private staging, K/V buffers are free now
+  T* os = (T*)smem + wave * 32 * OS;  // wave-private staging, K/V buffers are free now
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
