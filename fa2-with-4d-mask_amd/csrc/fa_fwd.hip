@@ -22,14 +22,17 @@
 // VALU work; a workgroup barrier separates the phases.  The MFMA wave runs at
 // a raised issue priority so that the softmax wave fills the gaps.
 //
-// K/V staging: tiles go from global memory straight into LDS with
-// buffer_load ... lds (no VGPR staging, no LDS stores): three buffers each for
-// K and V, a tile's loads issued three or four phases before its first use and
-// waited for (vmcnt) only at the barrier just before that use.  Rows are stored
-// unpadded with an XOR swizzle of their 16-byte chunks, chosen per tile kind
-// so that the K reads (ds_read_b128, 16 rows per bank cycle) and the V reads
-// (ds_read_b64_tr_b16, 4 rows x 4 chunks per bank cycle) are conflict-free.
-// Rows past the end of the keys are zero-filled by the buffer range check.
+// K/V staging: three LDS buffers each for K and V.  In its softmax phase each
+// wave writes its share of the tiles loaded one phase pair earlier (16 bytes
+// per lane per chunk, held in registers meanwhile) and loads its share of the
+// next ones, with buffer loads whose per-lane offsets are loop-invariant and
+// whose tile base sits in scalar registers; rows past the end of the keys are
+// zero-filled by the buffer range check.  (Direct global->LDS loads were
+// measured slower here: their issue stalls once ~32 KB per CU are in flight.)
+// Rows are stored unpadded with an XOR swizzle of their 16-byte chunks, chosen
+// per tile kind so that the K reads (ds_read_b128, 16 rows per bank cycle) and
+// the V reads (ds_read_b64_tr_b16, 4 rows x 4 chunks per bank cycle) are
+// conflict-free.
 //
 // Softmax fast path: p = exp2(s c - m_run) with the running maximum m_run
 // left unchanged, and the row sum taken over the packed P with v_dot2.  Only
@@ -116,15 +119,8 @@ __device__ __forceinline__ s16x4 lds_read_tr_at(uint32_t addr) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((FA_LDS s16x4*)(uintptr_t)addr);
 }
 
-typedef int i32x4 __attribute__((ext_vector_type(4)));
-
-// One 16-byte-per-lane buffer load into LDS: lane l's 16 bytes from
-// rsrc.base + voff land at LDS byte lds_addr + 16 l (lds_addr wave-uniform).
-// Issued as inline asm so that the compiler neither orders LDS reads behind
-// it nor counts it: every use is covered by an explicit vm_wait + barrier.
-__device__ __forceinline__ void dma16(i32x4 rsrc, uint32_t lds_addr, uint32_t voff) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-               :: "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(voff), "s"(rsrc) : "memory", "m0");
+__device__ __forceinline__ void lds_write16_at(uint32_t addr, u32x4 v) {
+  *(FA_LDS u32x4*)(uintptr_t)addr = v;
 }
 
 // Workgroup barrier that waits for this wave's LDS traffic only.
@@ -133,15 +129,6 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   __builtin_amdgcn_sched_barrier(0);
 }
-// Wait until at most N of this wave's vector-memory loads are outstanding
-// (loads complete in issue order, LDS-DMA loads included).
-template <int N>
-__device__ __forceinline__ void vm_wait() {
-  __builtin_amdgcn_sched_barrier(0);
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-  __builtin_amdgcn_sched_barrier(0);
-}
-
 template <typename T, int D, bool CAUSAL, bool MASK, bool SCORE>
 __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
   using V8 = typename Vec8<T>::type;
@@ -151,13 +138,12 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
   constexpr int CH = D / 8;             // 16-byte chunks per row
   constexpr int ROWB = 2 * D;           // bytes per tile row
   constexpr int TILEB = BN * ROWB;      // bytes per K or V tile
-  constexpr int NI = TILEB / 1024;      // 1 KB DMA instructions per tile
-  constexpr int IPW = NI / kWaves;      // ... per wave
-  constexpr int RPI = 1024 / ROWB;      // tile rows per DMA instruction
-  constexpr int NDMA = 2 * IPW;         // DMA instructions per wave per batch (K + V tile)
-  constexpr int XMIN = 8 * ((MASK ? 1 : 0) + (SCORE ? 1 : 0));  // >= mask/score loads per M step
+  constexpr int NI = TILEB / 1024;      // 1 KB slots (64 lanes x 16 bytes) per tile
+  constexpr int IPW = NI / kWaves;      // ... staged by each wave
+  constexpr int RPI = 1024 / ROWB;      // tile rows per slot
+  constexpr int NSTG = 2 * IPW;         // staging registers (x 16 bytes) per lane: K + V
   constexpr int KOFF = 0, VOFF = kNBuf * TILEB;
-  static_assert(NI % kWaves == 0 && IPW >= 1, "DMA split");
+  static_assert(NI % kWaves == 0 && IPW >= 1, "staging split");
   static_assert(kNBuf * TILEB <= 65536, "buffer + row offsets fit the 16-bit DS immediate");
   constexpr int OS = D + 8;             // epilogue O staging stride (elements)
   static_assert(kWaves * 32 * OS * 2 <= 2 * kNBuf * TILEB, "O staging fits in the K/V buffers");
@@ -210,34 +196,54 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
 
   const uint32_t lds0 = (uint32_t)(uintptr_t)(FA_LDS char*)smem;
 
-  // ---- LDS-DMA of K/V tiles ---------------------------------------------------
-  // DMA instruction n of a tile writes LDS bytes [1024 n, 1024 n + 1024): lane
-  // l -> tile row r = n RPI + l / CH, physical chunk l % CH, which holds the
-  // row's logical chunk (l % CH) ^ swz(r).  Wave w issues n = w IPW .. + IPW-1.
-  uint32_t voff_k[IPW], voff_v[IPW];
+  // ---- K/V staging ------------------------------------------------------------
+  // Slot n of a tile (wave w stages n = w IPW .. + IPW-1): lane l -> tile row
+  // r = n RPI + l / CH, logical chunk c = l % CH (1 KB of whole rows, read
+  // coalesced), written at physical chunk c ^ swz(r) of row r.
+  uint32_t goff_k[IPW], goff_v[IPW], soff_k[IPW], soff_v[IPW];
 #pragma unroll
   for (int u = 0; u < IPW; ++u) {
-    const int r = (wave * IPW + u) * RPI + lane / CH, pc = lane % CH;
-    voff_k[u] = (uint32_t)(r * a.kst * 2) + (uint32_t)((pc ^ swz_k<D>(r)) * 16);
-    voff_v[u] = (uint32_t)(r * a.vst * 2) + (uint32_t)((pc ^ swz_v<D>(r)) * 16);
+    const int r = (wave * IPW + u) * RPI + lane / CH, c = lane % CH;
+    goff_k[u] = (uint32_t)(r * a.kst * 2) + (uint32_t)(c * 16);
+    goff_v[u] = (uint32_t)(r * a.vst * 2) + (uint32_t)(c * 16);
+    soff_k[u] = opaque(lds0 + KOFF + r * ROWB + ((c ^ swz_k<D>(r)) * 16));
+    soff_v[u] = opaque(lds0 + VOFF + r * ROWB + ((c ^ swz_v<D>(r)) * 16));
   }
-  // Tile t's rows [t BN, min(Tk, t BN + BN)); t >= nt gives an empty range, so
-  // the instructions still issue (fixed vmcnt accounting) but only write zeros.
-  auto dma = [&](const T* base, int64_t st, const uint32_t (&voff)[IPW], int t, int lds_off) __attribute__((always_inline)) {
+  // Tile t's rows [t BN, min(Tk, t BN + BN)); t >= nt gives an empty range
+  // (the loads return zeros).
+  auto rsrc_of = [&](const T* base, int64_t st, int t) __attribute__((always_inline)) {
     uint32_t nrec = 0;
     if (t < nt) {
       const int64_t rows = min(Tk - t * BN, BN);
       nrec = (uint32_t)min((rows - 1) * st * 2 + ROWB, (int64_t)0xfffffff0);
     }
-    const uint64_t tb = (uint64_t)(base + (int64_t)t * BN * st);
-    const i32x4 rs = {(int)(uint32_t)tb, (int)((uint32_t)(tb >> 32) & 0xffffu), (int)nrec, 0x00020000};
-#pragma unroll
-    for (int u = 0; u < IPW; ++u) dma16(rs, lds0 + lds_off + (wave * IPW + u) * 1024, voff[u]);
+    return __builtin_amdgcn_make_buffer_rsrc((void*)(base + (int64_t)t * BN * st), (short)0, (int)nrec, 0x00020000);
   };
+  u32x4 stg[NSTG];   // K slots, then V slots, of the next batch
   // Batch of pair p: K(p+2) -> K buffer (p+2)%3, V(p+1) -> V buffer (p+1)%3.
-  auto dma_batch = [&](int p, int kbuf, int vbuf) __attribute__((always_inline)) {
-    dma(kp, a.kst, voff_k, p + 2, KOFF + kbuf * TILEB);
-    dma(vp, a.vst, voff_v, p + 1, VOFF + vbuf * TILEB);
+  auto load_batch = [&](int p) __attribute__((always_inline)) {
+    const auto rk = rsrc_of(kp, a.kst, p + 2), rv = rsrc_of(vp, a.vst, p + 1);
+#pragma unroll
+    for (int u = 0; u < IPW; ++u) {
+      stg[u] = __builtin_amdgcn_raw_buffer_load_b128(rk, goff_k[u], 0, 0);
+      stg[IPW + u] = __builtin_amdgcn_raw_buffer_load_b128(rv, goff_v[u], 0, 0);
+    }
+  };
+  auto store_batch = [&](int kbuf, int vbuf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < IPW; ++u) {
+      lds_write16_at(soff_k[u] + kbuf * TILEB, stg[u]);
+      lds_write16_at(soff_v[u] + vbuf * TILEB, stg[IPW + u]);
+    }
+  };
+  // Tile written straight through the staging registers (prologue).
+  auto put_tile = [&](bool is_k, int t, int buf) __attribute__((always_inline)) {
+    const auto rs = is_k ? rsrc_of(kp, a.kst, t) : rsrc_of(vp, a.vst, t);
+#pragma unroll
+    for (int u = 0; u < IPW; ++u) {
+      const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(rs, is_k ? goff_k[u] : goff_v[u], 0, 0);
+      lds_write16_at((is_k ? soff_k[u] : soff_v[u]) + buf * TILEB, x);
+    }
   };
 
   // ---- per-lane LDS read addresses -------------------------------------------
@@ -355,7 +361,7 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
   // ---- V(p): softmax of S(p) -> P(p) ----------------------------------------------
   // lane's entry (kb, e) is key 64 p + 32 kb + 8 (e/4) + 4 hf + e%4 of row qrow;
   // key slot t of k-step kk (= 2 kb + c) <-> key 32 kb + 16 c + 4 hf + t%4 + 8 (t/4)
-  auto v_step = [&](int p, auto&& issue_dma) __attribute__((always_inline)) {
+  auto v_step = [&](int p, auto&& stage) __attribute__((always_inline)) {
     const int k0 = p * BN;
     if constexpr (SCORE) {
 #pragma unroll
@@ -388,7 +394,7 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
     }
     // The mask/score registers are consumed: loads issued from here on do not
     // delay this wave's next wait for them.
-    issue_dma();
+    stage();
     // Fast path against the current m_run (+inf offset while m_run is -inf,
     // which makes the sum inf or NaN and forces the slow path).
     float lsum = make_p(-m_run);
@@ -412,48 +418,45 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
     l_run += lsum;
   };
 
-  // ---- prologue: zero V buffer 2 (read as V(-1) with P = 0), DMA K(0), K(1), V(0)
+  // ---- prologue: zero V buffer 2 (read as V(-1) with P = 0), K(0), K(1), V(0)
+  // to LDS, batch 0 (K(2), V(1)) into the staging registers.
   {
     char* z = smem + VOFF + 2 * TILEB;
 #pragma unroll
     for (int u = 0; u < TILEB / (kThreads * 16); ++u) lds_write16(z + (tid + u * kThreads) * 16, u32x4{0, 0, 0, 0});
   }
-  dma(kp, a.kst, voff_k, 0, KOFF + 0 * TILEB);
   load_q();
-  // The compiler waits for Q here (vmcnt(0)), which also covers K(0).
-#pragma unroll
-  for (int ds = 0; ds < DS; ++ds) asm volatile("" ::"v"(qf[ds]));
-  dma(kp, a.kst, voff_k, 1, KOFF + 1 * TILEB);
-  dma(vp, a.vst, voff_v, 0, VOFF + 0 * TILEB);
+  put_tile(true, 0, 0);
+  put_tile(true, 1, 1);
+  put_tile(false, 0, 0);
+  load_batch(0);
   lds_barrier();
 
   // ---- main loop over phase pairs p = 0 .. nt ------------------------------------
-  // pair p: phase 2p   group 0: M(p)            group 1: V(p-1) + DMA batch p
-  //         phase 2p+1 group 0: V(p) + batch p  group 1: M(p)
-  // Each wave issues its share of batch p (K(p+2), V(p+1)) in its softmax
-  // phase, after the mask/score registers are consumed.  End of phase 2p+1:
-  // batch p-1 (K(p+1), V(p), needed from phase 2p+2 on) must have landed.  Of
-  // this wave's loads issued after it, the newest are batch p (group 0), or
-  // batch p followed by the mask/score loads of M(p) when that ran (group 1).
+  // pair p: phase 2p   group 0: M(p)   group 1: V(p-1)
+  //         phase 2p+1 group 0: V(p)   group 1: M(p)
+  // In its softmax phase of pair p each wave stores its share of batch p
+  // (K(p+2), V(p+1), loaded during pair p-1) and loads its share of batch
+  // p+1.  The buffers written are free (last read in pair p-1), and the
+  // barriers that follow make the tiles visible before pair p+2 reads them.
   auto pair = [&](auto KBc, int p) __attribute__((always_inline)) {
     constexpr int KB = decltype(KBc)::value;
-    auto batch = [&]() __attribute__((always_inline)) { dma_batch(p, (KB + 2) % kNBuf, (KB + 1) % kNBuf); };
-    const bool m_act = p <= nt_w;
+    auto stage = [&]() __attribute__((always_inline)) {
+      store_batch((KB + 2) % kNBuf, (KB + 1) % kNBuf);
+      load_batch(p + 1);
+    };
     if (grp == 0) {
-      if (m_act) m_step(KBc, p);
+      if (p <= nt_w) m_step(KBc, p);
     } else {
-      if (p >= 1 && p - 1 < nt_w) v_step(p - 1, batch);
-      else batch();
+      if (p >= 1 && p - 1 < nt_w) v_step(p - 1, stage);
+      else stage();
     }
     lds_barrier();
     if (grp == 0) {
-      if (p < nt_w) v_step(p, batch);
-      else batch();
-      vm_wait<NDMA>();
+      if (p < nt_w) v_step(p, stage);
+      else stage();
     } else {
-      if (m_act) m_step(KBc, p);
-      if (XMIN > 0 && p < nt_w) vm_wait<NDMA + XMIN>();
-      else vm_wait<NDMA>();
+      if (p <= nt_w) m_step(KBc, p);
     }
     lds_barrier();
   };
@@ -466,8 +469,6 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
   }
 
   // ---- epilogue: O = acc / l (NaN for a row with no kept key), LSE ----------------
-  vm_wait<0>();   // the last (zero-filling) DMA batch must not land on the staging area
-  lds_barrier();
   const float l_tot = half_sum(l_run);
   const float inv = 1.0f / l_tot;
   T* os = (T*)smem + wave * 32 * OS;  // wave-private staging, K/V buffers are free now
