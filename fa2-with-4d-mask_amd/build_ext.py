@@ -23,7 +23,7 @@ CSRC = HERE / "csrc"
 BUILD = HERE / "_build"
 LIBDIR = HERE / "tilelang_fa2_4d_mask" / "_lib"
 LIB = LIBDIR / "libfa2_4d_mask.so"
-SOURCES = ["fa_fwd.hip", "fa_bwd.hip", "fa_api.cpp"]
+SOURCES = ["fa_fwd.hip", "fa_bwd.hip", "fa_bwd_kv.hip", "fa_api.cpp"]
 ARCH = "gfx950"
 
 

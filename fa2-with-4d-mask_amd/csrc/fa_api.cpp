@@ -81,7 +81,8 @@ int launch_status(hipError_t e, const char* what) {
 int choose_split(const FaBwdParams* p) {
   if (p->kv_split > 0) return p->kv_split;
   const int G = p->heads_q / p->heads_k;
-  const int nkt = (p->seqlen_k + fa::dkdv_block_keys() - 1) / fa::dkdv_block_keys();
+  const int kb = p->atomic_dq ? fa::dkdv_block_keys() : fa::dkdv2_block_keys();
+  const int nkt = (p->seqlen_k + kb - 1) / kb;
   const int64_t base = (int64_t)p->batch * p->heads_k * nkt;
   const int64_t target = 512;  // two workgroups per CU on a 256-CU part
   int split = 1;
@@ -153,6 +154,10 @@ static int check_bwd(const FaBwdParams* p, int split) {
   if ((st = check_operand("dq", p->dq, p->dq_stride_b, p->dq_stride_t, p->dq_stride_h))) return st;
   if ((st = check_operand("dk", p->dk, p->dk_stride_b, p->dk_stride_t, p->dk_stride_h))) return st;
   if ((st = check_operand("dv", p->dv, p->dv_stride_b, p->dv_stride_t, p->dv_stride_h))) return st;
+  // The dK/dV kernel stages Q/dO tiles with 32-bit buffer offsets (32 rows of a tile).
+  if (p->q_stride_t < 0 || p->q_stride_t >= (1LL << 24) || p->do_stride_t < 0 || p->do_stride_t >= (1LL << 24))
+    return fail(FA_ERR_STRIDE, "q/dout time strides (%lld, %lld) must lie in [0, 2^24) elements",
+                (long long)p->q_stride_t, (long long)p->do_stride_t);
   if (!p->lse) return fail(FA_ERR_NULL, "lse is NULL");
   if (!p->delta) return fail(FA_ERR_NULL, "delta is NULL");
   if (!p->dead_flags) return fail(FA_ERR_NULL, "dead_flags is NULL");
@@ -222,7 +227,8 @@ int fa_bwd(const FaBwdParams* p) {
   a.ssb = p->score_stride_b; a.ssh = p->score_stride_h; a.ssq = p->score_stride_q;
   a.B = p->batch; a.Tq = p->seqlen_q; a.Tk = p->seqlen_k; a.Hq = p->heads_q; a.Hk = p->heads_k;
   a.G = p->heads_q / p->heads_k;
-  a.nkt = (p->seqlen_k + fa::dkdv_block_keys() - 1) / fa::dkdv_block_keys();
+  const int kb = p->atomic_dq ? fa::dkdv_block_keys() : fa::dkdv2_block_keys();
+  a.nkt = (p->seqlen_k + kb - 1) / kb;
   a.nqt = (p->seqlen_q + fa::dq_block_rows() - 1) / fa::dq_block_rows();
   a.split = split;
   a.do_dq = p->atomic_dq ? 1 : 0;
@@ -233,8 +239,10 @@ int fa_bwd(const FaBwdParams* p) {
   a.score_vec = score_vec_ok(p->score, p->score_stride_b, p->score_stride_h, p->score_stride_q);
   const bool causal = p->is_causal != 0;
 
-  if ((st = launch_status(fa::launch_bwd_dkdv(a, p->head_dim, p->dtype, causal, s), "dkdv"))) return st;
-  if (!p->atomic_dq) {
+  if (p->atomic_dq) {
+    if ((st = launch_status(fa::launch_bwd_dkdv(a, p->head_dim, p->dtype, causal, s), "dkdv"))) return st;
+  } else {
+    if ((st = launch_status(fa::launch_bwd_dkdv2(a, p->head_dim, p->dtype, causal, s), "dkdv"))) return st;
     if ((st = launch_status(fa::launch_bwd_dq(a, p->head_dim, p->dtype, causal, s), "dq"))) return st;
   }
   return FA_OK;

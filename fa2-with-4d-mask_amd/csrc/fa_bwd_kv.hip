@@ -1,0 +1,460 @@
+// dK/dV of the FlashAttention-2 backward for gfx950 (MI355X), deterministic
+// path (dQ comes from the separate dQ kernel).  Restates the dK/dV part of the
+// reference's TileLang backward (python/fa2.py:181-302, 305-426): per key
+// block, over every query row of every query head of the GQA group,
+//   S  = Q K^T, dP = dO V^T            P  = exp2(S scale log2e - LSE2)
+//   dS = P (dP - Delta) scale          dV += P^T dO,  dK += dS^T Q
+// with dK/dV of the whole group accumulated in registers.
+//
+// Work decomposition: one workgroup of 4 waves (one per SIMD, 512 registers
+// each) per (128 keys, kv-head, batch[, head-group split]); wave w owns keys
+// 32 w .. 32 w + 31 and walks the query rows in steps of 32.  Per step:
+//   S, dP     32x32x16 MFMA, A = Q / dO rows (ds_read_b128 from LDS),
+//             B = K / V fragments resident in registers
+//   P, dS     fp32 VALU on the accumulators, packed to 16 bits in place
+//   dV^T, dK^T += dO^T P, Q^T dS   A = dO^T / Q^T (ds_read_b64_tr_b16),
+//             B = P / dS straight from the accumulator registers
+// The step loop is software-pipelined inside each wave: iteration j issues
+// the MFMAs of S/dP(j+1) and of dV/dK(j-1) interleaved with the VALU work of
+// P/dS(j), which depends on neither, so one wave keeps its SIMD's MFMA and
+// VALU pipes busy at the same time.
+//
+// Q/dO step tiles (32 rows) live in 4 LDS buffers (tiles j-1 and j+1 are read
+// in iteration j while j+2 is written), rows unpadded with one XOR swizzle of
+// their 16-byte chunks that keeps both the ds_read_b128 pattern (16 rows) and
+// the transpose-read pattern (4 rows x 4 chunks) conflict-free.  Tiles are
+// staged through registers: loaded with buffer loads (loop-invariant lane
+// offsets, tile base in scalar registers, rows past Tq zero-filled) two
+// iterations ahead and written one iteration ahead.  LSE and Delta*scale of
+// the tile's rows travel with it (LSE = +inf past Tq, so P = 0 there).
+#include "fa_common.h"
+#include "fa_kernels.h"
+
+namespace fa {
+namespace {
+
+constexpr int kKvWaves = 4;
+constexpr int kKvKeys = kKvWaves * 32;   // keys per workgroup
+constexpr int kStep = 32;                // query rows per step
+constexpr int kNBuf = 4;                 // LDS buffers of step tiles
+
+template <int N> struct IC { static constexpr int value = N; };
+
+// Chunk swizzle of a [32][D] 16-bit tile (16-byte chunks).  ds_read_b128 of
+// one chunk over 16 consecutive rows and ds_read_b64_tr_b16 over rows
+// 4 r0 .. 4 r0 + 3 x chunks 4 m .. 4 m + 3 both hit 64 distinct banks.
+template <int D> __device__ __forceinline__ int swz_q(int r) {
+  return D == 128 ? (((r & 3) << 2) | ((r >> 2) & 3)) : ((((r >> 1) & 1) << 2) | ((r >> 2) & 3));
+}
+
+__device__ __forceinline__ uint32_t opaque(uint32_t x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+__device__ __forceinline__ u32x4 lds_rd16(uint32_t addr) { return *(const FA_LDS u32x4*)(uintptr_t)addr; }
+__device__ __forceinline__ f32x4 lds_rdf4(uint32_t addr) { return *(const FA_LDS f32x4*)(uintptr_t)addr; }
+__device__ __forceinline__ s16x4 lds_rdtr(uint32_t addr) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((FA_LDS s16x4*)(uintptr_t)addr);
+}
+__device__ __forceinline__ void lds_wr16(uint32_t addr, u32x4 v) { *(FA_LDS u32x4*)(uintptr_t)addr = v; }
+__device__ __forceinline__ void lds_wrf(uint32_t addr, float v) { *(FA_LDS float*)(uintptr_t)addr = v; }
+__device__ __forceinline__ void lds_wr8(uint32_t addr, u32x2 v) { *(FA_LDS u32x2*)(uintptr_t)addr = v; }
+
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+template <typename T>
+__device__ __forceinline__ u32x2 pack4(float x0, float x1, float x2, float x3) {
+  typedef T T4 __attribute__((ext_vector_type(4)));
+  T4 v;
+  v[0] = (T)x0; v[1] = (T)x1; v[2] = (T)x2; v[3] = (T)x3;
+  return __builtin_bit_cast(u32x2, v);
+}
+
+template <typename T, int D, bool CAUSAL, bool MASK, bool SCORE>
+__global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) void dkdv2_kernel(const BwdArgs a) {
+  using V8 = typename Vec8<T>::type;
+  constexpr int DS = D / 16, NB = D / 32, CH = D / 8, ROWB = 2 * D;
+  constexpr int QTILE = kStep * ROWB;            // bytes of one Q (or dO) step tile
+  constexpr int DOFF = kNBuf * QTILE;            // dO tiles follow the Q tiles
+  constexpr int LOFF = 2 * kNBuf * QTILE;        // [buf][LSE | Delta*scale][32] fp32
+  constexpr int LBUF = 2 * kStep * 4;
+  constexpr int UQ = kStep * CH / (kKvWaves * 64);  // chunks per thread per tile
+  constexpr int OS = D + 8;                      // epilogue staging stride (elements)
+  static_assert(UQ >= 1, "tile split");
+  static_assert(DOFF + kNBuf * QTILE <= 65536, "buffer offsets fit the DS immediate");
+  static_assert(kKvWaves * 32 * OS * 2 <= 2 * kNBuf * QTILE, "epilogue staging fits");
+  __shared__ __attribute__((aligned(1024))) char smem[LOFF + kNBuf * LBUF];
+
+  // ---- which (batch, kv-head, split, key block) ------------------------------
+  const int nblk = a.B * a.Hk * a.nkt * a.split;
+  const int W = xcd_remap(blockIdx.x, nblk);
+  const int per_bk = a.split * a.nkt;
+  const int bk = W / per_bk;
+  const int rem = W - bk * per_bk;
+  const int sp = rem / a.nkt;
+  const int kt = rem - sp * a.nkt;        // ascending = most causal work first
+  const int b = bk / a.Hk, kvh = bk - b * a.Hk;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, hf = lane >> 5;
+  const int Tq = a.Tq, Tk = a.Tk;
+  const int kt0 = kt * kKvKeys, kw0 = kt0 + wave * 32;
+  const int key = kw0 + l32;              // this lane's key (column of S)
+  const int kc = min(key, Tk - 1);
+  // scale == 0: every kept logit is 0, i.e. P = exp2(-LSE2): a zero multiplier
+  const float c2 = a.zero_scale ? 0.f : a.scale_log2, scale = a.scale;
+
+  const T* __restrict__ kp = (const T*)a.k + b * a.ksb + kvh * a.ksh;
+  const T* __restrict__ vp = (const T*)a.v + b * a.vsb + kvh * a.vsh;
+
+  // K, V fragments (B operands of S = Q K^T, dP = dO V^T): lane holds
+  // K[key][16 ds + 8 hf .. +7].  Keys past Tk read row Tk-1: their dK/dV
+  // rows are never stored and nothing else depends on them.
+  V8 kf[DS], vf[DS];
+#pragma unroll
+  for (int ds = 0; ds < DS; ++ds) {
+    kf[ds] = as_vec8<T>(gload16(kp + (int64_t)kc * a.kst + ds * 16 + hf * 8));
+    vf[ds] = as_vec8<T>(gload16(vp + (int64_t)kc * a.vst + ds * 16 + hf * 8));
+  }
+
+  // ---- iteration space: (head of the group split, 32-row step) ---------------
+  const int gsz = a.G / a.split;
+  const int g0 = sp * gsz;
+  const int qstart = CAUSAL ? (kt0 / kStep) * kStep : 0;   // rows above the block are masked
+  const int nst = qstart < Tq ? (Tq - qstart + kStep - 1) / kStep : 0;
+  const int n = gsz * nst;
+
+  // ---- LDS addresses -----------------------------------------------------------
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(FA_LDS char*)smem;
+  // ds_read_b128 (A of S / dP): row l32, logical chunk 2 ds + hf.  dO: + DOFF.
+  uint32_t ab[DS];
+#pragma unroll
+  for (int ds = 0; ds < DS; ++ds) ab[ds] = opaque(lds0 + l32 * ROWB + (((2 * ds + hf) ^ swz_q<D>(l32)) * 16));
+  // transpose reads (A of dV^T / dK^T): rows 16 c + 4 hf + rr (+8 for hi),
+  // columns 32 nb + tr_col; the swizzle of those rows does not depend on c.
+  const int rr = (lane >> 2) & 3;
+  const int tr_col = ((lane >> 4) & 1) * 16 + (lane & 3) * 4;
+  uint32_t at[2][NB];
+#pragma unroll
+  for (int hi = 0; hi < 2; ++hi)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      const int row = 4 * hf + rr + 8 * hi, col = nb * 32 + tr_col;
+      at[hi][nb] = opaque(lds0 + row * ROWB + (((col >> 3) ^ swz_q<D>(row)) * 16) + (col & 7) * 2);
+    }
+  // LSE / Delta*scale of rows 8 gi + 4 hf .. +3
+  const uint32_t al = opaque(lds0 + LOFF + hf * 16);
+
+  // ---- tile staging ------------------------------------------------------------
+  // chunk u of thread t: tile row r = idx / CH, logical chunk c = idx % CH
+  // (idx = t + 256 u): coalesced rows in, swizzled position out.
+  uint32_t gq[UQ], gd[UQ], sw[UQ];
+#pragma unroll
+  for (int u = 0; u < UQ; ++u) {
+    const int idx = tid + u * kKvWaves * 64, r = idx / CH, c = idx % CH;
+    gq[u] = (uint32_t)(r * a.qst * 2 + c * 16);
+    gd[u] = (uint32_t)(r * a.dst * 2 + c * 16);
+    sw[u] = opaque(lds0 + r * ROWB + ((c ^ swz_q<D>(r)) * 16));
+  }
+  u32x4 stq[UQ], std_[UQ];
+  float stl = 0.f, std_l = 0.f;  // staged LSE / Delta of row l32 (wave 0), selected at store time
+  int st_rows = 0;           // valid rows of the staged tile
+  auto tile_h = [&](int it) __attribute__((always_inline)) { return kvh * a.G + g0 + it / max(nst, 1); };
+  auto tile_qs = [&](int it) __attribute__((always_inline)) { return qstart + (it % max(nst, 1)) * kStep; };
+  // Position of the next tile to load, advanced by one step per call (no
+  // divisions in the loop): head ld_h, first row ld_qs, running element
+  // offsets of Q, dO and of the LSE/Delta rows.
+  int ld_it = 0, ld_h = kvh * a.G + g0, ld_qs = qstart;
+  int64_t ld_qo = (int64_t)b * a.qsb + (int64_t)ld_h * a.qsh + (int64_t)qstart * a.qst;
+  int64_t ld_do = (int64_t)b * a.dsb + (int64_t)ld_h * a.dsh + (int64_t)qstart * a.dst;
+  int64_t ld_lo = ((int64_t)b * a.Hq + ld_h) * Tq + qstart;
+  auto load_next = [&]() __attribute__((always_inline)) {
+    const int rows = ld_it < n ? min(kStep, Tq - ld_qs) : 0;
+    const int64_t nq = rows > 0 ? (int64_t)(rows - 1) * a.qst * 2 + ROWB : 0;
+    const int64_t nd = rows > 0 ? (int64_t)(rows - 1) * a.dst * 2 + ROWB : 0;
+    const auto rq = __builtin_amdgcn_make_buffer_rsrc((void*)((const T*)a.q + ld_qo), (short)0, (int)nq, 0x00020000);
+    const auto rd = __builtin_amdgcn_make_buffer_rsrc((void*)((const T*)a.dout + ld_do), (short)0, (int)nd, 0x00020000);
+#pragma unroll
+    for (int u = 0; u < UQ; ++u) {
+      stq[u] = __builtin_amdgcn_raw_buffer_load_b128(rq, gq[u], 0, 0);
+      std_[u] = __builtin_amdgcn_raw_buffer_load_b128(rd, gd[u], 0, 0);
+    }
+    if (wave == 0) {  // lanes 0-31: LSE rows, 32-63: Delta rows (uniform descriptors, lane select)
+      const auto rl = __builtin_amdgcn_make_buffer_rsrc((void*)(a.lse + ld_lo), (short)0, rows * 4, 0x00020000);
+      const auto rdl = __builtin_amdgcn_make_buffer_rsrc((void*)(a.delta + ld_lo), (short)0, rows * 4, 0x00020000);
+      const uint32_t vo = (uint32_t)l32 * 4;
+      stl = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rl, vo, 0, 0));
+      std_l = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rdl, vo, 0, 0));
+    }
+    st_rows = rows;
+    // advance to the following tile
+    ++ld_it;
+    ld_qs += kStep;
+    ld_qo += (int64_t)kStep * a.qst;
+    ld_do += (int64_t)kStep * a.dst;
+    ld_lo += kStep;
+    if (ld_qs >= Tq) {
+      ++ld_h;
+      ld_qs = qstart;
+      ld_qo = (int64_t)b * a.qsb + (int64_t)ld_h * a.qsh + (int64_t)qstart * a.qst;
+      ld_do = (int64_t)b * a.dsb + (int64_t)ld_h * a.dsh + (int64_t)qstart * a.dst;
+      ld_lo = ((int64_t)b * a.Hq + ld_h) * Tq + qstart;
+    }
+  };
+  auto store_tile = [&](int buf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < UQ; ++u) {
+      lds_wr16(sw[u] + buf * QTILE, stq[u]);
+      lds_wr16(sw[u] + DOFF + buf * QTILE, std_[u]);
+    }
+    if (wave == 0) {
+      const bool ok = l32 < st_rows;
+      const float v = hf == 0 ? (ok ? stl : kPosInf) : (ok ? std_l * scale : 0.f);
+      lds_wrf(lds0 + LOFF + buf * LBUF + tid * 4, v);
+    }
+  };
+
+  // ---- mask / score of a step (lane's 16 query rows at its key) -----------------
+  uint32_t mreg[MASK ? 4 : 1];
+  float sreg[SCORE ? 16 : 1];
+  auto load_ms = [&](int it) __attribute__((always_inline)) {
+    if constexpr (MASK || SCORE) {
+      const int h = tile_h(min(it, max(n - 1, 0))), qs = tile_qs(min(it, max(n - 1, 0)));
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int q = min(qs + 8 * (i >> 2) + 4 * hf + (i & 3), Tq - 1);
+        if constexpr (MASK) {
+          const uint32_t m = a.mask[b * a.msb + h * a.msh + (int64_t)q * a.msq + kc] != 0;
+          if ((i & 3) == 0) mreg[i >> 2] = m; else mreg[i >> 2] |= m << (8 * (i & 3));
+        }
+        if constexpr (SCORE) sreg[i] = a.score[b * a.ssb + h * a.ssh + (int64_t)q * a.ssq + kc];
+      }
+    }
+  };
+
+  // ---- accumulators ---------------------------------------------------------------
+  f32x16 dkt[NB], dvt[NB];   // dK^T / dV^T [32 nb + 8 (i/4) + 4 hf + i%4][key]
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) { dkt[nb] = f32x16{}; dvt[nb] = f32x16{}; }
+  f32x16 sacc[2], pacc[2];   // S / dP of steps j (parity) ; lane: [q = 8 (i/4) + 4 hf + i%4][key]
+  V8 ppk[2][2], dspk[2][2];  // P / dS packed: [parity][c], k-slot (hf, t) <-> row 16 c + 4 hf + t%4 + 8 (t/4)
+#pragma unroll
+  for (int x = 0; x < 2; ++x) {
+    sacc[x] = f32x16{}; pacc[x] = f32x16{};
+#pragma unroll
+    for (int c = 0; c < 2; ++c) { ppk[x][c] = V8{}; dspk[x][c] = V8{}; }
+  }
+
+  // S/dP of step "it" (tile in buffer BUF) -> parity PAR; dV/dK of step it-2
+  // (buffer (BUF+2)%4, parity PAR) -- one interleaved MFMA stream, with the
+  // P/dS VALU work of step it-1 (parity PAR^1) threaded through it.
+  auto iter = [&](auto BUFc, int j) __attribute__((always_inline)) {
+    // j: step whose P/dS is computed now; S/dP of j+1; dV/dK of j-1
+    constexpr int BUF = decltype(BUFc)::value;          // buffer of step j
+    constexpr int BN1 = (BUF + 1) % kNBuf, BM1 = (BUF + kNBuf - 1) % kNBuf;
+    constexpr int PJ = BUF & 1, PN = PJ ^ 1;            // parities of j and j +- 1
+    const int h = tile_h(j), qs = tile_qs(j);
+    const bool edge = MASK || (CAUSAL && kw0 + 31 > qs);
+
+    // operand reads for the two MFMA streams, AHEAD ops ahead
+    auto rd_sd = [&](int t) __attribute__((always_inline)) -> u32x4 {   // t: ds = t/2, Q (even) / dO (odd)
+      return lds_rd16(ab[t >> 1] + (uint32_t)((t & 1) * DOFF + BN1 * QTILE));
+    };
+    auto rd_tr = [&](int t) __attribute__((always_inline)) -> V8 {       // t: c = t / (2 NB), nb, dO (even) / Q (odd)
+      const int c = t / (2 * NB), nb = (t / 2) % NB, isq = t & 1;
+      const uint32_t off = (uint32_t)((isq ? 0 : DOFF) + BM1 * QTILE + 16 * c * ROWB);
+      return cat_tr<T>(lds_rdtr(at[0][nb] + off), lds_rdtr(at[1][nb] + off));
+    };
+    constexpr int NOP = 2 * DS;                          // == 4 * NB: ops per stream
+    constexpr int AHEAD = 4;
+    u32x4 xs[AHEAD];
+    V8 xt[AHEAD];
+#pragma unroll
+    for (int t = 0; t < AHEAD; ++t) { xs[t] = rd_sd(t); xt[t] = rd_tr(t); }
+
+    // P / dS of step j, 4 rows (gi) at a time
+    auto valu_gi = [&](int gi) __attribute__((always_inline)) {
+      const f32x4 l4 = lds_rdf4(al + BUF * LBUF + gi * 32);
+      const f32x4 d4 = lds_rdf4(al + BUF * LBUF + kStep * 4 + gi * 32);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int i = gi * 4 + t;
+        float sv = sacc[PJ][i];
+        if constexpr (SCORE) sv += sreg[i];
+        float p = exp2_fast(fmaf(sv, c2, -l4[t]));
+        if (edge) {
+          const int q = qs + 8 * gi + 4 * hf + t;
+          bool keep = true;
+          if constexpr (CAUSAL) keep = key <= q;
+          if constexpr (MASK) keep = keep && ((mreg[gi] >> (8 * t)) & 0xffu) != 0;
+          p = keep ? p : 0.f;
+        }
+        sacc[PJ][i] = p;
+        pacc[PJ][i] = p * fmaf(pacc[PJ][i], scale, -d4[t]);
+      }
+      if (gi & 1) {
+        const int c = gi >> 1;
+        ppk[PJ][c] = pack8<T>(sacc[PJ][8 * c + 0], sacc[PJ][8 * c + 1], sacc[PJ][8 * c + 2], sacc[PJ][8 * c + 3],
+                              sacc[PJ][8 * c + 4], sacc[PJ][8 * c + 5], sacc[PJ][8 * c + 6], sacc[PJ][8 * c + 7]);
+        dspk[PJ][c] = pack8<T>(pacc[PJ][8 * c + 0], pacc[PJ][8 * c + 1], pacc[PJ][8 * c + 2], pacc[PJ][8 * c + 3],
+                               pacc[PJ][8 * c + 4], pacc[PJ][8 * c + 5], pacc[PJ][8 * c + 6], pacc[PJ][8 * c + 7]);
+      }
+    };
+    // Values first used in a later iteration would otherwise be sunk there by
+    // the optimiser: pinning them keeps each quarter's VALU work in its quarter.
+    auto pin_gi = [&](int gi) __attribute__((always_inline)) {
+      if (gi & 1) {
+        const int c = gi >> 1;
+        asm volatile("" : "+v"(ppk[PJ][c]), "+v"(dspk[PJ][c]));
+      } else {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) asm volatile("" : "+v"(sacc[PJ][gi * 4 + t]), "+v"(pacc[PJ][gi * 4 + t]));
+      }
+    };
+
+    // One scheduling region: AHEAD op pairs of operands prefetched, then per op
+    // pair two MFMAs, a share of the P/dS VALU work (4 rows per NOP/4 pairs,
+    // placed at the start of their quarter), and the reads AHEAD pairs ahead.
+    constexpr int QT = NOP / 4;
+    __builtin_amdgcn_sched_group_barrier(0x100, 3 * AHEAD, 0);
+#pragma unroll
+    for (int t = 0; t < NOP; ++t) {
+      if (t % QT == 0) valu_gi(t / QT);
+      // stream 1: S / dP of step j+1 (ds = t/2)
+      if ((t & 1) == 0) sacc[PN] = mfma32(as_vec8<T>(xs[t % AHEAD]), kf[t >> 1], (t >> 1) == 0 ? f32x16{} : sacc[PN]);
+      else pacc[PN] = mfma32(as_vec8<T>(xs[t % AHEAD]), vf[t >> 1], (t >> 1) == 0 ? f32x16{} : pacc[PN]);
+      // stream 2: dV / dK of step j-1 (c, nb)
+      {
+        const int c = t / (2 * NB), nb = (t / 2) % NB;
+        if ((t & 1) == 0) dvt[nb] = mfma32(xt[t % AHEAD], ppk[PN][c], dvt[nb]);
+        else dkt[nb] = mfma32(xt[t % AHEAD], dspk[PN][c], dkt[nb]);
+      }
+      if (t + AHEAD < NOP) { xs[t % AHEAD] = rd_sd(t + AHEAD); xt[t % AHEAD] = rd_tr(t + AHEAD); }
+      if (t % QT == QT - 1) pin_gi(t / QT);
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x402, 7, 0);
+      if (t + AHEAD < NOP) __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
+    }
+    // mask / score of step j+1 (registers of step j are consumed)
+    load_ms(j + 1);
+  };
+
+  // ---- prologue --------------------------------------------------------------------
+  // Buffer 3 is read as step -1 (with P = dS = 0): zero it.
+#pragma unroll
+  for (int u = 0; u < UQ; ++u) {
+    lds_wr16(sw[u] + 3 * QTILE, u32x4{0, 0, 0, 0});
+    lds_wr16(sw[u] + DOFF + 3 * QTILE, u32x4{0, 0, 0, 0});
+  }
+  load_next(); store_tile(0);   // tile 0
+  load_next(); store_tile(1);   // tile 1
+  load_next();                  // tile 2 staged
+  load_ms(0);
+  lds_barrier();
+  // S / dP of step 0 (parity 0)
+#pragma unroll
+  for (int ds = 0; ds < DS; ++ds) {
+    sacc[0] = mfma32(as_vec8<T>(lds_rd16(ab[ds])), kf[ds], ds == 0 ? f32x16{} : sacc[0]);
+    pacc[0] = mfma32(as_vec8<T>(lds_rd16(ab[ds] + DOFF)), vf[ds], ds == 0 ? f32x16{} : pacc[0]);
+  }
+
+  // ---- main loop: iteration j computes P/dS(j), S/dP(j+1), dV/dK(j-1) ---------------
+  // j runs over [0, n4) with n4 = n + 1 rounded up to a multiple of 4: the
+  // iterations past n - 1 work on zero tiles whose rows carry LSE = +inf, so
+  // their P and dS are exactly 0 and they add nothing, while iteration n
+  // contributes dV/dK(n-1).  Four copies of the body with static buffers and
+  // a single loop exit keep the accumulators in fixed registers.
+  auto step = [&](auto BUFc, int j) __attribute__((always_inline)) {
+    constexpr int BUF = decltype(BUFc)::value;
+    iter(BUFc, j);
+    store_tile((BUF + 2) % kNBuf);   // tile j+2 (loaded one iteration ago)
+    load_next();                     // tile j+3
+    lds_barrier();
+  };
+  int n4 = n > 0 ? (n + 4) & ~3 : 0;
+  asm volatile("" : "+s"(n4));   // hide the trip count (uniform: scalar register)
+  for (int j = 0; j < n4; j += 4) {
+    step(IC<0>{}, j);
+    step(IC<1>{}, j + 1);
+    step(IC<2>{}, j + 2);
+    step(IC<3>{}, j + 3);
+  }
+
+  // ---- epilogue: dK, dV (dV of a kv-head with a dead row is NaN) ---------------------
+  const bool dead = a.dead[b * a.Hk + kvh] != 0;
+  const float nanv = __builtin_nanf("");
+  lds_barrier();
+  if (a.split == 1) {
+    // stage [key][d] through LDS (wave-private rows), then coalesced 16-byte stores
+    T* stg = (T*)smem + wave * 32 * OS;
+    auto put = [&](const f32x16 (&acc)[NB], bool nan_out, T* dst, int64_t dstt) __attribute__((always_inline)) {
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int gi = 0; gi < 4; ++gi) {
+          const int d = nb * 32 + gi * 8 + hf * 4;
+          const u32x2 v = nan_out ? pack4<T>(nanv, nanv, nanv, nanv)
+                                  : pack4<T>(acc[nb][gi * 4 + 0], acc[nb][gi * 4 + 1], acc[nb][gi * 4 + 2], acc[nb][gi * 4 + 3]);
+          lds_write8(stg + l32 * OS + d, v);
+        }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+      for (int u = 0; u < 32 * CH / 64; ++u) {
+        const int idx = lane + u * 64, r = idx / CH, c = idx % CH;
+        if (kw0 + r < Tk) gstore16(dst + (int64_t)(kw0 + r) * dstt + c * 8, lds_read16(stg + r * OS + c * 8));
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    };
+    put(dkt, false, (T*)a.dk + b * a.dksb + kvh * a.dksh, a.dkst);
+    put(dvt, dead, (T*)a.dv + b * a.dvsb + kvh * a.dvsh, a.dvst);
+  } else {
+    // head-group split: fp32 slabs [split][B, Tk, Hk, D], summed in a fixed order later
+    const int64_t slab = (int64_t)sp * a.B * Tk * a.Hk * D;
+    if (key < Tk) {
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int gi = 0; gi < 4; ++gi) {
+          const int d = nb * 32 + gi * 8 + hf * 4;
+          const int64_t o = slab + (((int64_t)b * Tk + key) * a.Hk + kvh) * D + d;
+          f32x4 k4, v4;
+#pragma unroll
+          for (int t = 0; t < 4; ++t) { k4[t] = dkt[nb][gi * 4 + t]; v4[t] = dead ? nanv : dvt[nb][gi * 4 + t]; }
+          *(f32x4*)(a.dk_accum + o) = k4;
+          *(f32x4*)(a.dv_accum + o) = v4;
+        }
+    }
+  }
+}
+
+template <typename T, int D, bool CAUSAL>
+hipError_t launch_t(const BwdArgs& a, hipStream_t s) {
+  const dim3 grid((unsigned)(a.B * a.Hk * a.nkt * a.split)), block(kKvWaves * 64);
+  const bool m = a.mask != nullptr, sc = a.score != nullptr;
+  if (m && sc) hipLaunchKernelGGL((dkdv2_kernel<T, D, CAUSAL, true, true>), grid, block, 0, s, a);
+  else if (m) hipLaunchKernelGGL((dkdv2_kernel<T, D, CAUSAL, true, false>), grid, block, 0, s, a);
+  else if (sc) hipLaunchKernelGGL((dkdv2_kernel<T, D, CAUSAL, false, true>), grid, block, 0, s, a);
+  else hipLaunchKernelGGL((dkdv2_kernel<T, D, CAUSAL, false, false>), grid, block, 0, s, a);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+int dkdv2_block_keys() { return kKvKeys; }
+
+hipError_t launch_bwd_dkdv2(const BwdArgs& a, int D, int dtype, bool causal, hipStream_t s) {
+  if (dtype == 0) {
+    if (D == 128) return causal ? launch_t<bf16, 128, true>(a, s) : launch_t<bf16, 128, false>(a, s);
+    if (D == 64) return causal ? launch_t<bf16, 64, true>(a, s) : launch_t<bf16, 64, false>(a, s);
+  } else {
+    if (D == 128) return causal ? launch_t<f16, 128, true>(a, s) : launch_t<f16, 128, false>(a, s);
+    if (D == 64) return causal ? launch_t<f16, 64, true>(a, s) : launch_t<f16, 64, false>(a, s);
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace fa

@@ -62,6 +62,9 @@ hipError_t launch_fwd(const FwdArgs& a, int D, int dtype, bool causal, hipStream
 hipError_t launch_preprocess(const PreArgs& a, int D, int dtype, hipStream_t s);
 hipError_t launch_bwd_dkdv(const BwdArgs& a, int D, int dtype, bool causal, hipStream_t s);
 hipError_t launch_bwd_dq(const BwdArgs& a, int D, int dtype, bool causal, hipStream_t s);
+// dK/dV of the deterministic path (no dQ), 4 waves x 32 keys per workgroup.
+hipError_t launch_bwd_dkdv2(const BwdArgs& a, int D, int dtype, bool causal, hipStream_t s);
+int dkdv2_block_keys();
 hipError_t launch_convert(const CvtArgs& a, int dtype, hipStream_t s);
 
 }  // namespace fa
