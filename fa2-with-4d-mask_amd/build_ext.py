@@ -24,6 +24,9 @@ BUILD = HERE / "_build"
 LIBDIR = HERE / "tilelang_fa2_4d_mask" / "_lib"
 LIB = LIBDIR / "libfa2_4d_mask.so"
 SOURCES = ["fa_fwd.hip", "fa_bwd.hip", "fa_bwd_kv.hip", "fa_api.cpp"]
+# Per-file extra flags.  fa_bwd_kv.hip keeps its dK/dV accumulators in AGPRs
+# through inline asm and wants every other MFMA result in VGPRs (read by VALU).
+EXTRA_FLAGS = {"fa_bwd_kv.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 ARCH = "gfx950"
 
 
@@ -66,7 +69,7 @@ def build(jobs: int = 4, verbose: bool = False) -> Path:
 
     def obj(src: str) -> Path:
         o = BUILD / (Path(src).stem + ".o")
-        _run([cc, *flags, "-c", str(CSRC / src), "-o", str(o)], verbose)
+        _run([cc, *flags, *EXTRA_FLAGS.get(src, []), "-c", str(CSRC / src), "-o", str(o)], verbose)
         return o
 
     with ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:

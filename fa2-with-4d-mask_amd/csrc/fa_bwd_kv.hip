@@ -4,6 +4,8 @@
 // block, over every query row of every query head of the GQA group,
 //   S  = Q K^T, dP = dO V^T            P  = exp2(S scale log2e - LSE2)
 //   dS = P (dP - Delta) scale          dV += P^T dO,  dK += dS^T Q
+// (dP - Delta comes out of the MFMA chain started from -Delta, and the factor
+// scale is applied once to dK at the end.)
 // with dK/dV of the whole group accumulated in registers.
 //
 // Work decomposition: one workgroup of 4 waves (one per SIMD, 512 registers
@@ -24,9 +26,9 @@
 // their 16-byte chunks that keeps both the ds_read_b128 pattern (16 rows) and
 // the transpose-read pattern (4 rows x 4 chunks) conflict-free.  Tiles are
 // staged through registers: loaded with buffer loads (loop-invariant lane
-// offsets, tile base in scalar registers, rows past Tq zero-filled) two
-// iterations ahead and written one iteration ahead.  LSE and Delta*scale of
-// the tile's rows travel with it (LSE = +inf past Tq, so P = 0 there).
+// offsets, tile base in scalar registers, rows past Tq zero-filled) and
+// written into LDS one iteration later, both at the start of an iteration.  LSE and -Delta of the
+// tile's rows travel with it (LSE = +inf past Tq, so P = 0 there).
 #include "fa_common.h"
 #include "fa_kernels.h"
 
@@ -66,6 +68,19 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_sched_barrier(0);
 }
 
+// dK/dV accumulation: MFMA with the accumulator pinned to AGPRs.  The S/dP
+// MFMAs (compiler builtins, built in VGPR form for this file) then leave
+// their results in VGPRs, where the P/dS VALU work reads them without copies.
+// Operands: A from an LDS read (the compiler places the wait for it before
+// the asm), B packed one iteration earlier; each accumulator is touched only
+// by these MFMAs, NB ops apart.
+__device__ __forceinline__ void mfma_acc(f32x16& acc, bf16x8 a, bf16x8 b) {
+  asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+__device__ __forceinline__ void mfma_acc(f32x16& acc, f16x8 a, f16x8 b) {
+  asm volatile("v_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+
 template <typename T>
 __device__ __forceinline__ u32x2 pack4(float x0, float x1, float x2, float x3) {
   typedef T T4 __attribute__((ext_vector_type(4)));
@@ -80,7 +95,7 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
   constexpr int DS = D / 16, NB = D / 32, CH = D / 8, ROWB = 2 * D;
   constexpr int QTILE = kStep * ROWB;            // bytes of one Q (or dO) step tile
   constexpr int DOFF = kNBuf * QTILE;            // dO tiles follow the Q tiles
-  constexpr int LOFF = 2 * kNBuf * QTILE;        // [buf][LSE | Delta*scale][32] fp32
+  constexpr int LOFF = 2 * kNBuf * QTILE;        // [buf][LSE | -Delta][32] fp32
   constexpr int LBUF = 2 * kStep * 4;
   constexpr int UQ = kStep * CH / (kKvWaves * 64);  // chunks per thread per tile
   constexpr int OS = D + 8;                      // epilogue staging stride (elements)
@@ -146,7 +161,7 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
       const int row = 4 * hf + rr + 8 * hi, col = nb * 32 + tr_col;
       at[hi][nb] = opaque(lds0 + row * ROWB + (((col >> 3) ^ swz_q<D>(row)) * 16) + (col & 7) * 2);
     }
-  // LSE / Delta*scale of rows 8 gi + 4 hf .. +3
+  // LSE / -Delta of rows 8 gi + 4 hf .. +3
   const uint32_t al = opaque(lds0 + LOFF + hf * 16);
 
   // ---- tile staging ------------------------------------------------------------
@@ -213,7 +228,7 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
     }
     if (wave == 0) {
       const bool ok = l32 < st_rows;
-      const float v = hf == 0 ? (ok ? stl : kPosInf) : (ok ? std_l * scale : 0.f);
+      const float v = hf == 0 ? (ok ? stl : kPosInf) : (ok ? -std_l : 0.f);
       lds_wrf(lds0 + LOFF + buf * LBUF + tid * 4, v);
     }
   };
@@ -270,74 +285,73 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
       return cat_tr<T>(lds_rdtr(at[0][nb] + off), lds_rdtr(at[1][nb] + off));
     };
     constexpr int NOP = 2 * DS;                          // == 4 * NB: ops per stream
+    // -Delta of the rows of step j+1: initial accumulator of its dP chain
+    f32x16 nd_next;
+#pragma unroll
+    for (int gi = 0; gi < 4; ++gi) {
+      const f32x4 d4 = lds_rdf4(al + BN1 * LBUF + kStep * 4 + gi * 32);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) nd_next[gi * 4 + t] = d4[t];
+    }
     constexpr int AHEAD = 4;
     u32x4 xs[AHEAD];
     V8 xt[AHEAD];
 #pragma unroll
     for (int t = 0; t < AHEAD; ++t) { xs[t] = rd_sd(t); xt[t] = rd_tr(t); }
 
-    // P / dS of step j, 4 rows (gi) at a time
-    auto valu_gi = [&](int gi) __attribute__((always_inline)) {
-      const f32x4 l4 = lds_rdf4(al + BUF * LBUF + gi * 32);
-      const f32x4 d4 = lds_rdf4(al + BUF * LBUF + kStep * 4 + gi * 32);
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const int i = gi * 4 + t;
-        float sv = sacc[PJ][i];
-        if constexpr (SCORE) sv += sreg[i];
-        float p = exp2_fast(fmaf(sv, c2, -l4[t]));
-        if (edge) {
-          const int q = qs + 8 * gi + 4 * hf + t;
-          bool keep = true;
-          if constexpr (CAUSAL) keep = key <= q;
-          if constexpr (MASK) keep = keep && ((mreg[gi] >> (8 * t)) & 0xffu) != 0;
-          p = keep ? p : 0.f;
-        }
-        sacc[PJ][i] = p;
-        pacc[PJ][i] = p * fmaf(pacc[PJ][i], scale, -d4[t]);
+    // P / dS of step j, element by element (lane entry i: row 8 (i/4) + 4 hf + i%4)
+    f32x4 l4[2];                           // LSE of rows group gi (double-buffered by gi parity)
+    auto read_l = [&](int gi) __attribute__((always_inline)) { l4[gi & 1] = lds_rdf4(al + BUF * LBUF + gi * 32); };
+    auto elem = [&](int i) __attribute__((always_inline)) {
+      const int gi = i >> 2, t = i & 3;
+      float sv = sacc[PJ][i];
+      if constexpr (SCORE) sv += sreg[i];
+      float p = exp2_fast(fmaf(sv, c2, -l4[gi & 1][t]));
+      if (edge) {
+        const int q = qs + 8 * gi + 4 * hf + t;
+        bool keep = true;
+        if constexpr (CAUSAL) keep = key <= q;
+        if constexpr (MASK) keep = keep && ((mreg[gi] >> (8 * t)) & 0xffu) != 0;
+        p = keep ? p : 0.f;
       }
-      if (gi & 1) {
-        const int c = gi >> 1;
+      sacc[PJ][i] = p;
+      pacc[PJ][i] = p * pacc[PJ][i];   // P (dP - Delta); the factor scale goes into dK
+      if ((i & 7) == 7) {
+        const int c = i >> 3;
         ppk[PJ][c] = pack8<T>(sacc[PJ][8 * c + 0], sacc[PJ][8 * c + 1], sacc[PJ][8 * c + 2], sacc[PJ][8 * c + 3],
                               sacc[PJ][8 * c + 4], sacc[PJ][8 * c + 5], sacc[PJ][8 * c + 6], sacc[PJ][8 * c + 7]);
         dspk[PJ][c] = pack8<T>(pacc[PJ][8 * c + 0], pacc[PJ][8 * c + 1], pacc[PJ][8 * c + 2], pacc[PJ][8 * c + 3],
                                pacc[PJ][8 * c + 4], pacc[PJ][8 * c + 5], pacc[PJ][8 * c + 6], pacc[PJ][8 * c + 7]);
-      }
-    };
-    // Values first used in a later iteration would otherwise be sunk there by
-    // the optimiser: pinning them keeps each quarter's VALU work in its quarter.
-    auto pin_gi = [&](int gi) __attribute__((always_inline)) {
-      if (gi & 1) {
-        const int c = gi >> 1;
         asm volatile("" : "+v"(ppk[PJ][c]), "+v"(dspk[PJ][c]));
       } else {
-#pragma unroll
-        for (int t = 0; t < 4; ++t) asm volatile("" : "+v"(sacc[PJ][gi * 4 + t]), "+v"(pacc[PJ][gi * 4 + t]));
+        // keep the element's work in its slot (its result is first used later)
+        asm volatile("" : "+v"(sacc[PJ][i]), "+v"(pacc[PJ][i]));
       }
     };
 
-    // One scheduling region: AHEAD op pairs of operands prefetched, then per op
-    // pair two MFMAs, a share of the P/dS VALU work (4 rows per NOP/4 pairs,
-    // placed at the start of their quarter), and the reads AHEAD pairs ahead.
-    constexpr int QT = NOP / 4;
-    __builtin_amdgcn_sched_group_barrier(0x100, 3 * AHEAD, 0);
+    // Slot t (own scheduling region): MFMAs of op t of both streams, the
+    // operand reads of op t + AHEAD, and 16/NOP elements of P/dS.
+    constexpr int EPS = 16 / NOP;          // elements per slot
+    read_l(0);
 #pragma unroll
     for (int t = 0; t < NOP; ++t) {
-      if (t % QT == 0) valu_gi(t / QT);
       // stream 1: S / dP of step j+1 (ds = t/2)
       if ((t & 1) == 0) sacc[PN] = mfma32(as_vec8<T>(xs[t % AHEAD]), kf[t >> 1], (t >> 1) == 0 ? f32x16{} : sacc[PN]);
-      else pacc[PN] = mfma32(as_vec8<T>(xs[t % AHEAD]), vf[t >> 1], (t >> 1) == 0 ? f32x16{} : pacc[PN]);
+      else pacc[PN] = mfma32(as_vec8<T>(xs[t % AHEAD]), vf[t >> 1], (t >> 1) == 0 ? nd_next : pacc[PN]);
       // stream 2: dV / dK of step j-1 (c, nb)
       {
         const int c = t / (2 * NB), nb = (t / 2) % NB;
-        if ((t & 1) == 0) dvt[nb] = mfma32(xt[t % AHEAD], ppk[PN][c], dvt[nb]);
-        else dkt[nb] = mfma32(xt[t % AHEAD], dspk[PN][c], dkt[nb]);
+        if ((t & 1) == 0) mfma_acc(dvt[nb], xt[t % AHEAD], ppk[PN][c]);
+        else mfma_acc(dkt[nb], xt[t % AHEAD], dspk[PN][c]);
       }
       if (t + AHEAD < NOP) { xs[t % AHEAD] = rd_sd(t + AHEAD); xt[t % AHEAD] = rd_tr(t + AHEAD); }
-      if (t % QT == QT - 1) pin_gi(t / QT);
-      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-      __builtin_amdgcn_sched_group_barrier(0x402, 7, 0);
-      if (t + AHEAD < NOP) __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
+#pragma unroll
+      for (int e = 0; e < EPS; ++e) {
+        const int i = t * EPS + e;
+        if ((i & 3) == 1 && i + 3 < 16) read_l((i >> 2) + 1);   // LSE of the next row group
+        elem(i);
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
     // mask / score of step j+1 (registers of step j are consumed)
     load_ms(j + 1);
@@ -355,11 +369,18 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
   load_next();                  // tile 2 staged
   load_ms(0);
   lds_barrier();
-  // S / dP of step 0 (parity 0)
+  // S / dP of step 0 (parity 0); the dP chain starts from -Delta
+  f32x16 nd0;
+#pragma unroll
+  for (int gi = 0; gi < 4; ++gi) {
+    const f32x4 d4 = lds_rdf4(al + kStep * 4 + gi * 32);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) nd0[gi * 4 + t] = d4[t];
+  }
 #pragma unroll
   for (int ds = 0; ds < DS; ++ds) {
     sacc[0] = mfma32(as_vec8<T>(lds_rd16(ab[ds])), kf[ds], ds == 0 ? f32x16{} : sacc[0]);
-    pacc[0] = mfma32(as_vec8<T>(lds_rd16(ab[ds] + DOFF)), vf[ds], ds == 0 ? f32x16{} : pacc[0]);
+    pacc[0] = mfma32(as_vec8<T>(lds_rd16(ab[ds] + DOFF)), vf[ds], ds == 0 ? nd0 : pacc[0]);
   }
 
   // ---- main loop: iteration j computes P/dS(j), S/dP(j+1), dV/dK(j-1) ---------------
@@ -368,11 +389,14 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
   // their P and dS are exactly 0 and they add nothing, while iteration n
   // contributes dV/dK(n-1).  Four copies of the body with static buffers and
   // a single loop exit keep the accumulators in fixed registers.
+  // Staging first: buffer (j+2)%4 is not read in iteration j, so tile j+2
+  // (loaded during iteration j-1) is written while the MFMA stream runs, and
+  // the loads of tile j+3 get a whole iteration of latency.
   auto step = [&](auto BUFc, int j) __attribute__((always_inline)) {
     constexpr int BUF = decltype(BUFc)::value;
-    iter(BUFc, j);
-    store_tile((BUF + 2) % kNBuf);   // tile j+2 (loaded one iteration ago)
+    store_tile((BUF + 2) % kNBuf);   // tile j+2
     load_next();                     // tile j+3
+    iter(BUFc, j);
     lds_barrier();
   };
   int n4 = n > 0 ? (n + 4) & ~3 : 0;
@@ -383,6 +407,10 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
     step(IC<2>{}, j + 2);
     step(IC<3>{}, j + 3);
   }
+
+  // The compiler does not see the asm MFMAs as such: give their last results
+  // the MFMA-to-VALU wait states before the epilogue reads the accumulators.
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
 
   // ---- epilogue: dK, dV (dV of a kv-head with a dead row is NaN) ---------------------
   const bool dead = a.dead[b * a.Hk + kvh] != 0;
@@ -409,6 +437,8 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
       }
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     };
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) dkt[nb] *= scale;
     put(dkt, false, (T*)a.dk + b * a.dksb + kvh * a.dksh, a.dkst);
     put(dvt, dead, (T*)a.dv + b * a.dvsb + kvh * a.dvsh, a.dvst);
   } else {
@@ -423,7 +453,7 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
           const int64_t o = slab + (((int64_t)b * Tk + key) * a.Hk + kvh) * D + d;
           f32x4 k4, v4;
 #pragma unroll
-          for (int t = 0; t < 4; ++t) { k4[t] = dkt[nb][gi * 4 + t]; v4[t] = dead ? nanv : dvt[nb][gi * 4 + t]; }
+          for (int t = 0; t < 4; ++t) { k4[t] = dkt[nb][gi * 4 + t] * scale; v4[t] = dead ? nanv : dvt[nb][gi * 4 + t]; }
           *(f32x4*)(a.dk_accum + o) = k4;
           *(f32x4*)(a.dv_accum + o) = v4;
         }
