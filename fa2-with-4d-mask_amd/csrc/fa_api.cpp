@@ -90,6 +90,18 @@ int choose_split(const FaBwdParams* p) {
   return split;
 }
 
+// Deterministic path: 16-bit dS tiles of every stored 32x32 block (causal:
+// blocks on or below the diagonal), when they fit the caller's limit.
+int64_t ds_elems(const FaBwdParams* p) {
+  if (p->atomic_dq) return 0;
+  const int64_t limit = p->ds_limit_bytes == 0 ? (int64_t)8 << 30 : p->ds_limit_bytes;
+  if (limit < 0) return 0;
+  const int64_t nq32 = (p->seqlen_q + 31) / 32, nk32 = (p->seqlen_k + 31) / 32;
+  const int64_t plane = fa::ds_row(nq32, nk32, p->is_causal != 0);
+  const int64_t elems = (int64_t)p->batch * p->heads_q * plane * 1024;
+  return 2 * elems <= limit ? elems : 0;
+}
+
 void fill_scales(float scale, float* scale_log2_fwd, float* qsign, int* zero, float* scale_log2_bwd) {
   *zero = scale == 0.f;
   *qsign = scale < 0.f ? -1.f : 1.f;
@@ -155,9 +167,15 @@ static int check_bwd(const FaBwdParams* p, int split) {
   if ((st = check_operand("dk", p->dk, p->dk_stride_b, p->dk_stride_t, p->dk_stride_h))) return st;
   if ((st = check_operand("dv", p->dv, p->dv_stride_b, p->dv_stride_t, p->dv_stride_h))) return st;
   // The dK/dV kernel stages Q/dO tiles with 32-bit buffer offsets (32 rows of a tile).
-  if (p->q_stride_t < 0 || p->q_stride_t >= (1LL << 24) || p->do_stride_t < 0 || p->do_stride_t >= (1LL << 24))
-    return fail(FA_ERR_STRIDE, "q/dout time strides (%lld, %lld) must lie in [0, 2^24) elements",
-                (long long)p->q_stride_t, (long long)p->do_stride_t);
+  // The dQ kernel stages K tiles the same way.
+  if (p->q_stride_t < 0 || p->q_stride_t >= (1LL << 24) || p->do_stride_t < 0 || p->do_stride_t >= (1LL << 24) ||
+      p->k_stride_t < 0 || p->k_stride_t >= (1LL << 24))
+    return fail(FA_ERR_STRIDE, "q/dout/k time strides (%lld, %lld, %lld) must lie in [0, 2^24) elements",
+                (long long)p->q_stride_t, (long long)p->do_stride_t, (long long)p->k_stride_t);
+  // ... and reaches a tile's first row of Q / dO with a 32-bit scalar byte offset.
+  const int64_t qspan = (int64_t)(p->seqlen_q + 32) * 2 * (p->q_stride_t > p->do_stride_t ? p->q_stride_t : p->do_stride_t);
+  if (qspan >= (1LL << 32))
+    return fail(FA_ERR_STRIDE, "seqlen_q * q/dout time stride too large (%lld bytes, the limit is 2^32)", (long long)qspan);
   if (!p->lse) return fail(FA_ERR_NULL, "lse is NULL");
   if (!p->delta) return fail(FA_ERR_NULL, "delta is NULL");
   if (!p->dead_flags) return fail(FA_ERR_NULL, "dead_flags is NULL");
@@ -169,6 +187,8 @@ static int check_bwd(const FaBwdParams* p, int split) {
     return fail(FA_ERR_WORKSPACE, "kv_split %d needs dk_accum and dv_accum", split);
   if (split > 1 && (!aligned16(p->dk_accum) || !aligned16(p->dv_accum)))
     return fail(FA_ERR_STRIDE, "dk_accum/dv_accum must be 16-byte aligned");
+  if (ds_elems(p) > 0 && !p->ds_tiles) return fail(FA_ERR_WORKSPACE, "deterministic dQ needs ds_tiles");
+  if (ds_elems(p) > 0 && !aligned16(p->ds_tiles)) return fail(FA_ERR_STRIDE, "ds_tiles must be 16-byte aligned");
   return check_mask_score(p->mask, p->mask_stride_b, p->mask_stride_h, p->mask_stride_q, p->score,
                           p->score_stride_b, p->score_stride_h, p->score_stride_q);
 }
@@ -187,6 +207,7 @@ int fa_bwd_plan(const FaBwdParams* p, FaBwdPlan* plan) {
   // path: one slab per split, fully overwritten (no zeroing needed).
   plan->dkv_accum_elems =
       split > 1 ? (int64_t)(p->atomic_dq ? 1 : split) * p->batch * p->seqlen_k * p->heads_k * p->head_dim : 0;
+  plan->ds_elems = ds_elems(p);
   return FA_OK;
 }
 
@@ -242,8 +263,18 @@ int fa_bwd(const FaBwdParams* p) {
   if (p->atomic_dq) {
     if ((st = launch_status(fa::launch_bwd_dkdv(a, p->head_dim, p->dtype, causal, s), "dkdv"))) return st;
   } else {
+    const bool via_ds = ds_elems(p) > 0;
+    a.nq32 = (p->seqlen_q + 31) / 32;
+    a.nk32 = (p->seqlen_k + 31) / 32;
+    a.ds = via_ds ? p->ds_tiles : nullptr;
+    a.ds_plane = fa::ds_row(a.nq32, a.nk32, causal);
     if ((st = launch_status(fa::launch_bwd_dkdv2(a, p->head_dim, p->dtype, causal, s), "dkdv"))) return st;
-    if ((st = launch_status(fa::launch_bwd_dq(a, p->head_dim, p->dtype, causal, s), "dq"))) return st;
+    if (via_ds) {
+      a.nqt = (p->seqlen_q + fa::dq_ds_block_rows() - 1) / fa::dq_ds_block_rows();
+      if ((st = launch_status(fa::launch_bwd_dq_ds(a, p->head_dim, p->dtype, causal, s), "dq"))) return st;
+    } else {
+      if ((st = launch_status(fa::launch_bwd_dq(a, p->head_dim, p->dtype, causal, s), "dq"))) return st;
+    }
   }
   return FA_OK;
 }

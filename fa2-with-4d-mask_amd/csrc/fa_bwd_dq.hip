@@ -1,0 +1,233 @@
+// dQ of the deterministic FlashAttention-2 backward for gfx950 (MI355X), from
+// the dS tiles the dK/dV kernel writes:
+//   dQ = scale * dS K,   dS = P (dP - Delta) per (query row, key)
+// which is the dQ part of the reference's TileLang backward
+// (python/fa2.py:181-302, 305-426: dq = dS K accumulated over key blocks).
+// Storing dS (16-bit, the precision the dQ MFMA consumes anyway) replaces the
+// second evaluation of S, P and dP that a separate dQ kernel would need: this
+// kernel is one streaming pass over the dS tiles with a small GEMM on top.
+//
+// dS tile (b, h, s, kb): 32 keys x 32 query rows, row "key" of 64 bytes whose
+// 16-bit entries hold, at position p, query row
+//   perm(p) = 16 (p / 16) + 4 ((p / 8) % 2) + 8 ((p / 4) % 2) + p % 4
+// (the order in which the dK/dV kernel's lanes hold them).  ds_read_b64_tr_b16
+// over that [key][p] tile yields the B operand of dQ^T = K^T dS^T with lane
+// l = position p directly, so perm only matters when dQ rows are stored.
+//
+// Work decomposition: one workgroup of 4 waves per (256 query rows, head,
+// batch); wave w owns query steps 8 qb + 2 w, + 1 (64 rows) and walks the key
+// steps of 32.  Per step the workgroup stages one K tile (shared, XOR-swizzled
+// for the transpose reads) and each wave its two dS tiles (private) through
+// registers into LDS, two steps ahead of use; the kernel is bound by the HBM
+// reads of the dS tiles.
+#include "fa_common.h"
+#include "fa_kernels.h"
+#include "fa_pipe.h"
+
+namespace fa {
+namespace {
+
+using namespace pipe;
+
+constexpr int kDqWaves = 4;
+constexpr int kDqSteps = 2;                           // 32-row query steps per wave
+constexpr int kDqRows = kDqWaves * kDqSteps * 32;     // query rows per workgroup
+
+template <typename T, int D, bool CAUSAL>
+__global__ __launch_bounds__(kDqWaves * 64, 2) void dq_ds_kernel(const BwdArgs a) {
+  using V8 = typename Vec8<T>::type;
+  constexpr int NB = D / 32, CH = D / 8, ROWB = 2 * D;
+  constexpr int KTILE = 32 * ROWB;                   // bytes of one K step tile
+  constexpr int DSW = kDqSteps * 2048;               // dS bytes of one wave and step
+  constexpr int BUFB = KTILE + kDqWaves * DSW;       // one LDS buffer
+  constexpr int UK = 32 * CH / (kDqWaves * 64);      // K chunks per thread
+  constexpr int UD = DSW / (64 * 16);                // dS chunks per lane
+  constexpr int OS = D + 8;                          // epilogue staging stride (elements)
+  static_assert(UK >= 1 && UD >= 1, "tile split");
+  static_assert(kDqWaves * 32 * OS * 2 <= 2 * BUFB, "epilogue staging fits");
+  __shared__ __attribute__((aligned(1024))) char smem[2 * BUFB];
+
+  // ---- which (batch, head, 256-row block) ----------------------------------------
+  // Logical order: kv-head major (the heads of a group share K in L2), longest
+  // causal blocks first.
+  const int nqb = a.nqt;
+  const int nblk = a.B * a.Hq * nqb;
+  const int W = xcd_remap(blockIdx.x, nblk);
+  const int per_kv = a.G * nqb;
+  const int bk = W / per_kv;
+  const int rem = W - bk * per_kv;
+  const int qb_rev = rem / a.G;
+  const int g = rem - qb_rev * a.G;
+  const int qb = nqb - 1 - qb_rev;
+  const int b = bk / a.Hk, kvh = bk - b * a.Hk;
+  const int h = kvh * a.G + g;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, hf = lane >> 5;
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
+  const int Tq = a.Tq, Tk = a.Tk, nk32 = a.nk32, nq32 = a.nq32;
+  const int s0 = qb * (kDqRows / 32) + wv * kDqSteps;          // this wave's first query step
+  const int s_last = min(qb * (kDqRows / 32) + kDqRows / 32, nq32) - 1;
+  const int nstep = CAUSAL ? min(s_last + 1, nk32) : nk32;       // key steps of the workgroup
+  const int nstep2 = (nstep + 1) & ~1;
+
+  // ---- LDS addresses ---------------------------------------------------------------
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(FA_LDS char*)smem;
+  const int rr = (lane >> 2) & 3;
+  const int tr_col = ((lane >> 4) & 1) * 16 + (lane & 3) * 4;
+  // A = K^T (transpose reads of the swizzled K tile), rows 4 hf + rr (+8), key chunk c adds 16 rows
+  uint32_t at[2][NB];
+#pragma unroll
+  for (int hi = 0; hi < 2; ++hi)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      const int row = 4 * hf + rr + 8 * hi, col = nb * 32 + tr_col;
+      at[hi][nb] = opaque(lds0 + row * ROWB + (((col >> 3) ^ swz_q<D>(row)) * 16) + (col & 7) * 2);
+    }
+  // B = dS^T (transpose reads of the wave's [key][p] tiles, 64-byte rows, unswizzled)
+  uint32_t bd[2];
+#pragma unroll
+  for (int hi = 0; hi < 2; ++hi) bd[hi] = opaque(lds0 + KTILE + wv * DSW + (4 * hf + rr + 8 * hi) * 64 + tr_col * 2);
+
+  // ---- staging -----------------------------------------------------------------------
+  const T* __restrict__ kbase = (const T*)a.k + b * a.ksb + kvh * a.ksh;
+  uint32_t gk[UK], swk[UK];
+#pragma unroll
+  for (int u = 0; u < UK; ++u) {
+    const int idx = tid + u * kDqWaves * 64, r = idx / CH, c = idx % CH;
+    gk[u] = (uint32_t)(r * a.kst * 2 + c * 16);
+    swk[u] = opaque(lds0 + r * ROWB + ((c ^ swz_q<D>(r)) * 16));
+  }
+  const uint32_t sd = opaque(lds0 + KTILE + wv * DSW + lane * 16);   // + 1024 u
+  const uint16_t* __restrict__ dsp = (const uint16_t*)a.ds;
+  const int64_t plane = ((int64_t)b * a.Hq + h) * a.ds_plane;
+  int64_t row0[kDqSteps];
+#pragma unroll
+  for (int i = 0; i < kDqSteps; ++i) row0[i] = plane + ds_row(s0 + i, nk32, CAUSAL);
+
+  u32x4 stk[2][UK], std_[2][UD];
+  // Tile kb into staging set S (keys past Tk and dS tiles outside the stored
+  // set load as zeros).
+  auto load = [&](auto Sc, int kb) __attribute__((always_inline)) {
+    constexpr int S = decltype(Sc)::value;
+    const int rows = kb < nstep ? min(32, Tk - kb * 32) : 0;
+    const int nrec = rows > 0 ? (int)((int64_t)(rows - 1) * a.kst * 2 + ROWB) : 0;
+    const auto rk = __builtin_amdgcn_make_buffer_rsrc((void*)(kbase + (int64_t)kb * 32 * a.kst), (short)0, nrec, 0x00020000);
+#pragma unroll
+    for (int u = 0; u < UK; ++u) stk[S][u] = __builtin_amdgcn_raw_buffer_load_b128(rk, gk[u], 0, 0);
+#pragma unroll
+    for (int i = 0; i < kDqSteps; ++i) {
+      const int s = s0 + i;
+      const bool ok = kb < nstep && s < nq32 && (!CAUSAL || kb <= s);
+      const auto rd = __builtin_amdgcn_make_buffer_rsrc((void*)(dsp + (row0[i] + kb) * 1024), (short)0, ok ? 2048 : 0,
+                                                        0x00020000);
+#pragma unroll
+      for (int u = 0; u < UD / kDqSteps; ++u)
+        std_[S][i * (UD / kDqSteps) + u] = __builtin_amdgcn_raw_buffer_load_b128(rd, (uint32_t)(lane * 16 + u * 1024), 0, 0);
+    }
+  };
+  auto store = [&](auto Sc, auto Bc) __attribute__((always_inline)) {
+    constexpr int S = decltype(Sc)::value, BUF = decltype(Bc)::value;
+#pragma unroll
+    for (int u = 0; u < UK; ++u) lds_wr16(swk[u] + BUF * BUFB, stk[S][u]);
+#pragma unroll
+    for (int u = 0; u < UD; ++u) lds_wr16(sd + BUF * BUFB + u * 1024, std_[S][u]);
+  };
+
+  // ---- accumulators: dQ^T [32 nb + 8 (e/4) + 4 hf + e%4][position l32] per query step ----
+  f32x16 acc[kDqSteps][NB];
+#pragma unroll
+  for (int i = 0; i < kDqSteps; ++i)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) acc[i][nb] = f32x16{};
+
+  auto compute = [&](auto Bc) __attribute__((always_inline)) {
+    constexpr int BUF = decltype(Bc)::value;
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      V8 bf[kDqSteps];
+#pragma unroll
+      for (int i = 0; i < kDqSteps; ++i) {
+        const uint32_t off = (uint32_t)(BUF * BUFB + i * 2048 + c * 1024);
+        bf[i] = cat_tr<T>(lds_rdtr(bd[0] + off), lds_rdtr(bd[1] + off));
+      }
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        const uint32_t off = (uint32_t)(BUF * BUFB + c * 16 * ROWB);
+        const V8 af = cat_tr<T>(lds_rdtr(at[0][nb] + off), lds_rdtr(at[1][nb] + off));
+#pragma unroll
+        for (int i = 0; i < kDqSteps; ++i) acc[i][nb] = mfma32(af, bf[i], acc[i][nb]);
+      }
+    }
+  };
+
+  // ---- prologue: tiles 0, 1 staged, tile 0 in buffer 0, tile 2 loading ----------------
+  load(IC<0>{}, 0);
+  load(IC<1>{}, 1);
+  store(IC<0>{}, IC<0>{});
+  load(IC<0>{}, 2);
+  lds_barrier();
+
+  // ---- main loop: iteration j writes tile j+1 to LDS, loads tile j+3, computes tile j ----
+  int n2 = nstep2;
+  asm volatile("" : "+s"(n2));
+  for (int j = 0; j < n2; j += 2) {
+    store(IC<1>{}, IC<1>{});
+    load(IC<1>{}, j + 3);
+    compute(IC<0>{});
+    lds_barrier();
+    store(IC<0>{}, IC<0>{});
+    load(IC<0>{}, j + 4);
+    compute(IC<1>{});
+    lds_barrier();
+  }
+
+  // ---- epilogue: dQ rows of each query step through LDS, coalesced stores --------------
+  const float scale = a.scale;
+  T* stg = (T*)smem + wv * 32 * OS;
+  T* dqp = (T*)a.dq + b * a.dqsb + h * a.dqsh;
+  const int qrow = 16 * (l32 >> 4) + 4 * ((l32 >> 3) & 1) + 8 * ((l32 >> 2) & 1) + (l32 & 3);
+#pragma unroll
+  for (int i = 0; i < kDqSteps; ++i) {
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int gi = 0; gi < 4; ++gi) {
+        const int d = nb * 32 + gi * 8 + hf * 4;
+        lds_write8(stg + qrow * OS + d, pack4<T>(acc[i][nb][gi * 4 + 0] * scale, acc[i][nb][gi * 4 + 1] * scale,
+                                                 acc[i][nb][gi * 4 + 2] * scale, acc[i][nb][gi * 4 + 3] * scale));
+      }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    const int q0 = (s0 + i) * 32;
+#pragma unroll
+    for (int u = 0; u < 32 * CH / 64; ++u) {
+      const int idx = lane + u * 64, r = idx / CH, c = idx % CH;
+      if (q0 + r < Tq) gstore16(dqp + (int64_t)(q0 + r) * a.dqst + c * 8, lds_read16(stg + r * OS + c * 8));
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  }
+}
+
+template <typename T, int D, bool CAUSAL>
+hipError_t launch_t(const BwdArgs& a, hipStream_t s) {
+  const dim3 grid((unsigned)(a.B * a.Hq * a.nqt)), block(kDqWaves * 64);
+  hipLaunchKernelGGL((dq_ds_kernel<T, D, CAUSAL>), grid, block, 0, s, a);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+int dq_ds_block_rows() { return kDqRows; }
+
+hipError_t launch_bwd_dq_ds(const BwdArgs& a, int D, int dtype, bool causal, hipStream_t s) {
+  if (dtype == 0) {
+    if (D == 128) return causal ? launch_t<bf16, 128, true>(a, s) : launch_t<bf16, 128, false>(a, s);
+    if (D == 64) return causal ? launch_t<bf16, 64, true>(a, s) : launch_t<bf16, 64, false>(a, s);
+  } else {
+    if (D == 128) return causal ? launch_t<f16, 128, true>(a, s) : launch_t<f16, 128, false>(a, s);
+    if (D == 64) return causal ? launch_t<f16, 64, true>(a, s) : launch_t<f16, 64, false>(a, s);
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace fa

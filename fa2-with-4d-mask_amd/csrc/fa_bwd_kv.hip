@@ -71,7 +71,8 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, hf = lane >> 5;
   const int Tq = a.Tq, Tk = a.Tk;
-  const int kt0 = kt * kKvKeys, kw0 = kt0 + wave * 32;
+  const int wv = __builtin_amdgcn_readfirstlane(wave);   // wave-uniform copy for scalar branches
+  const int kt0 = kt * kKvKeys, kw0 = kt0 + wv * 32;
   const int key = kw0 + l32;              // this lane's key (column of S)
   const int kc = min(key, Tk - 1);
   // scale == 0: every kept logit is 0, i.e. P = exp2(-LSE2): a zero multiplier
@@ -129,79 +130,121 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
     gd[u] = (uint32_t)(r * a.dst * 2 + c * 16);
     sw[u] = opaque(lds0 + r * ROWB + ((c ^ swz_q<D>(r)) * 16));
   }
-  u32x4 stq[UQ], std_[UQ];
-  float stl = 0.f, std_l = 0.f;  // staged LSE / Delta of row l32 (wave 0), selected at store time
-  int st_rows = 0;           // valid rows of the staged tile
-  auto tile_h = [&](int it) __attribute__((always_inline)) { return kvh * a.G + g0 + it / max(nst, 1); };
-  auto tile_qs = [&](int it) __attribute__((always_inline)) { return qstart + (it % max(nst, 1)) * kStep; };
-  // Position of the next tile to load, advanced by one step per call (no
-  // divisions in the loop): head ld_h, first row ld_qs, running element
-  // offsets of Q, dO and of the LSE/Delta rows.
+  // two staging sets (tiles j+3, j+4 in flight during iteration j): [set]
+  u32x4 stq[2][UQ], std_[2][UQ];
+  float stl[2] = {0.f, 0.f}, std_l[2] = {0.f, 0.f};  // staged LSE / Delta of row l32 (wave 0)
+  int st_rows[2] = {0, 0};                             // valid rows of the staged tile
+  // Loads address a head through one descriptor whose records end after row
+  // Tq - 1; a tile's first row is reached with the scalar offset, which the
+  // range check includes, so rows past Tq read as zeros.  Padding steps use
+  // descriptors without records.  State: next tile ld_it (head ld_h, first
+  // row ld_qs), scalar byte offsets of that row in Q, dO and LSE/Delta.
+  const uint32_t q_rec = (uint32_t)((int64_t)(Tq - 1) * a.qst * 2 + ROWB);
+  const uint32_t d_rec = (uint32_t)((int64_t)(Tq - 1) * a.dst * 2 + ROWB);
+  const uint32_t inc_q = (uint32_t)(kStep * a.qst * 2), inc_d = (uint32_t)(kStep * a.dst * 2);
+  const uint32_t so_q0 = (uint32_t)qstart * (uint32_t)a.qst * 2, so_d0 = (uint32_t)qstart * (uint32_t)a.dst * 2;
   int ld_it = 0, ld_h = kvh * a.G + g0, ld_qs = qstart;
-  int64_t ld_qo = (int64_t)b * a.qsb + (int64_t)ld_h * a.qsh + (int64_t)qstart * a.qst;
-  int64_t ld_do = (int64_t)b * a.dsb + (int64_t)ld_h * a.dsh + (int64_t)qstart * a.dst;
-  int64_t ld_lo = ((int64_t)b * a.Hq + ld_h) * Tq + qstart;
-  auto load_next = [&]() __attribute__((always_inline)) {
-    const int rows = ld_it < n ? min(kStep, Tq - ld_qs) : 0;
-    const int64_t nq = rows > 0 ? (int64_t)(rows - 1) * a.qst * 2 + ROWB : 0;
-    const int64_t nd = rows > 0 ? (int64_t)(rows - 1) * a.dst * 2 + ROWB : 0;
-    const auto rq = __builtin_amdgcn_make_buffer_rsrc((void*)((const T*)a.q + ld_qo), (short)0, (int)nq, 0x00020000);
-    const auto rd = __builtin_amdgcn_make_buffer_rsrc((void*)((const T*)a.dout + ld_do), (short)0, (int)nd, 0x00020000);
+  uint32_t so_q = so_q0, so_d = so_d0, so_l = (uint32_t)qstart * 4;
+  const T* q_head = (const T*)a.q + b * a.qsb + (int64_t)ld_h * a.qsh;
+  const T* d_head = (const T*)a.dout + b * a.dsb + (int64_t)ld_h * a.dsh;
+  const float* l_head = a.lse + ((int64_t)b * a.Hq + ld_h) * Tq;
+  const float* e_head = a.delta + ((int64_t)b * a.Hq + ld_h) * Tq;
+  auto load_next = [&](auto Sc) __attribute__((always_inline)) {
+    constexpr int S = decltype(Sc)::value;
+    const bool live = ld_it < n;
+    const auto rq = __builtin_amdgcn_make_buffer_rsrc((void*)q_head, (short)0, live ? (int)q_rec : 0, 0x00020000);
+    const auto rd = __builtin_amdgcn_make_buffer_rsrc((void*)d_head, (short)0, live ? (int)d_rec : 0, 0x00020000);
 #pragma unroll
     for (int u = 0; u < UQ; ++u) {
-      stq[u] = __builtin_amdgcn_raw_buffer_load_b128(rq, gq[u], 0, 0);
-      std_[u] = __builtin_amdgcn_raw_buffer_load_b128(rd, gd[u], 0, 0);
+      stq[S][u] = __builtin_amdgcn_raw_buffer_load_b128(rq, gq[u], so_q, 0);
+      std_[S][u] = __builtin_amdgcn_raw_buffer_load_b128(rd, gd[u], so_d, 0);
     }
-    if (wave == 0) {  // lanes 0-31: LSE rows, 32-63: Delta rows (uniform descriptors, lane select)
-      const auto rl = __builtin_amdgcn_make_buffer_rsrc((void*)(a.lse + ld_lo), (short)0, rows * 4, 0x00020000);
-      const auto rdl = __builtin_amdgcn_make_buffer_rsrc((void*)(a.delta + ld_lo), (short)0, rows * 4, 0x00020000);
-      const uint32_t vo = (uint32_t)l32 * 4;
-      stl = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rl, vo, 0, 0));
-      std_l = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rdl, vo, 0, 0));
+    if (wv == 0) {  // lanes 0-31: LSE rows, 32-63: Delta rows
+      const auto rl = __builtin_amdgcn_make_buffer_rsrc((void*)l_head, (short)0, live ? Tq * 4 : 0, 0x00020000);
+      const auto re = __builtin_amdgcn_make_buffer_rsrc((void*)e_head, (short)0, live ? Tq * 4 : 0, 0x00020000);
+      stl[S] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rl, (uint32_t)l32 * 4, so_l, 0));
+      std_l[S] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(re, (uint32_t)l32 * 4, so_l, 0));
     }
-    st_rows = rows;
-    // advance to the following tile
+    st_rows[S] = live ? min(kStep, Tq - ld_qs) : 0;
     ++ld_it;
     ld_qs += kStep;
-    ld_qo += (int64_t)kStep * a.qst;
-    ld_do += (int64_t)kStep * a.dst;
-    ld_lo += kStep;
+    so_q += inc_q;
+    so_d += inc_d;
+    so_l += kStep * 4;
     if (ld_qs >= Tq) {
       ++ld_h;
       ld_qs = qstart;
-      ld_qo = (int64_t)b * a.qsb + (int64_t)ld_h * a.qsh + (int64_t)qstart * a.qst;
-      ld_do = (int64_t)b * a.dsb + (int64_t)ld_h * a.dsh + (int64_t)qstart * a.dst;
-      ld_lo = ((int64_t)b * a.Hq + ld_h) * Tq + qstart;
+      so_q = so_q0;
+      so_d = so_d0;
+      so_l = (uint32_t)qstart * 4;
+      q_head += a.qsh;
+      d_head += a.dsh;
+      l_head += Tq;
+      e_head += Tq;
     }
   };
-  auto store_tile = [&](int buf) __attribute__((always_inline)) {
+  auto store_tile = [&](int buf, auto Sc) __attribute__((always_inline)) {
+    constexpr int S = decltype(Sc)::value;
 #pragma unroll
     for (int u = 0; u < UQ; ++u) {
-      lds_wr16(sw[u] + buf * QTILE, stq[u]);
-      lds_wr16(sw[u] + DOFF + buf * QTILE, std_[u]);
+      lds_wr16(sw[u] + buf * QTILE, stq[S][u]);
+      lds_wr16(sw[u] + DOFF + buf * QTILE, std_[S][u]);
     }
-    if (wave == 0) {
-      const bool ok = l32 < st_rows;
-      const float v = hf == 0 ? (ok ? stl : kPosInf) : (ok ? -std_l : 0.f);
-      lds_wrf(lds0 + LOFF + buf * LBUF + tid * 4, v);
+    if (wv == 0) {
+      // rows past the tile's end: LSE = +inf (P = 0 whatever S is), -Delta = 0
+      const bool ok = l32 < st_rows[S];
+      const float v = hf == 0 ? (ok ? stl[S] : kPosInf) : (ok ? -std_l[S] : 0.f);
+      lds_wrf(lds0 + LOFF + buf * LBUF + lane * 4, v);
     }
   };
+
+  // ---- step being computed: head it_h, first row it_qs (advanced per step) -----------
+  int it_h = kvh * a.G + g0, it_qs = qstart;
 
   // ---- mask / score of a step (lane's 16 query rows at its key) -----------------
   uint32_t mreg[MASK ? 4 : 1];
   float sreg[SCORE ? 16 : 1];
-  auto load_ms = [&](int it) __attribute__((always_inline)) {
+  auto load_ms = [&](bool live) __attribute__((always_inline)) {
     if constexpr (MASK || SCORE) {
-      const int h = tile_h(min(it, max(n - 1, 0))), qs = tile_qs(min(it, max(n - 1, 0)));
+      // padding steps reread the last real step's rows (harmless)
+      const int h = live ? it_h : kvh * a.G + g0 + gsz - 1;
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const int q = min(qs + 8 * (i >> 2) + 4 * hf + (i & 3), Tq - 1);
+        const int q = min(it_qs + 8 * (i >> 2) + 4 * hf + (i & 3), Tq - 1);
         if constexpr (MASK) {
           const uint32_t m = a.mask[b * a.msb + h * a.msh + (int64_t)q * a.msq + kc] != 0;
           if ((i & 3) == 0) mreg[i >> 2] = m; else mreg[i >> 2] |= m << (8 * (i & 3));
         }
         if constexpr (SCORE) sreg[i] = a.score[b * a.ssb + h * a.ssh + (int64_t)q * a.ssq + kc];
       }
+    }
+  };
+
+  // ---- dS tiles for the dQ kernel --------------------------------------------------
+  // dS of each step (this wave's 32 keys x the step's 32 rows) is stored as
+  // tile row "key" = 64 bytes, 16 bytes per lane and chunk c: the lane's
+  // packed values of rows 16 c + 4 hf + {0..3, 8..11}.  Stores of step j-1
+  // are issued in iteration j; a descriptor with no records drops them
+  // (padding steps, tiles above the causal diagonal, keys past Tk, no dS).
+  // it_tile: tile of (it_h, step it_qs / 32) and this wave's keys.
+  const int kb32 = __builtin_amdgcn_readfirstlane(kw0) >> 5;
+  const bool ds_on = a.ds != nullptr && kb32 < a.nk32;
+  const uint32_t ds_vo = (uint32_t)(l32 * 64 + hf * 16);
+  const int64_t ds_h0 = ((int64_t)b * a.Hq + it_h) * a.ds_plane + ds_row(qstart >> 5, a.nk32, CAUSAL) + kb32;
+  int64_t it_tile = ds_h0;
+  auto ds_rs = __builtin_amdgcn_make_buffer_rsrc((void*)a.ds, (short)0, 0, 0x00020000);
+  // descriptor of step j's tile, then advance (it_h, it_qs, it_tile) to step j+1
+  auto next_step = [&](int j) __attribute__((always_inline)) {
+    const int s = it_qs >> 5;
+    const bool ok = ds_on && j < n && (!CAUSAL || kb32 <= s);
+    ds_rs = __builtin_amdgcn_make_buffer_rsrc((void*)((uint16_t*)a.ds + it_tile * 1024), (short)0, ok ? 2048 : 0,
+                                              0x00020000);
+    it_qs += kStep;
+    it_tile += CAUSAL ? min(s + 1, a.nk32) : a.nk32;
+    if (it_qs >= Tq) {
+      ++it_h;
+      it_qs = qstart;
+      it_tile = ds_h0 + (int64_t)(it_h - (kvh * a.G + g0)) * a.ds_plane;
     }
   };
 
@@ -220,14 +263,15 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
 
   // S/dP of step "it" (tile in buffer BUF) -> parity PAR; dV/dK of step it-2
   // (buffer (BUF+2)%4, parity PAR) -- one interleaved MFMA stream, with the
-  // P/dS VALU work of step it-1 (parity PAR^1) threaded through it.
-  auto iter = [&](auto BUFc, int j) __attribute__((always_inline)) {
+  // P/dS VALU work of step it-1 (parity PAR^1) threaded through it.  EDGE:
+  // some (row, key) of the step is masked (causal diagonal or a mask).
+  auto iter = [&](auto BUFc, auto EDGEc, int j) __attribute__((always_inline)) {
     // j: step whose P/dS is computed now; S/dP of j+1; dV/dK of j-1
     constexpr int BUF = decltype(BUFc)::value;          // buffer of step j
+    constexpr bool EDGE = decltype(EDGEc)::value != 0;
     constexpr int BN1 = (BUF + 1) % kNBuf, BM1 = (BUF + kNBuf - 1) % kNBuf;
     constexpr int PJ = BUF & 1, PN = PJ ^ 1;            // parities of j and j +- 1
-    const int h = tile_h(j), qs = tile_qs(j);
-    const bool edge = MASK || (CAUSAL && kw0 + 31 > qs);
+    const int dkq = key - (it_qs + 4 * hf);              // causal: keep iff dkq <= 8 gi + t
 
     // operand reads for the two MFMA streams, AHEAD ops ahead
     auto rd_sd = [&](int t) __attribute__((always_inline)) -> u32x4 {   // t: ds = t/2, Q (even) / dO (odd)
@@ -253,18 +297,23 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
 #pragma unroll
     for (int t = 0; t < AHEAD; ++t) { xs[t] = rd_sd(t); xt[t] = rd_tr(t); }
 
-    // P / dS of step j, element by element (lane entry i: row 8 (i/4) + 4 hf + i%4)
+    // P / dS of step j, element by element (lane entry i: row 8 (i/4) + 4 hf + i%4),
+    // in two halves one slot apart: exp, then mask / dS / packing.
     f32x4 l4[2];                           // LSE of rows group gi (double-buffered by gi parity)
     auto read_l = [&](int gi) __attribute__((always_inline)) { l4[gi & 1] = lds_rdf4(al + BUF * LBUF + gi * 32); };
-    auto elem = [&](int i) __attribute__((always_inline)) {
+    auto elem_exp = [&](int i) __attribute__((always_inline)) -> float {
       const int gi = i >> 2, t = i & 3;
       float sv = sacc[PJ][i];
       if constexpr (SCORE) sv += sreg[i];
       float p = exp2_fast(fmaf(sv, c2, -l4[gi & 1][t]));
-      if (edge) {
-        const int q = qs + 8 * gi + 4 * hf + t;
+      asm volatile("" : "+v"(p));
+      return p;
+    };
+    auto elem_fin = [&](int i, float p) __attribute__((always_inline)) {
+      const int gi = i >> 2, t = i & 3;
+      if constexpr (EDGE) {
         bool keep = true;
-        if constexpr (CAUSAL) keep = key <= q;
+        if constexpr (CAUSAL) keep = dkq <= 8 * gi + t;
         if constexpr (MASK) keep = keep && ((mreg[gi] >> (8 * t)) & 0xffu) != 0;
         p = keep ? p : 0.f;
       }
@@ -284,14 +333,18 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
     };
 
     // Slot t (own scheduling region): MFMAs of op t of both streams, the
-    // operand reads of op t + AHEAD, and 16/NOP elements of P/dS.
-    constexpr int EPS = 16 / NOP;          // elements per slot
+    // operand reads of op t + AHEAD, the exp of elements of slot t and the
+    // rest of the elements of slot t-1 (16/NOP elements per slot).
+    constexpr int EPS = 16 / NOP;
+    float pe[2][EPS];
     read_l(0);
 #pragma unroll
     for (int t = 0; t < NOP; ++t) {
       // stream 1: S / dP of step j+1 (ds = t/2)
       if ((t & 1) == 0) sacc[PN] = mfma32(as_vec8<T>(xs[t % AHEAD]), kf[t >> 1], (t >> 1) == 0 ? f32x16{} : sacc[PN]);
       else pacc[PN] = mfma32(as_vec8<T>(xs[t % AHEAD]), vf[t >> 1], (t >> 1) == 0 ? nd_next : pacc[PN]);
+      // dS of step j-1 out to its tile
+      if (t < 2) __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, dspk[PN][t]), ds_rs, ds_vo + 32 * t, 0, 0);
       // stream 2: dV / dK of step j-1 (c, nb)
       {
         const int c = t / (2 * NB), nb = (t / 2) % NB;
@@ -303,12 +356,19 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
       for (int e = 0; e < EPS; ++e) {
         const int i = t * EPS + e;
         if ((i & 3) == 1 && i + 3 < 16) read_l((i >> 2) + 1);   // LSE of the next row group
-        elem(i);
+        pe[t & 1][e] = elem_exp(i);
+      }
+      if (t > 0) {
+#pragma unroll
+        for (int e = 0; e < EPS; ++e) elem_fin((t - 1) * EPS + e, pe[(t - 1) & 1][e]);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
-    // mask / score of step j+1 (registers of step j are consumed)
-    load_ms(j + 1);
+#pragma unroll
+    for (int e = 0; e < EPS; ++e) elem_fin((NOP - 1) * EPS + e, pe[(NOP - 1) & 1][e]);
+    // next step's dS descriptor and position, then its mask / score
+    next_step(j);
+    load_ms(j + 1 < n);
   };
 
   // ---- prologue --------------------------------------------------------------------
@@ -318,10 +378,11 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
     lds_wr16(sw[u] + 3 * QTILE, u32x4{0, 0, 0, 0});
     lds_wr16(sw[u] + DOFF + 3 * QTILE, u32x4{0, 0, 0, 0});
   }
-  load_next(); store_tile(0);   // tile 0
-  load_next(); store_tile(1);   // tile 1
-  load_next();                  // tile 2 staged
-  load_ms(0);
+  load_next(IC<0>{}); store_tile(0, IC<0>{});   // tile 0
+  load_next(IC<1>{}); store_tile(1, IC<1>{});   // tile 1
+  load_next(IC<0>{});                           // tile 2 staged (set 0)
+  load_next(IC<1>{});                           // tile 3 staged (set 1)
+  load_ms(n > 0);
   lds_barrier();
   // S / dP of step 0 (parity 0); the dP chain starts from -Delta
   f32x16 nd0;
@@ -348,9 +409,11 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
   // the loads of tile j+3 get a whole iteration of latency.
   auto step = [&](auto BUFc, int j) __attribute__((always_inline)) {
     constexpr int BUF = decltype(BUFc)::value;
-    store_tile((BUF + 2) % kNBuf);   // tile j+2
-    load_next();                     // tile j+3
-    iter(BUFc, j);
+    store_tile((BUF + 2) % kNBuf, IC<BUF & 1>{});   // tile j+2 (staged two iterations ago)
+    load_next(IC<BUF & 1>{});                       // tile j+4
+    // causal: the compare runs on every step (a second copy of the body for
+    // the steps off the diagonal would not fit the register budget)
+    iter(BUFc, IC<(MASK || CAUSAL) ? 1 : 0>{}, j);
     lds_barrier();
   };
   int n4 = n > 0 ? (n + 4) & ~3 : 0;

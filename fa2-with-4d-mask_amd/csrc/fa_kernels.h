@@ -46,7 +46,21 @@ struct BwdArgs {
   float qsign;
   int zero_scale;
   int mask_vec, score_vec;
+  // dS tiles of the deterministic path (written by the dK/dV kernel, read by
+  // the dQ kernel); null when dQ is recomputed instead.  Tile (b, h, s, kb)
+  // holds dS / scale of query rows 32 s.. and keys 32 kb.. as [key][32] 16-bit
+  // values, element offset ((b Hq + h) ds_plane + ds_row(s) + kb) * 1024.
+  void* ds;
+  int64_t ds_plane;     // tiles per (b, h)
+  int nq32, nk32;       // 32-row / 32-key steps
 };
+
+// First tile of query step s in a (b, h) plane of dS tiles: causal planes
+// keep tiles kb <= s only (and kb < nk32), full planes keep every kb < nk32.
+__host__ __device__ inline int64_t ds_row(int64_t s, int64_t nk32, bool causal) {
+  if (!causal) return s * nk32;
+  return s <= nk32 ? s * (s + 1) / 2 : nk32 * (nk32 + 1) / 2 + (s - nk32) * nk32;
+}
 
 struct CvtArgs {
   const float* src;      // nsplit fp32 slabs, element (b, t, h, d) at b*src_sb + t*src_st + h*src_sh + d
@@ -65,6 +79,9 @@ hipError_t launch_bwd_dq(const BwdArgs& a, int D, int dtype, bool causal, hipStr
 // dK/dV of the deterministic path (no dQ), 4 waves x 32 keys per workgroup.
 hipError_t launch_bwd_dkdv2(const BwdArgs& a, int D, int dtype, bool causal, hipStream_t s);
 int dkdv2_block_keys();
+// dQ = scale * dS K from the dS tiles, 256 query rows per workgroup.
+hipError_t launch_bwd_dq_ds(const BwdArgs& a, int D, int dtype, bool causal, hipStream_t s);
+int dq_ds_block_rows();
 hipError_t launch_convert(const CvtArgs& a, int dtype, hipStream_t s);
 
 }  // namespace fa

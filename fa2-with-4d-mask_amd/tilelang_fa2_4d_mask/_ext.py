@@ -19,7 +19,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must be loaded before the HIP library, see above)
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libfa2_4d_mask.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 FA_DTYPE_BF16 = 0
 FA_DTYPE_FP16 = 1
@@ -60,7 +60,8 @@ class FaBwdParams(ctypes.Structure):
         ("batch seqlen_q seqlen_k heads_q heads_k head_dim", _i32),
         ("scale", ctypes.c_float),
         ("is_causal atomic_dq kv_split dtype", _i32),
-        ("stream", _vp),
+        ("stream ds_tiles", _vp),
+        ("ds_limit_bytes", _i64),
     )
 
 
@@ -70,6 +71,7 @@ class FaBwdPlan(ctypes.Structure):
         ("needs_dq_accum", _i32),
         ("dq_accum_elems", _i64),
         ("dkv_accum_elems", _i64),
+        ("ds_elems", _i64),
     ]
 
 

@@ -29,6 +29,11 @@ from torch.autograd.function import once_differentiable
 
 from . import _ext
 
+# Largest dS workspace (bytes) the deterministic backward may allocate to hand
+# dS from the dK/dV kernel to the dQ kernel; 0 = the library's default (8 GiB),
+# negative = never (dQ is then recomputed from Q, K, V, dO).
+DS_LIMIT_BYTES = 0
+
 
 def _norm_strides(x: torch.Tensor) -> tuple:
     """Strides with size-1 dimensions reported as 0 (never stepped over)."""
@@ -211,6 +216,7 @@ class _flash_attention_with_4d_mask(torch.autograd.Function):
             p.atomic_dq = 1 if ctx.use_atomic_backward else 0
             p.kv_split = 0
             p.dtype = _ext.dtype_code(q.dtype)
+            p.ds_limit_bytes = DS_LIMIT_BYTES
             lib = _ext.load_library()
             plan = _ext.FaBwdPlan()
             _ext.check(lib.fa_bwd_plan(ctypes.byref(p), ctypes.byref(plan)), "fa_bwd_plan", lib)
@@ -230,7 +236,10 @@ class _flash_attention_with_4d_mask(torch.autograd.Function):
             p.q, p.k, p.v, p.o, p.dout = q.data_ptr(), k.data_ptr(), v.data_ptr(), O.data_ptr(), do.data_ptr()
             p.lse, p.delta, p.dead_flags = LSE.data_ptr(), delta.data_ptr(), dead.data_ptr()
             p.mask, p.score = _ext.ptr(mask), _ext.ptr(score)
+            # deterministic path: dS tiles handed from the dK/dV kernel to the dQ kernel
+            ds = torch.empty((plan.ds_elems,), dtype=q.dtype, device=dev) if plan.ds_elems else None
             p.dq_accum, p.dk_accum, p.dv_accum = _ext.ptr(dq_acc), _ext.ptr(dk_acc), _ext.ptr(dv_acc)
+            p.ds_tiles = _ext.ptr(ds)
             p.dq, p.dk, p.dv = dQ.data_ptr(), dK.data_ptr(), dV.data_ptr()
             p.q_stride_b, p.q_stride_t, p.q_stride_h = _bthd_strides(q)
             p.k_stride_b, p.k_stride_t, p.k_stride_h = _bthd_strides(k)

@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define FA_ABI_VERSION 1
+#define FA_ABI_VERSION 2
 
 enum FaDtype { FA_DTYPE_BF16 = 0, FA_DTYPE_FP16 = 1 };
 
@@ -100,6 +100,8 @@ typedef struct FaBwdParams {
   int32_t kv_split;              /* query-head-group split of the dK/dV kernel; 0 = let fa_bwd_plan choose */
   int32_t dtype;
   void* stream;
+  void* ds_tiles;                /* workspace of plan.ds_elems 16-bit values (deterministic path), else unused */
+  int64_t ds_limit_bytes;        /* largest dS workspace the caller accepts; 0 = 8 GiB, < 0 = none */
 } FaBwdParams;
 
 /* What fa_bwd will do for a problem, so the caller can size workspaces. */
@@ -108,6 +110,8 @@ typedef struct FaBwdPlan {
   int32_t needs_dq_accum;        /* 1 if dq_accum is used */
   int64_t dq_accum_elems;        /* B*Tq*Hq*D when used, else 0 */
   int64_t dkv_accum_elems;       /* B*Tk*Hk*D when kv_split > 1, else 0 */
+  int64_t ds_elems;              /* atomic_dq = 0: size of ds_tiles (dS of every kept 32x32 block, 16-bit),
+                                    0 when it would exceed ds_limit_bytes (dQ is then recomputed) */
 } FaBwdPlan;
 
 /* Forward.  Replaces the reference's `flash_attention_fwd_with_4d_mask`
@@ -126,7 +130,9 @@ int fa_bwd_preprocess(const FaBwdParams* p);
  * `flash_attention_bwd_with_4d_mask_reduce` (python/fa2.py:305-426, launched at
  * :543-547) when atomic_dq = 0.  atomic_dq = 1: one kernel; dK/dV are written in
  * dtype (kv_split = 1) or added to dk_accum/dv_accum, dQ is added to dq_accum.
- * atomic_dq = 0: the dK/dV kernel and a deterministic dQ kernel writing dq in dtype.
+ * atomic_dq = 0: the dK/dV kernel and a deterministic dQ kernel writing dq in dtype;
+ * with plan.ds_elems > 0 the dK/dV kernel also stores dS into ds_tiles and the dQ
+ * kernel is dQ = scale dS K over them, otherwise it recomputes S, P and dP.
  * Must follow fa_bwd_preprocess on the same stream. */
 int fa_bwd(const FaBwdParams* p);
 

@@ -185,6 +185,33 @@ def test_plan_headline_needs_no_split(lib):
     assert plan.needs_dq_accum == 0 and plan.dq_accum_elems == 0
 
 
+def test_plan_ds_tiles(lib):
+    # causal 8192 x 8192: 256 query steps x 256 key steps, lower triangle with
+    # the diagonal = 256 * 257 / 2 tiles of 32 x 32 per head
+    assert _plan(lib).ds_elems == 0    # atomic path: no dS tiles
+    plan = _plan(lib, atomic_dq=0, is_causal=1)
+    assert plan.ds_elems == 32 * (256 * 257 // 2) * 1024
+    plan = _plan(lib, atomic_dq=0)
+    assert plan.ds_elems == 32 * 256 * 256 * 1024
+    # ragged causal, Tq > Tk: steps past the last key step keep nk32 tiles
+    plan = _plan(lib, atomic_dq=0, is_causal=1, seqlen_q=333, seqlen_k=130, heads_q=4, heads_k=2)
+    nq, nk = 11, 5
+    assert plan.ds_elems == 4 * (nk * (nk + 1) // 2 + (nq - nk) * nk) * 1024
+    # caller limits: below the need, or none at all -> dQ recomputed
+    assert _plan(lib, atomic_dq=0, ds_limit_bytes=1 << 30).ds_elems == 0
+    assert _plan(lib, atomic_dq=0, is_causal=1, ds_limit_bytes=-1).ds_elems == 0
+    assert _plan(lib, atomic_dq=0, is_causal=1, ds_limit_bytes=3 << 30).ds_elems > 0
+
+
+def test_det_path_needs_ds_tiles(lib):
+    p = bwd_params(atomic_dq=0)
+    assert lib.fa_bwd(ctypes.byref(p)) == 8
+    assert "needs ds_tiles" in lib.fa_last_error().decode()
+    p = bwd_params(atomic_dq=0, ds_tiles=FAKE + 8)
+    assert lib.fa_bwd(ctypes.byref(p)) == 5
+    assert "ds_tiles must be 16-byte aligned" in lib.fa_last_error().decode()
+
+
 def test_plan_mqa_splits_the_group(lib):
     # BASELINE config M: B1 Tq2048 Tk16384 Hq32 Hk1 D64 -> 128 key tiles; split 4 -> 512 workgroups
     m = dict(seqlen_q=2048, seqlen_k=16384, heads_q=32, heads_k=1, head_dim=64)

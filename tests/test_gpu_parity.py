@@ -36,8 +36,13 @@ def _api():
     return api
 
 
-def run_ours(case, cfg, *, atomic=True, scale=None, attention_mask=None, backward=True):
+def run_ours(case, cfg, *, atomic=True, scale=None, attention_mask=None, backward=True, ds_limit=0):
+    """ds_limit: dS workspace limit of the deterministic backward (0 = default,
+    dQ from the stored dS tiles; -1 = dQ recomputed from Q, K, V, dO)."""
     api = _api()
+    import tilelang_fa2_4d_mask.fa2 as fa2mod
+
+    fa2mod.DS_LIMIT_BYTES = ds_limit
     dev = torch.device("cuda:0")
     q = case["q"].to(dev).detach().requires_grad_(backward)
     k = case["k"].to(dev).detach().requires_grad_(backward)
@@ -50,10 +55,13 @@ def run_ours(case, cfg, *, atomic=True, scale=None, attention_mask=None, backwar
         layout=cfg.layout, use_atomic_backward=atomic,
     )
     res = {"out": out.detach()}
-    if backward:
-        out.backward(case["grad"].to(dev))
-        res.update(dq=q.grad, dk=k.grad, dv=v.grad)
-    torch.cuda.synchronize()
+    try:
+        if backward:
+            out.backward(case["grad"].to(dev))
+            res.update(dq=q.grad, dk=k.grad, dv=v.grad)
+        torch.cuda.synchronize()
+    finally:
+        fa2mod.DS_LIMIT_BYTES = 0
     if cfg.layout == "bshd":
         res = {n: t.transpose(1, 2) for n, t in res.items()}
     return {n: t.float().cpu() for n, t in res.items()}
@@ -123,23 +131,31 @@ SMALL = [
 ]
 
 
-@pytest.mark.parametrize("atomic", [True, False], ids=["atomic", "deterministic"])
+# backward modes: fp32-atomic dQ; deterministic with dQ from the stored dS
+# tiles; deterministic with dQ recomputed (no dS workspace allowed)
+MODES = {"atomic": (True, 0), "det_ds": (False, 0), "det_recompute": (False, -1)}
+
+
+@pytest.mark.parametrize("mode", list(MODES))
 @pytest.mark.parametrize("cfg", SMALL, ids=[c.name for c in SMALL])
-def test_small_vs_oracle(cuda, cfg, atomic):
+def test_small_vs_oracle(cuda, cfg, mode):
     case = I.make_case(cfg, seed=0)
-    print(f"case {cfg.name} atomic={atomic}", flush=True)
-    ours = run_ours(case, cfg, atomic=atomic)
+    print(f"case {cfg.name} mode={mode}", flush=True)
+    atomic, ds_limit = MODES[mode]
+    ours = run_ours(case, cfg, atomic=atomic, ds_limit=ds_limit)
     ref = run_oracle_cpu(case, cfg)
-    check(ours, ref, label=f"{cfg.name}/{'atomic' if atomic else 'det'}")
+    check(ours, ref, label=f"{cfg.name}/{mode}")
 
 
+@pytest.mark.parametrize("mode", ["atomic", "det_ds"])
 @pytest.mark.parametrize("scale", [0.05, -0.08, 0.0], ids=["small", "negative", "zero"])
-def test_scale_values(cuda, scale):
+def test_scale_values(cuda, scale, mode):
     cfg = C("scale", 1, 200, 260, 4, 2, 128, mask="bernoulli", score="normal")
     case = I.make_case(cfg, seed=1)
-    ours = run_ours(case, cfg, scale=scale)
+    atomic, ds_limit = MODES[mode]
+    ours = run_ours(case, cfg, scale=scale, atomic=atomic, ds_limit=ds_limit)
     ref = run_oracle_cpu(case, cfg, scale=scale)
-    check(ours, ref, label=f"scale={scale}")
+    check(ours, ref, label=f"scale={scale}/{mode}")
 
 
 def test_dead_rows_policy(cuda):
@@ -151,11 +167,11 @@ def test_dead_rows_policy(cuda):
     m[1, 3, 200, :] = False    # batch 1, head 3 (kv-head 1)
     m[1, 3, 0:64, :] = False   # a fully dead leading q tile
     case["mask"] = m
-    for atomic in (True, False):
-        ours = run_ours(case, cfg, atomic=atomic)
+    for mode, (atomic, ds_limit) in MODES.items():
+        ours = run_ours(case, cfg, atomic=atomic, ds_limit=ds_limit)
         ref = run_oracle_cpu(case, cfg)
         assert torch.isnan(ref["out"][0, 1, 17]).all() and torch.isnan(ref["dv"][0, 0]).all()
-        check(ours, ref, label=f"dead/{atomic}")
+        check(ours, ref, label=f"dead/{mode}")
         assert torch.isnan(ours["out"][0, 1, 17]).all()
         assert (ours["dq"][0, 1, 17] == 0).all() and (ours["dq"][1, 3, 200] == 0).all()
         assert (ours["dq"][1, 3, 0:64] == 0).all()
@@ -206,7 +222,8 @@ def test_bhsd_contiguous_inputs(cuda):
     check(ours, run_oracle_cpu(case, cfg), label="bhsd-contiguous")
 
 
-def test_tiny_lengths(cuda):
+@pytest.mark.parametrize("mode", ["atomic", "det_ds"])
+def test_tiny_lengths(cuda, mode):
     # Boundary/indexing test (an indexing bug gives O(1) errors).  With a few
     # hundred entries per output the mean is dominated by single bf16 rounding
     # steps (mean bar: one ulp of the typical entry, 2^-7), and with 3 keys each
@@ -216,14 +233,17 @@ def test_tiny_lengths(cuda):
     for (tq, tk, causal) in [(1, 1, False), (1, 7, False), (5, 1, True), (3, 65, True), (70, 3, False)]:
         cfg = C("tiny", 1, tq, tk, 2, 1, 64, is_causal=causal)
         case = I.make_case(cfg, seed=6)
-        check(run_ours(case, cfg), run_oracle_cpu(case, cfg), label=f"tiny {tq}x{tk} causal={causal}",
+        atomic, ds_limit = MODES[mode]
+        check(run_ours(case, cfg, atomic=atomic, ds_limit=ds_limit), run_oracle_cpu(case, cfg),
+              label=f"tiny {tq}x{tk} causal={causal} {mode}",
               mean_rel=2.0 ** -7, abs_bar=4e-2, rel_bar=2.0 ** -5)
 
 
-def test_deterministic_path_is_bitwise_repeatable(cuda):
+@pytest.mark.parametrize("ds_limit", [0, -1], ids=["det_ds", "det_recompute"])
+def test_deterministic_path_is_bitwise_repeatable(cuda, ds_limit):
     cfg = C("det", 1, 512, 512, 8, 2, 128, is_causal=True, mask="bernoulli")
     case = I.make_case(cfg, seed=7)
-    a = run_ours(case, cfg, atomic=False)
-    b = run_ours(case, cfg, atomic=False)
+    a = run_ours(case, cfg, atomic=False, ds_limit=ds_limit)
+    b = run_ours(case, cfg, atomic=False, ds_limit=ds_limit)
     for n in a:
         assert torch.equal(a[n], b[n]), n
