@@ -3,19 +3,23 @@
 
 One step = one fwd+bwd pass (non-causal) of ``tilelang_flash_attention`` over
 the BASELINE headline config: Q/K/V/dO ~ N(0,1) bf16, BHSD views
-over BTHD storage, scale D^-0.5 -- exactly what the reference's
-throughput_check.py times (fwd+bwd = zero grads, forward, backward(dO),
-benchmark/throughput_check.py:206-211).  The same run also times fwd and
-fwd+bwd with is_causal=True and fwd non-causal; those go into ``breakdown``.
+over BTHD storage, scale D^-0.5 -- what the reference's throughput_check.py
+times (fwd+bwd = zero grads, forward, backward(dO),
+benchmark/throughput_check.py:206-211).  ``value`` uses the deterministic
+backward (use_atomic_backward=False: dK/dV kernel that also stores dS, then
+dQ = dS K); the reference's default atomic-dQ backward is timed in the same run
+(``breakdown``), as are fwd and fwd+bwd with is_causal=True.
 
 FLOP convention (benchmark/throughput_check.py:85-92): fwd 4*B*Hq*Tq*Tk*D,
 fwd+bwd 14*..., x0.5 when causal.  Peak: MI355X dense bf16 MFMA 2.5 PFLOP/s.
 
-``roofline`` is for the dominant kernel of the step, the backward kernel
-launched by ``fa_bwd`` (dK/dV + atomic dQ, 10*B*Hq*Tq*Tk*D algorithmic FLOPs
-per launch), timed with HIP events on the launch stream inside the timed
-region.  ``cpu_baseline`` times this repository's eager fp32 oracle on the host
-cores on a bounded sample.
+``roofline`` is for the dominant kernel of the step, the dK/dV kernel launched
+by ``fa_bwd`` on the deterministic path: 4 GEMMs (S, dP, dV, dK), i.e.
+8*B*Hq*Tq*Tk*D algorithmic FLOPs per launch, timed with HIP events on the
+launch stream inside the timed region.  ``traffic`` (HBM bytes per launch) is
+read from profiles/dkdv2_H_traffic.json, written from rocprofv3 FETCH_SIZE /
+WRITE_SIZE runs scaled by a copy-kernel calibration.  ``cpu_baseline`` times
+this repository's eager fp32 oracle on the host cores on a bounded sample.
 
 Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline]
 """
@@ -144,40 +148,54 @@ def main() -> int:
                 api.tilelang_flash_attention(q0, k0, v0, is_causal=causal)
         return f
 
-    def fwd_bwd(causal):
+    def fwd_bwd(causal, atomic):
         def f():
             q.grad = k.grad = v.grad = None
-            out = api.tilelang_flash_attention(q, k, v, is_causal=causal)
+            out = api.tilelang_flash_attention(q, k, v, is_causal=causal, use_atomic_backward=atomic)
             out.backward(do)
         return f
 
     log(f"device: {torch.cuda.get_device_name(dev)}; workload B{B} T{T} Hq{HQ} Hk{HK} D{D} bf16")
     results = {}
     for name, fn, mode, causal in (
-        ("fwd_bwd", fwd_bwd(False), "fwd_bwd", False),
+        ("fwd_bwd", fwd_bwd(False, False), "fwd_bwd", False),
         ("fwd", fwd(False), "fwd", False),
         ("fwd_causal", fwd(True), "fwd", True),
-        ("fwd_bwd_causal", fwd_bwd(True), "fwd_bwd", True),
+        ("fwd_bwd_causal", fwd_bwd(True, False), "fwd_bwd", True),
+        ("fwd_bwd_atomic", fwd_bwd(False, True), "fwd_bwd", False),
+        ("fwd_bwd_causal_atomic", fwd_bwd(True, True), "fwd_bwd", True),
     ):
         ms, kern = time_steps(torch, fn, args.steps, args.warmup, record_kernel_events)
         tf = conv_flops(mode, causal) / (ms * 1e-3) * 1e-12
         results[name] = {"ms": round(ms, 4), "tflops": round(tf, 2), "frac_of_peak": round(tf / PEAK_TFLOPS, 4),
                          "kernel_ms": {k2: round(v2, 4) for k2, v2 in kern.items()}}
-        log(f"{name:15s} {ms:8.3f} ms  {tf:8.1f} TFLOPS  ({100 * tf / PEAK_TFLOPS:5.1f}% of peak)  kernels {kern}")
+        log(f"{name:22s} {ms:8.3f} ms  {tf:8.1f} TFLOPS  ({100 * tf / PEAK_TFLOPS:5.1f}% of peak)  kernels {kern}")
 
     main_res = results["fwd_bwd"]
-    bwd_ms = main_res["kernel_ms"]["fa_bwd"]
-    bwd_flops = 10.0 * B * HQ * T * T * D
-    achieved = bwd_flops / (bwd_ms * 1e-3) * 1e-12
+    # dominant kernel: dK/dV (fa_bwd on the deterministic path), 4 GEMMs
+    dkdv_ms = main_res["kernel_ms"]["fa_bwd"]
+    dkdv_flops = 8.0 * B * HQ * T * T * D
+    achieved = dkdv_flops / (dkdv_ms * 1e-3) * 1e-12
+    # dQ = dS K (fa_bwd_finalize on the deterministic path): streams the 16-bit dS tiles
+    dq_ms = main_res["kernel_ms"]["fa_bwd_finalize"]
+    dq_bytes = 2.0 * B * HQ * T * T + 2.0 * B * HQ * T * D * 2   # dS tiles + K rows (L2) + dQ out
     fwd_kernel_ms = results["fwd"]["kernel_ms"]["fa_fwd"]
     fwd_achieved = 4.0 * B * HQ * T * T * D / (fwd_kernel_ms * 1e-3) * 1e-12
     for name, r in results.items():
-        causal = name.endswith("causal")
-        if "fa_fwd" in r["kernel_ms"]:
-            r["fwd_kernel_tflops"] = round(conv_flops("fwd", causal) / (r["kernel_ms"]["fa_fwd"] * 1e-3) * 1e-12, 2)
-        if "fa_bwd" in r["kernel_ms"]:
-            r["bwd_kernel_tflops"] = round(10.0 * (0.5 if causal else 1.0) * B * HQ * T * T * D
-                                           / (r["kernel_ms"]["fa_bwd"] * 1e-3) * 1e-12, 2)
+        causal = "causal" in name
+        km = r["kernel_ms"]
+        if "fa_fwd" in km:
+            r["fwd_kernel_tflops"] = round(conv_flops("fwd", causal) / (km["fa_fwd"] * 1e-3) * 1e-12, 2)
+        if "fa_bwd" in km:
+            bwd_ms = km["fa_bwd"] + km.get("fa_bwd_finalize", 0.0)
+            r["bwd_tflops"] = round(10.0 * (0.5 if causal else 1.0) * B * HQ * T * T * D / (bwd_ms * 1e-3) * 1e-12, 2)
+    traffic = None
+    tpath = ROOT / "profiles" / "dkdv2_H_traffic.json"
+    if tpath.exists():
+        try:
+            traffic = json.loads(tpath.read_text()).get("bytes_per_launch")
+        except (OSError, ValueError):
+            traffic = None
 
     line = {
         "metric": METRIC,
@@ -193,23 +211,27 @@ def main() -> int:
         "dtype": "bf16",
         "data": "synthetic: Q/K/V/dO ~ N(0,1) bf16, seeded, BHSD views over BTHD storage",
         "config": {
-            "workload": "H (BASELINE configs[1]): fwd+bwd non-causal per step",
+            "workload": "H (BASELINE configs[1]): fwd+bwd non-causal per step, deterministic backward "
+                        "(use_atomic_backward=False); atomic-dQ default in breakdown",
             "batch": B, "seq_len_q": T, "seq_len_k": T, "heads_q": HQ, "heads_k": HK, "head_dim": D,
             "layout": "bhsd", "scale": "D^-0.5", "parallelism": "single GPU",
         },
         "breakdown": results,
         "roofline": {
-            "kernel": "dkdv_kernel<bf16,128> via fa_bwd (dK/dV + fp32-atomic dQ)",
+            "kernel": "dkdv2_kernel<bf16,128> via fa_bwd (dK/dV + dS tiles, deterministic path)",
             "bound": "mfma",
             "achieved": round(achieved, 2),
             "peak": PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_TFLOPS, 4),
-            "traffic": None,
-            "avg_launch_ms": round(bwd_ms, 4),
-            "flops_per_launch": bwd_flops,
+            "traffic": traffic,
+            "avg_launch_ms": round(dkdv_ms, 4),
+            "flops_per_launch": dkdv_flops,
             "fwd_kernel": {"achieved": round(fwd_achieved, 2), "frac": round(fwd_achieved / PEAK_TFLOPS, 4),
-                           "avg_launch_ms": round(fwd_kernel_ms, 4)},
+                           "avg_launch_ms": round(fwd_kernel_ms, 4), "unit": "TFLOP/s"},
+            "dq_kernel": {"bound": "hbm", "achieved": round(dq_bytes / (dq_ms * 1e-3) * 1e-9, 1), "peak": 8000.0,
+                          "unit": "GB/s", "frac": round(dq_bytes / (dq_ms * 1e-3) * 1e-9 / 8000.0, 4),
+                          "avg_launch_ms": round(dq_ms, 4), "bytes_per_launch": dq_bytes},
         },
     }
     if not args.no_cpu_baseline:

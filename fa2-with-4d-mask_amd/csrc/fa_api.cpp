@@ -225,12 +225,7 @@ int fa_bwd_preprocess(const FaBwdParams* p) {
   return launch_status(fa::launch_preprocess(a, p->head_dim, p->dtype, (hipStream_t)p->stream), "fa_bwd_preprocess");
 }
 
-int fa_bwd(const FaBwdParams* p) {
-  if (!p) return fail(FA_ERR_NULL, "params is NULL");
-  const int split = choose_split(p);
-  int st = check_bwd(p, split);
-  if (st) return st;
-  const hipStream_t s = (hipStream_t)p->stream;
+static fa::BwdArgs bwd_args(const FaBwdParams* p, int split) {
   fa::BwdArgs a{};
   a.q = p->q; a.k = p->k; a.v = p->v; a.dout = p->dout;
   a.lse = p->lse; a.delta = p->delta; a.dead = p->dead_flags;
@@ -258,23 +253,28 @@ int fa_bwd(const FaBwdParams* p) {
   fill_scales(p->scale, &sl2f, &a.qsign, &a.zero_scale, &a.scale_log2);
   a.mask_vec = mask_vec_ok(p->mask, p->mask_stride_b, p->mask_stride_h, p->mask_stride_q);
   a.score_vec = score_vec_ok(p->score, p->score_stride_b, p->score_stride_h, p->score_stride_q);
+  // dS tiles of the deterministic path
+  a.nq32 = (p->seqlen_q + 31) / 32;
+  a.nk32 = (p->seqlen_k + 31) / 32;
+  a.ds = !p->atomic_dq && ds_elems(p) > 0 ? p->ds_tiles : nullptr;
+  a.ds_plane = fa::ds_row(a.nq32, a.nk32, p->is_causal != 0);
+  return a;
+}
+
+int fa_bwd(const FaBwdParams* p) {
+  if (!p) return fail(FA_ERR_NULL, "params is NULL");
+  const int split = choose_split(p);
+  int st = check_bwd(p, split);
+  if (st) return st;
+  const hipStream_t s = (hipStream_t)p->stream;
+  const fa::BwdArgs a = bwd_args(p, split);
   const bool causal = p->is_causal != 0;
 
   if (p->atomic_dq) {
     if ((st = launch_status(fa::launch_bwd_dkdv(a, p->head_dim, p->dtype, causal, s), "dkdv"))) return st;
   } else {
-    const bool via_ds = ds_elems(p) > 0;
-    a.nq32 = (p->seqlen_q + 31) / 32;
-    a.nk32 = (p->seqlen_k + 31) / 32;
-    a.ds = via_ds ? p->ds_tiles : nullptr;
-    a.ds_plane = fa::ds_row(a.nq32, a.nk32, causal);
+    // deterministic path: dK/dV (+ dS tiles) here, dQ in fa_bwd_finalize
     if ((st = launch_status(fa::launch_bwd_dkdv2(a, p->head_dim, p->dtype, causal, s), "dkdv"))) return st;
-    if (via_ds) {
-      a.nqt = (p->seqlen_q + fa::dq_ds_block_rows() - 1) / fa::dq_ds_block_rows();
-      if ((st = launch_status(fa::launch_bwd_dq_ds(a, p->head_dim, p->dtype, causal, s), "dq"))) return st;
-    } else {
-      if ((st = launch_status(fa::launch_bwd_dq(a, p->head_dim, p->dtype, causal, s), "dq"))) return st;
-    }
   }
   return FA_OK;
 }
@@ -285,6 +285,17 @@ int fa_bwd_finalize(const FaBwdParams* p) {
   int st = check_bwd(p, split);
   if (st) return st;
   const hipStream_t s = (hipStream_t)p->stream;
+  if (!p->atomic_dq) {
+    // deterministic dQ: dQ = scale dS K from the tiles fa_bwd stored, or recomputed
+    fa::BwdArgs a = bwd_args(p, split);
+    const bool causal = p->is_causal != 0;
+    if (a.ds) {
+      a.nqt = (p->seqlen_q + fa::dq_ds_block_rows() - 1) / fa::dq_ds_block_rows();
+      if ((st = launch_status(fa::launch_bwd_dq_ds(a, p->head_dim, p->dtype, causal, s), "dq"))) return st;
+    } else {
+      if ((st = launch_status(fa::launch_bwd_dq(a, p->head_dim, p->dtype, causal, s), "dq"))) return st;
+    }
+  }
   if (p->atomic_dq) {
     // dq_accum is head-major [B, Hq, Tq, D]
     const int64_t D = p->head_dim, Tq = p->seqlen_q, Hq = p->heads_q;

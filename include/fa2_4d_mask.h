@@ -130,17 +130,18 @@ int fa_bwd_preprocess(const FaBwdParams* p);
  * `flash_attention_bwd_with_4d_mask_reduce` (python/fa2.py:305-426, launched at
  * :543-547) when atomic_dq = 0.  atomic_dq = 1: one kernel; dK/dV are written in
  * dtype (kv_split = 1) or added to dk_accum/dv_accum, dQ is added to dq_accum.
- * atomic_dq = 0: the dK/dV kernel and a deterministic dQ kernel writing dq in dtype;
- * with plan.ds_elems > 0 the dK/dV kernel also stores dS into ds_tiles and the dQ
- * kernel is dQ = scale dS K over them, otherwise it recomputes S, P and dP.
+ * atomic_dq = 0: the dK/dV kernel only (dK/dV in dtype or per-split slabs); with
+ * plan.ds_elems > 0 it also stores dS into ds_tiles for fa_bwd_finalize.
  * Must follow fa_bwd_preprocess on the same stream. */
 int fa_bwd(const FaBwdParams* p);
 
-/* Backward finalisation: fp32 accumulators -> dtype outputs (dq from dq_accum when
- * atomic_dq = 1; dk, dv from dk_accum/dv_accum when kv_split > 1); launches nothing
- * when neither applies.  Replaces the casts of python/fa2.py:535-536, the group sum
- * of python/fa2.py:548-549 and autograd's cast of the fp32 dQ the reference
- * returns (python/fa2.py:527, 556).  Must follow fa_bwd on the same stream. */
+/* Backward finalisation.  atomic_dq = 1: dq from the fp32 dq_accum; atomic_dq = 0:
+ * the deterministic dQ kernel writing dq in dtype (dQ = scale dS K over ds_tiles
+ * when plan.ds_elems > 0, otherwise recomputing S, P and dP).  Both: dk, dv from
+ * dk_accum/dv_accum when kv_split > 1.  Replaces the casts of python/fa2.py:535-536,
+ * the group sum of python/fa2.py:548-549 and autograd's cast of the fp32 dQ the
+ * reference returns (python/fa2.py:527, 556); the deterministic dQ replaces the dQ
+ * atomics of python/fa2.py:295-297, 420-421.  Must follow fa_bwd on the same stream. */
 int fa_bwd_finalize(const FaBwdParams* p);
 
 /* Fills *plan for the problem in *p (no launch, no GPU access). */
