@@ -18,8 +18,9 @@
 // batch); wave w owns query steps 8 qb + 2 w, + 1 (64 rows) and walks the key
 // steps of 32.  Per step the workgroup stages one K tile (shared, XOR-swizzled
 // for the transpose reads) and each wave its two dS tiles (private) through
-// registers into LDS, two steps ahead of use; the kernel is bound by the HBM
-// reads of the dS tiles.
+// registers into LDS, kSets steps ahead of use; the kernel is bound by the
+// HBM reads of the dS tiles, so it keeps as many bytes in flight as registers
+// allow at two workgroups per CU.
 #include "fa_common.h"
 #include "fa_kernels.h"
 #include "fa_pipe.h"
@@ -32,6 +33,7 @@ using namespace pipe;
 constexpr int kDqWaves = 4;
 constexpr int kDqSteps = 2;                           // 32-row query steps per wave
 constexpr int kDqRows = kDqWaves * kDqSteps * 32;     // query rows per workgroup
+constexpr int kSets = 3;                              // register staging sets: tiles in flight
 
 template <typename T, int D, bool CAUSAL>
 __global__ __launch_bounds__(kDqWaves * 64, 2) void dq_ds_kernel(const BwdArgs a) {
@@ -69,7 +71,6 @@ __global__ __launch_bounds__(kDqWaves * 64, 2) void dq_ds_kernel(const BwdArgs a
   const int s0 = qb * (kDqRows / 32) + wv * kDqSteps;          // this wave's first query step
   const int s_last = min(qb * (kDqRows / 32) + kDqRows / 32, nq32) - 1;
   const int nstep = CAUSAL ? min(s_last + 1, nk32) : nk32;       // key steps of the workgroup
-  const int nstep2 = (nstep + 1) & ~1;
 
   // ---- LDS addresses ---------------------------------------------------------------
   const uint32_t lds0 = (uint32_t)(uintptr_t)(FA_LDS char*)smem;
@@ -105,11 +106,10 @@ __global__ __launch_bounds__(kDqWaves * 64, 2) void dq_ds_kernel(const BwdArgs a
 #pragma unroll
   for (int i = 0; i < kDqSteps; ++i) row0[i] = plane + ds_row(s0 + i, nk32, CAUSAL);
 
-  u32x4 stk[2][UK], std_[2][UD];
+  u32x4 stk[kSets][UK], std_[kSets][UD];
   // Tile kb into staging set S (keys past Tk and dS tiles outside the stored
   // set load as zeros).
-  auto load = [&](auto Sc, int kb) __attribute__((always_inline)) {
-    constexpr int S = decltype(Sc)::value;
+  auto load = [&](int S, int kb) __attribute__((always_inline)) {
     const int rows = kb < nstep ? min(32, Tk - kb * 32) : 0;
     const int nrec = rows > 0 ? (int)((int64_t)(rows - 1) * a.kst * 2 + ROWB) : 0;
     const auto rk = __builtin_amdgcn_make_buffer_rsrc((void*)(kbase + (int64_t)kb * 32 * a.kst), (short)0, nrec, 0x00020000);
@@ -122,12 +122,11 @@ __global__ __launch_bounds__(kDqWaves * 64, 2) void dq_ds_kernel(const BwdArgs a
       const auto rd = __builtin_amdgcn_make_buffer_rsrc((void*)(dsp + (row0[i] + kb) * 1024), (short)0, ok ? 2048 : 0,
                                                         0x00020000);
 #pragma unroll
-      for (int u = 0; u < UD / kDqSteps; ++u)
-        std_[S][i * (UD / kDqSteps) + u] = __builtin_amdgcn_raw_buffer_load_b128(rd, (uint32_t)(lane * 16 + u * 1024), 0, 0);
+      for (int u = 0; u < UD / kDqSteps; ++u)   // non-temporal: each dS tile is read once
+        std_[S][i * (UD / kDqSteps) + u] = __builtin_amdgcn_raw_buffer_load_b128(rd, (uint32_t)(lane * 16 + u * 1024), 0, 2);
     }
   };
-  auto store = [&](auto Sc, auto Bc) __attribute__((always_inline)) {
-    constexpr int S = decltype(Sc)::value, BUF = decltype(Bc)::value;
+  auto store = [&](int S, int BUF) __attribute__((always_inline)) {
 #pragma unroll
     for (int u = 0; u < UK; ++u) lds_wr16(swk[u] + BUF * BUFB, stk[S][u]);
 #pragma unroll
@@ -141,8 +140,7 @@ __global__ __launch_bounds__(kDqWaves * 64, 2) void dq_ds_kernel(const BwdArgs a
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) acc[i][nb] = f32x16{};
 
-  auto compute = [&](auto Bc) __attribute__((always_inline)) {
-    constexpr int BUF = decltype(Bc)::value;
+  auto compute = [&](int BUF) __attribute__((always_inline)) {
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
       V8 bf[kDqSteps];
@@ -161,25 +159,26 @@ __global__ __launch_bounds__(kDqWaves * 64, 2) void dq_ds_kernel(const BwdArgs a
     }
   };
 
-  // ---- prologue: tiles 0, 1 staged, tile 0 in buffer 0, tile 2 loading ----------------
-  load(IC<0>{}, 0);
-  load(IC<1>{}, 1);
-  store(IC<0>{}, IC<0>{});
-  load(IC<0>{}, 2);
+  // ---- prologue: tiles 0 .. kSets-1 loading (tile t in set t % kSets), tile 0 in buffer 0 --
+#pragma unroll
+  for (int t = 0; t < kSets; ++t) load(t, t);
+  store(0, 0);
+  load(0, kSets);
   lds_barrier();
 
-  // ---- main loop: iteration j writes tile j+1 to LDS, loads tile j+3, computes tile j ----
-  int n2 = nstep2;
-  asm volatile("" : "+s"(n2));
-  for (int j = 0; j < n2; j += 2) {
-    store(IC<1>{}, IC<1>{});
-    load(IC<1>{}, j + 3);
-    compute(IC<0>{});
-    lds_barrier();
-    store(IC<0>{}, IC<0>{});
-    load(IC<0>{}, j + 4);
-    compute(IC<1>{});
-    lds_barrier();
+  // ---- main loop: iteration j writes tile j+1 to LDS buffer (j+1)%2, loads tile
+  // j+1+kSets into the set it freed, computes tile j from buffer j%2 ------------------
+  constexpr int U = kSets == 2 ? 2 : 6;   // lcm(kSets, 2): sets and buffers static per copy
+  int nu = (nstep + U - 1) / U * U;
+  asm volatile("" : "+s"(nu));
+  for (int j = 0; j < nu; j += U) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      store((u + 1) % kSets, (u + 1) & 1);
+      load((u + 1) % kSets, j + u + 1 + kSets);
+      compute(u & 1);
+      lds_barrier();
+    }
   }
 
   // ---- epilogue: dQ rows of each query step through LDS, coalesced stores --------------

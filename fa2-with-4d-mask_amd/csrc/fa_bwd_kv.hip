@@ -343,8 +343,8 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
       // stream 1: S / dP of step j+1 (ds = t/2)
       if ((t & 1) == 0) sacc[PN] = mfma32(as_vec8<T>(xs[t % AHEAD]), kf[t >> 1], (t >> 1) == 0 ? f32x16{} : sacc[PN]);
       else pacc[PN] = mfma32(as_vec8<T>(xs[t % AHEAD]), vf[t >> 1], (t >> 1) == 0 ? nd_next : pacc[PN]);
-      // dS of step j-1 out to its tile
-      if (t < 2) __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, dspk[PN][t]), ds_rs, ds_vo + 32 * t, 0, 0);
+      // dS of step j-1 out to its tile (non-temporal: read once, by the dQ kernel)
+      if (t < 2) __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, dspk[PN][t]), ds_rs, ds_vo + 32 * t, 0, 2);
       // stream 2: dV / dK of step j-1 (c, nb)
       {
         const int c = t / (2 * NB), nb = (t / 2) % NB;
