@@ -21,7 +21,12 @@ read from profiles/dkdv2_H_traffic.json, written from rocprofv3 FETCH_SIZE /
 WRITE_SIZE runs scaled by a copy-kernel calibration.  ``cpu_baseline`` times
 this repository's eager fp32 oracle on the host cores on a bounded sample.
 
-Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline]
+The other BASELINE configs (P: packed-document mask, S: score + sparse mask,
+M: MQA long KV, bshd) are timed after the headline and reported under
+``configs`` with dense-convention TFLOPS and GB/s against their algorithmic
+bytes (each tensor once; mask at its passed head count).
+
+Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline] [--no-side-configs]
 """
 
 from __future__ import annotations
@@ -61,6 +66,66 @@ def make_inputs(torch, dev):
     v = torch.randn((B, T, HK, D), generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
     do = torch.randn((B, T, HQ, D), generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
     return q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), do.transpose(1, 2)
+
+
+def packed_docs_mask(torch, dev, batch: int, t: int, gen, lo: int = 128, hi: int = 1024):
+    """[batch, 1, t, t] block-diagonal causal keep-mask of packed documents
+    segment lengths uniform in [lo, hi], last one truncated."""
+    seg = torch.empty((batch, t), dtype=torch.int32)
+    for bi in range(batch):
+        pos, sid = 0, 0
+        while pos < t:
+            n = int(torch.randint(lo, hi + 1, (1,), generator=gen).item())
+            seg[bi, pos:pos + n] = sid
+            pos, sid = pos + n, sid + 1
+    seg = seg.to(dev)
+    keep = (seg[:, :, None] == seg[:, None, :]) & torch.ones((t, t), dtype=torch.bool, device=dev).tril()
+    return keep.unsqueeze(1).contiguous()
+
+
+def side_configs(torch, dev):
+    """The other BASELINE configs as bench lines: P (packed-document mask), S
+    (score + sparse mask), M (MQA, long KV, bshd).  Yields (name, inputs)."""
+    g = torch.Generator(device="cpu")
+    g.manual_seed(0)
+
+    def rnd(shape):
+        return torch.randn(shape, generator=g).to(torch.bfloat16).to(dev)
+
+    # P: B2 T4096 Hq32 Hk8 D128, mask [2, 1, T, T]
+    b, t, hq, hk, d = 2, 4096, 32, 8, 128
+    q, k, v, do = rnd((b, t, hq, d)), rnd((b, t, hk, d)), rnd((b, t, hk, d)), rnd((b, t, hq, d))
+    mask = packed_docs_mask(torch, dev, b, t, g)
+    yield "P", dict(q=q.transpose(1, 2), k=k.transpose(1, 2), v=v.transpose(1, 2), do=do.transpose(1, 2),
+                    mask=mask, score=None, layout="bhsd", dims=(b, t, t, hq, hk, d))
+    del q, k, v, do, mask
+    # S: B1 T4096 Hq=Hk=16 D128, score [1,16,T,T] fp32 (ALiBi + N(0, 0.1)), mask [1,16,T,T] (p_drop 0.1, diag kept)
+    b, t, hq, hk, d = 1, 4096, 16, 16, 128
+    q, k, v, do = rnd((b, t, hq, d)), rnd((b, t, hk, d)), rnd((b, t, hk, d)), rnd((b, t, hq, d))
+    slopes = torch.tensor([2.0 ** (-8.0 * (h + 1) / hq) for h in range(hq)], device=dev).view(1, hq, 1, 1)
+    idx = torch.arange(t, device=dev, dtype=torch.float32)
+    score = -slopes * (idx[:, None] - idx[None, :]).abs() + 0.1 * torch.randn((b, hq, t, t), generator=g).to(dev)
+    mask = torch.rand((b, hq, t, t), generator=g).to(dev) >= 0.1
+    mask[:, :, torch.arange(t), torch.arange(t)] = True
+    yield "S", dict(q=q.transpose(1, 2), k=k.transpose(1, 2), v=v.transpose(1, 2), do=do.transpose(1, 2),
+                    mask=mask.contiguous(), score=score.contiguous(), layout="bhsd", dims=(b, t, t, hq, hk, d))
+    del q, k, v, do, mask, score
+    # M: B1 Tq2048 Tk16384 Hq32 Hk1 D64, bshd
+    b, tq, tk, hq, hk, d = 1, 2048, 16384, 32, 1, 64
+    yield "M", dict(q=rnd((b, tq, hq, d)), k=rnd((b, tk, hk, d)), v=rnd((b, tk, hk, d)), do=rnd((b, tq, hq, d)),
+                    mask=None, score=None, layout="bshd", dims=(b, tq, tk, hq, hk, d))
+
+
+def side_bytes(x, mode: str) -> float:
+    """Algorithmic HBM bytes: every tensor once (Q, K, V, O, LSE, mask at its
+    passed head count, score); fwd+bwd adds dO, dQ, dK, dV, Delta and a second
+    read of mask/score."""
+    b, tq, tk, hq, hk, d = x["dims"]
+    side = (x["mask"].numel() if x["mask"] is not None else 0) + 4 * (x["score"].numel() if x["score"] is not None else 0)
+    fwd = 2 * d * (2 * b * tq * hq + 2 * b * tk * hk) + 4 * b * hq * tq + side
+    if mode == "fwd":
+        return float(fwd)
+    return float(fwd + 2 * d * (2 * b * tq * hq + 2 * b * tk * hk) + 4 * b * hq * tq + side)
 
 
 def time_steps(torch, fn, steps: int, warmup: int, record_events):
@@ -121,6 +186,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-side-configs", action="store_true",
+                    help="skip the P / S / M config lines (mask, score+mask, MQA)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     args = ap.parse_args()
     if args.gpus != 1:
@@ -171,6 +238,47 @@ def main() -> int:
                          "kernel_ms": {k2: round(v2, 4) for k2, v2 in kern.items()}}
         log(f"{name:22s} {ms:8.3f} ms  {tf:8.1f} TFLOPS  ({100 * tf / PEAK_TFLOPS:5.1f}% of peak)  kernels {kern}")
 
+    side = {}
+    if not args.no_side_configs:
+        del q, k, v
+        for name, x in side_configs(torch, dev):
+            bq, tq, tk, hq, hk, d = x["dims"]
+            flops_fwd = 4.0 * bq * hq * tq * tk * d
+            xq = x["q"].detach().requires_grad_(True)
+            xk = x["k"].detach().requires_grad_(True)
+            xv = x["v"].detach().requires_grad_(True)
+            kw = dict(mask=x["mask"], score=x["score"], layout=x["layout"])
+
+            def sfwd():
+                with torch.no_grad():
+                    api.tilelang_flash_attention(x["q"], x["k"], x["v"], **kw)
+
+            def sfb(atomic):
+                def f():
+                    xq.grad = xk.grad = xv.grad = None
+                    api.tilelang_flash_attention(xq, xk, xv, use_atomic_backward=atomic, **kw).backward(x["do"])
+                return f
+
+            entry = {}
+            for mode, fn in (("fwd", sfwd), ("fwd_bwd", sfb(False)), ("fwd_bwd_atomic", sfb(True))):
+                ms, kern = time_steps(torch, fn, max(3, args.steps // 2), max(1, args.warmup // 2), record_kernel_events)
+                fl = flops_fwd * (1.0 if mode == "fwd" else 3.5)
+                nbytes = side_bytes(x, "fwd" if mode == "fwd" else "fwd_bwd")
+                entry[mode] = {"ms": round(ms, 4), "tflops_dense_conv": round(fl / (ms * 1e-3) * 1e-12, 2),
+                               "frac_of_peak": round(fl / (ms * 1e-3) * 1e-12 / PEAK_TFLOPS, 4),
+                               "alg_bytes": nbytes, "gbps": round(nbytes / (ms * 1e-3) * 1e-9, 1),
+                               "kernel_ms": {k2: round(v2, 4) for k2, v2 in kern.items()}}
+                log(f"{name} {mode:15s} {ms:8.3f} ms  {entry[mode]['tflops_dense_conv']:8.1f} TFLOPS (dense conv.)"
+                    f"  {entry[mode]['gbps']:8.1f} GB/s of {nbytes / 1e9:.3f} GB algorithmic  kernels {kern}")
+            if x["mask"] is not None:
+                entry["mask_keep_fraction"] = round(x["mask"].float().mean().item(), 4)
+            entry["config"] = {"B": bq, "Tq": tq, "Tk": tk, "Hq": hq, "Hk": hk, "D": d, "layout": x["layout"],
+                               "mask": None if x["mask"] is None else list(x["mask"].shape),
+                               "score": None if x["score"] is None else list(x["score"].shape)}
+            side[name] = entry
+            del x, xq, xk, xv
+            torch.cuda.empty_cache()
+
     main_res = results["fwd_bwd"]
     # dominant kernel: dK/dV (fa_bwd on the deterministic path), 4 GEMMs
     dkdv_ms = main_res["kernel_ms"]["fa_bwd"]
@@ -217,6 +325,7 @@ def main() -> int:
             "layout": "bhsd", "scale": "D^-0.5", "parallelism": "single GPU",
         },
         "breakdown": results,
+        "configs": side,
         "roofline": {
             "kernel": "dkdv2_kernel<bf16,128> via fa_bwd (dK/dV + dS tiles, deterministic path)",
             "bound": "mfma",
