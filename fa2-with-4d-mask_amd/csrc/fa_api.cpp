@@ -73,33 +73,69 @@ int score_vec_ok(const float* s, int64_t sb, int64_t sh, int64_t sq) {
   return s && ((uintptr_t)s % 16 == 0) && sb % 4 == 0 && sh % 4 == 0 && sq % 4 == 0;
 }
 
+fa::MaskLayout layout_of(int32_t B, int32_t Hq, int32_t Tq, int32_t Tk, int64_t msb, int64_t msh) {
+  return fa::mask_layout(B, Hq, Tq, Tk, msb == 0, msh == 0);
+}
+
+// A prepared mask is required beside a mask; it must be 256-byte aligned.
+int check_mask_ws(const uint8_t* mask, const void* ws) {
+  if (!mask) return FA_OK;
+  if (!ws) return fail(FA_ERR_WORKSPACE, "a mask needs its prepared workspace (fa_mask_prepare): mask_ws is NULL");
+  if ((uintptr_t)ws % 256) return fail(FA_ERR_STRIDE, "mask_ws must be 256-byte aligned");
+  return FA_OK;
+}
+
 int launch_status(hipError_t e, const char* what) {
   if (e != hipSuccess) return fail(FA_ERR_LAUNCH, "%s launch failed: %s", what, hipGetErrorString(e));
   return FA_OK;
 }
 
-int choose_split(const FaBwdParams* p) {
-  if (p->kv_split > 0) return p->kv_split;
-  const int G = p->heads_q / p->heads_k;
-  const int kb = p->atomic_dq ? fa::dkdv_block_keys() : fa::dkdv2_block_keys();
-  const int nkt = (p->seqlen_k + kb - 1) / kb;
-  const int64_t base = (int64_t)p->batch * p->heads_k * nkt;
-  const int64_t target = 512;  // two workgroups per CU on a 256-CU part
-  int split = 1;
-  while (split * 2 <= G && G % (split * 2) == 0 && base * split < target) split *= 2;
-  return split;
-}
-
-// Deterministic path: 16-bit dS tiles of every stored 32x32 block (causal:
-// blocks on or below the diagonal), when they fit the caller's limit.
+// dS tiles (16-bit, every stored 32x32 block; causal: blocks on or below the
+// diagonal) handed from the dK/dV kernel to the dQ kernel, when they fit the
+// caller's limit.
 int64_t ds_elems(const FaBwdParams* p) {
-  if (p->atomic_dq) return 0;
   const int64_t limit = p->ds_limit_bytes == 0 ? (int64_t)8 << 30 : p->ds_limit_bytes;
   if (limit < 0) return 0;
   const int64_t nq32 = (p->seqlen_q + 31) / 32, nk32 = (p->seqlen_k + 31) / 32;
   const int64_t plane = fa::ds_row(nq32, nk32, p->is_causal != 0);
   const int64_t elems = (int64_t)p->batch * p->heads_q * plane * 1024;
   return 2 * elems <= limit ? elems : 0;
+}
+
+// How the backward runs.  With the dS tiles: the pipelined dK/dV kernel
+// stores dS and a dQ kernel streams it, writing dQ (deterministic) or adding
+// fp32 partials over key ranges atomically (atomic).  Without them: the fused
+// dK/dV kernel with fp32-atomic dQ (atomic), or a dQ kernel that recomputes
+// S, P and dP (deterministic).
+enum Route { kDsAtomic, kDsDet, kFusedAtomic, kRecomputeDet };
+Route route_of(const FaBwdParams* p) {
+  const bool ds = ds_elems(p) > 0;
+  if (p->atomic_dq) return ds ? kDsAtomic : kFusedAtomic;
+  return ds ? kDsDet : kRecomputeDet;
+}
+
+// Key ranges of the atomic dQ-from-dS kernel: at least 2, more while the grid
+// is below ~1024 workgroups and each range keeps >= 4 key steps.
+int dq_split_of(const FaBwdParams* p) {
+  if (route_of(p) != kDsAtomic) return 1;
+  const int64_t nblk = (int64_t)p->batch * p->heads_q * ((p->seqlen_q + fa::dq_ds_block_rows() - 1) / fa::dq_ds_block_rows());
+  const int nks = (p->seqlen_k + 31) / 32;
+  if (nks < 2) return 1;
+  int split = 2;
+  while (split < 8 && nblk * split < 1024 && nks / (2 * split) >= 4) split *= 2;
+  return split;
+}
+
+int choose_split(const FaBwdParams* p) {
+  if (p->kv_split > 0) return p->kv_split;
+  const int G = p->heads_q / p->heads_k;
+  const int kb = route_of(p) == kFusedAtomic ? fa::dkdv_block_keys() : fa::dkdv2_block_keys();
+  const int nkt = (p->seqlen_k + kb - 1) / kb;
+  const int64_t base = (int64_t)p->batch * p->heads_k * nkt;
+  const int64_t target = 512;  // two workgroups per CU on a 256-CU part
+  int split = 1;
+  while (split * 2 <= G && G % (split * 2) == 0 && base * split < target) split *= 2;
+  return split;
 }
 
 void fill_scales(float scale, float* scale_log2_fwd, float* qsign, int* zero, float* scale_log2_bwd) {
@@ -116,6 +152,47 @@ extern "C" {
 
 int fa_abi_version(void) { return FA_ABI_VERSION; }
 
+static int check_mask_params(const FaMaskParams* p) {
+  if (!p) return fail(FA_ERR_NULL, "params is NULL");
+  if (p->batch < 1 || p->seqlen_q < 1 || p->seqlen_k < 1 || p->heads_q < 1)
+    return fail(FA_ERR_SHAPE, "sizes must be >= 1 (B=%d Tq=%d Tk=%d Hq=%d)", p->batch, p->seqlen_q, p->seqlen_k,
+                p->heads_q);
+  if (!p->mask) return fail(FA_ERR_NULL, "mask is NULL");
+  if (p->mask_stride_b < 0 || p->mask_stride_h < 0 || p->mask_stride_q < 0)
+    return fail(FA_ERR_STRIDE, "mask strides must be non-negative");
+  const fa::MaskLayout ml = layout_of(p->batch, p->heads_q, p->seqlen_q, p->seqlen_k, p->mask_stride_b,
+                                      p->mask_stride_h);
+  if ((int64_t)ml.Bm * ml.Hm > 65535 || (p->seqlen_q + 127) / 128 > 65535)
+    return fail(FA_ERR_SHAPE, "mask too large for the preparation grid (planes %d x %d, Tq %d)", ml.Bm, ml.Hm,
+                p->seqlen_q);
+  return FA_OK;
+}
+
+int fa_mask_plan(const FaMaskParams* p, int64_t* workspace_bytes) {
+  int st = check_mask_params(p);
+  if (st) return st;
+  if (!workspace_bytes) return fail(FA_ERR_NULL, "workspace_bytes is NULL");
+  *workspace_bytes = layout_of(p->batch, p->heads_q, p->seqlen_q, p->seqlen_k, p->mask_stride_b, p->mask_stride_h).total;
+  return FA_OK;
+}
+
+int fa_mask_prepare(const FaMaskParams* p) {
+  int st = check_mask_params(p);
+  if (st) return st;
+  if (!p->workspace) return fail(FA_ERR_WORKSPACE, "workspace is NULL");
+  if ((uintptr_t)p->workspace % 256) return fail(FA_ERR_STRIDE, "workspace must be 256-byte aligned");
+  fa::MaskArgs a{};
+  a.mask = p->mask;
+  a.msb = p->mask_stride_b; a.msh = p->mask_stride_h; a.msq = p->mask_stride_q;
+  a.Tq = p->seqlen_q; a.Tk = p->seqlen_k;
+  a.is_causal = p->is_causal != 0;
+  a.vec16 = ((uintptr_t)p->mask % 16 == 0) && p->mask_stride_b % 16 == 0 && p->mask_stride_h % 16 == 0 &&
+            p->mask_stride_q % 16 == 0;
+  a.ws = (char*)p->workspace;
+  a.ml = layout_of(p->batch, p->heads_q, p->seqlen_q, p->seqlen_k, p->mask_stride_b, p->mask_stride_h);
+  return launch_status(fa::launch_mask_prepare(a, (hipStream_t)p->stream), "fa_mask_prepare");
+}
+
 const char* fa_last_error(void) { return g_err; }
 
 int fa_fwd(const FaFwdParams* p) {
@@ -130,6 +207,7 @@ int fa_fwd(const FaFwdParams* p) {
   if ((st = check_mask_score(p->mask, p->mask_stride_b, p->mask_stride_h, p->mask_stride_q, p->score,
                              p->score_stride_b, p->score_stride_h, p->score_stride_q)))
     return st;
+  if ((st = check_mask_ws(p->mask, p->mask_ws))) return st;
 
   // The forward stages K/V tiles with 32-bit buffer offsets (64 rows of a tile).
   if (p->k_stride_t < 0 || p->k_stride_t >= (1LL << 24) || p->v_stride_t < 0 || p->v_stride_t >= (1LL << 24))
@@ -152,6 +230,10 @@ int fa_fwd(const FaFwdParams* p) {
   fill_scales(p->scale, &a.scale_log2, &a.qsign, &a.zero_scale, &sl2b);
   a.mask_vec = mask_vec_ok(p->mask, p->mask_stride_b, p->mask_stride_h, p->mask_stride_q);
   a.score_vec = score_vec_ok(p->score, p->score_stride_b, p->score_stride_h, p->score_stride_q);
+  if (p->mask) {
+    a.mws = (const char*)p->mask_ws;
+    a.ml = layout_of(p->batch, p->heads_q, p->seqlen_q, p->seqlen_k, p->mask_stride_b, p->mask_stride_h);
+  }
   return launch_status(fa::launch_fwd(a, p->head_dim, p->dtype, p->is_causal != 0, (hipStream_t)p->stream), "fa_fwd");
 }
 
@@ -187,8 +269,9 @@ static int check_bwd(const FaBwdParams* p, int split) {
     return fail(FA_ERR_WORKSPACE, "kv_split %d needs dk_accum and dv_accum", split);
   if (split > 1 && (!aligned16(p->dk_accum) || !aligned16(p->dv_accum)))
     return fail(FA_ERR_STRIDE, "dk_accum/dv_accum must be 16-byte aligned");
-  if (ds_elems(p) > 0 && !p->ds_tiles) return fail(FA_ERR_WORKSPACE, "deterministic dQ needs ds_tiles");
+  if (ds_elems(p) > 0 && !p->ds_tiles) return fail(FA_ERR_WORKSPACE, "dQ from dS tiles needs ds_tiles (plan.ds_elems)");
   if (ds_elems(p) > 0 && !aligned16(p->ds_tiles)) return fail(FA_ERR_STRIDE, "ds_tiles must be 16-byte aligned");
+  if ((st = check_mask_ws(p->mask, p->mask_ws))) return st;
   return check_mask_score(p->mask, p->mask_stride_b, p->mask_stride_h, p->mask_stride_q, p->score,
                           p->score_stride_b, p->score_stride_h, p->score_stride_q);
 }
@@ -200,14 +283,17 @@ int fa_bwd_plan(const FaBwdParams* p, FaBwdPlan* plan) {
   const int split = choose_split(p);
   const int G = p->heads_q / p->heads_k;
   if (split < 1 || G % split != 0) return fail(FA_ERR_SHAPE, "kv_split %d must divide the group size %d", split, G);
+  const Route r = route_of(p);
   plan->kv_split = split;
   plan->needs_dq_accum = p->atomic_dq ? 1 : 0;
   plan->dq_accum_elems = p->atomic_dq ? (int64_t)p->batch * p->seqlen_q * p->heads_q * p->head_dim : 0;
-  // atomic dQ: one zeroed fp32 accumulator for dK and one for dV; deterministic
-  // path: one slab per split, fully overwritten (no zeroing needed).
+  // fused atomic kernel: one zeroed fp32 accumulator for dK and one for dV;
+  // pipelined dK/dV kernel: one slab per split, fully overwritten.
+  plan->dkv_accum_zeroed = split > 1 && r == kFusedAtomic ? 1 : 0;
   plan->dkv_accum_elems =
-      split > 1 ? (int64_t)(p->atomic_dq ? 1 : split) * p->batch * p->seqlen_k * p->heads_k * p->head_dim : 0;
+      split > 1 ? (int64_t)(r == kFusedAtomic ? 1 : split) * p->batch * p->seqlen_k * p->heads_k * p->head_dim : 0;
   plan->ds_elems = ds_elems(p);
+  plan->dq_split = dq_split_of(p);
   return FA_OK;
 }
 
@@ -248,6 +334,7 @@ static fa::BwdArgs bwd_args(const FaBwdParams* p, int split) {
   a.nqt = (p->seqlen_q + fa::dq_block_rows() - 1) / fa::dq_block_rows();
   a.split = split;
   a.do_dq = p->atomic_dq ? 1 : 0;
+  a.dq_split = dq_split_of(p);
   a.scale = p->scale;
   float sl2f;
   fill_scales(p->scale, &sl2f, &a.qsign, &a.zero_scale, &a.scale_log2);
@@ -256,8 +343,12 @@ static fa::BwdArgs bwd_args(const FaBwdParams* p, int split) {
   // dS tiles of the deterministic path
   a.nq32 = (p->seqlen_q + 31) / 32;
   a.nk32 = (p->seqlen_k + 31) / 32;
-  a.ds = !p->atomic_dq && ds_elems(p) > 0 ? p->ds_tiles : nullptr;
+  a.ds = ds_elems(p) > 0 ? p->ds_tiles : nullptr;
   a.ds_plane = fa::ds_row(a.nq32, a.nk32, p->is_causal != 0);
+  if (p->mask) {
+    a.mws = (const char*)p->mask_ws;
+    a.ml = layout_of(p->batch, p->heads_q, p->seqlen_q, p->seqlen_k, p->mask_stride_b, p->mask_stride_h);
+  }
   return a;
 }
 
@@ -270,10 +361,10 @@ int fa_bwd(const FaBwdParams* p) {
   const fa::BwdArgs a = bwd_args(p, split);
   const bool causal = p->is_causal != 0;
 
-  if (p->atomic_dq) {
+  if (route_of(p) == kFusedAtomic) {
     if ((st = launch_status(fa::launch_bwd_dkdv(a, p->head_dim, p->dtype, causal, s), "dkdv"))) return st;
   } else {
-    // deterministic path: dK/dV (+ dS tiles) here, dQ in fa_bwd_finalize
+    // pipelined dK/dV (+ dS tiles when the plan has them) here, dQ in fa_bwd_finalize
     if ((st = launch_status(fa::launch_bwd_dkdv2(a, p->head_dim, p->dtype, causal, s), "dkdv"))) return st;
   }
   return FA_OK;
@@ -285,8 +376,10 @@ int fa_bwd_finalize(const FaBwdParams* p) {
   int st = check_bwd(p, split);
   if (st) return st;
   const hipStream_t s = (hipStream_t)p->stream;
-  if (!p->atomic_dq) {
-    // deterministic dQ: dQ = scale dS K from the tiles fa_bwd stored, or recomputed
+  const Route r = route_of(p);
+  if (r != kFusedAtomic) {
+    // dQ = scale dS K from the tiles fa_bwd stored (written, or added over key
+    // ranges with fp32 atomics), or recomputed
     fa::BwdArgs a = bwd_args(p, split);
     const bool causal = p->is_causal != 0;
     if (a.ds) {
@@ -304,8 +397,8 @@ int fa_bwd_finalize(const FaBwdParams* p) {
     if ((st = launch_status(fa::launch_convert(c, p->dtype, s), "dq convert"))) return st;
   }
   if (split > 1) {
-    // atomic path: one zeroed accumulator; deterministic path: one slab per split.
-    const int nslab = p->atomic_dq ? 1 : split;
+    // fused atomic kernel: one zeroed accumulator; pipelined dK/dV kernel: one slab per split.
+    const int nslab = r == kFusedAtomic ? 1 : split;
     const int64_t slab = (int64_t)p->batch * p->seqlen_k * p->heads_k * p->head_dim;
     const int64_t D = p->head_dim, Tk = p->seqlen_k, Hk = p->heads_k;
     fa::CvtArgs ck{p->dk_accum, p->dk, p->dk_stride_b, p->dk_stride_t, p->dk_stride_h,

@@ -15,8 +15,13 @@
 // l = position p directly, so perm only matters when dQ rows are stored.
 //
 // Work decomposition: one workgroup of 4 waves per (256 query rows, head,
-// batch); wave w owns query steps 8 qb + 2 w, + 1 (64 rows) and walks the key
-// steps of 32.  Per step the workgroup stages one K tile (shared, XOR-swizzled
+// batch[, key split]); wave w owns query steps 8 qb + 2 w, + 1 (64 rows) and
+// walks the key steps of 32.  Deterministic: one workgroup covers every key
+// step and stores dQ.  Atomic (use_atomic_backward): the key steps are cut
+// into dq_split contiguous ranges and each workgroup adds its fp32 partial
+// dQ into the zeroed accumulator with fp32 atomics, one coalesced row segment
+// per instruction (the reference adds a partial per 64-key block,
+// python/fa2.py:295-297, which on this part is bound by atomic throughput).  Per step the workgroup stages one K tile (shared, XOR-swizzled
 // for the transpose reads) and each wave its two dS tiles (private) through
 // registers into LDS, kSets steps ahead of use; the kernel is bound by the
 // HBM reads of the dS tiles, so it keeps as many bytes in flight as registers
@@ -35,7 +40,7 @@ constexpr int kDqSteps = 2;                           // 32-row query steps per 
 constexpr int kDqRows = kDqWaves * kDqSteps * 32;     // query rows per workgroup
 constexpr int kSets = 3;                              // register staging sets: tiles in flight
 
-template <typename T, int D, bool CAUSAL>
+template <typename T, int D, bool CAUSAL, bool MASK, bool ATOMIC>
 __global__ __launch_bounds__(kDqWaves * 64, 2) void dq_ds_kernel(const BwdArgs a) {
   using V8 = typename Vec8<T>::type;
   constexpr int NB = D / 32, CH = D / 8, ROWB = 2 * D;
@@ -47,14 +52,20 @@ __global__ __launch_bounds__(kDqWaves * 64, 2) void dq_ds_kernel(const BwdArgs a
   constexpr int OS = D + 8;                          // epilogue staging stride (elements)
   static_assert(UK >= 1 && UD >= 1, "tile split");
   static_assert(kDqWaves * 32 * OS * 2 <= 2 * BUFB, "epilogue staging fits");
-  __shared__ __attribute__((aligned(1024))) char smem[2 * BUFB];
+  static_assert(kDqRows == kDqDsRows, "prepared-mask lists are built for this shape");
+  constexpr int OSF = D + 4;                         // atomic epilogue: fp32 staging stride
+  constexpr int SMEM = ATOMIC && kDqWaves * 32 * OSF * 4 > 2 * BUFB ? kDqWaves * 32 * OSF * 4 : 2 * BUFB;
+  __shared__ __attribute__((aligned(1024))) char smem[SMEM];
 
   // ---- which (batch, head, 256-row block) ----------------------------------------
   // Logical order: kv-head major (the heads of a group share K in L2), longest
   // causal blocks first.
   const int nqb = a.nqt;
-  const int nblk = a.B * a.Hq * nqb;
-  const int W = xcd_remap(blockIdx.x, nblk);
+  const int nsp = ATOMIC ? a.dq_split : 1;
+  const int nblk = a.B * a.Hq * nqb * nsp;
+  const int W0 = xcd_remap(blockIdx.x, nblk);
+  const int W = ATOMIC ? W0 / nsp : W0;
+  const int ksp = ATOMIC ? W0 - W * nsp : 0;        // key split of this workgroup
   const int per_kv = a.G * nqb;
   const int bk = W / per_kv;
   const int rem = W - bk * per_kv;
@@ -70,7 +81,21 @@ __global__ __launch_bounds__(kDqWaves * 64, 2) void dq_ds_kernel(const BwdArgs a
   const int Tq = a.Tq, Tk = a.Tk, nk32 = a.nk32, nq32 = a.nq32;
   const int s0 = qb * (kDqRows / 32) + wv * kDqSteps;          // this wave's first query step
   const int s_last = min(qb * (kDqRows / 32) + kDqRows / 32, nq32) - 1;
-  const int nstep = CAUSAL ? min(s_last + 1, nk32) : nk32;       // key steps of the workgroup
+  // Key steps of the workgroup: 0 .. nstep-1, or with a mask the live steps of
+  // the prepared list (causality folded in).  A dS tile is read only where the
+  // dK/dV kernel stored it: its 32x32 block holds a kept entry.
+  const int32_t* dql = nullptr;
+  const uint8_t* blk = nullptr;
+  if constexpr (MASK) {
+    const int pm = mask_plane(a.ml, b, h);
+    dql = (const int32_t*)(a.mws + a.ml.ldq + pm * a.ml.pldq) + (int64_t)qb * (1 + nk32);
+    blk = (const uint8_t*)(a.mws + a.ml.blk + pm * a.ml.pblk);
+  }
+  const int nstep = MASK ? dql[0] : (CAUSAL ? min(s_last + 1, nk32) : nk32);
+  // positions [jb, jb + nloc) of that sequence are this workgroup's
+  const int chunk = (nstep + nsp - 1) / nsp;
+  const int jb = min(nstep, ksp * chunk);
+  const int nloc = min(nstep, jb + chunk) - jb;
 
   // ---- LDS addresses ---------------------------------------------------------------
   const uint32_t lds0 = (uint32_t)(uintptr_t)(FA_LDS char*)smem;
@@ -107,10 +132,14 @@ __global__ __launch_bounds__(kDqWaves * 64, 2) void dq_ds_kernel(const BwdArgs a
   for (int i = 0; i < kDqSteps; ++i) row0[i] = plane + ds_row(s0 + i, nk32, CAUSAL);
 
   u32x4 stk[kSets][UK], std_[kSets][UD];
-  // Tile kb into staging set S (keys past Tk and dS tiles outside the stored
-  // set load as zeros).
-  auto load = [&](int S, int kb) __attribute__((always_inline)) {
-    const int rows = kb < nstep ? min(32, Tk - kb * 32) : 0;
+  // Key step at local position jl (position jb + jl) into staging set S (keys
+  // past Tk and dS tiles outside the stored set load as zeros; jl >= nloc
+  // loads nothing).
+  auto load = [&](int S, int jl) __attribute__((always_inline)) {
+    const bool inr = jl < nloc;
+    const int j = jb + jl;
+    const int kb = MASK ? (inr ? dql[1 + j] : 0) : j;
+    const int rows = inr ? min(32, Tk - kb * 32) : 0;
     const int nrec = rows > 0 ? (int)((int64_t)(rows - 1) * a.kst * 2 + ROWB) : 0;
     const auto rk = __builtin_amdgcn_make_buffer_rsrc((void*)(kbase + (int64_t)kb * 32 * a.kst), (short)0, nrec, 0x00020000);
 #pragma unroll
@@ -118,7 +147,8 @@ __global__ __launch_bounds__(kDqWaves * 64, 2) void dq_ds_kernel(const BwdArgs a
 #pragma unroll
     for (int i = 0; i < kDqSteps; ++i) {
       const int s = s0 + i;
-      const bool ok = kb < nstep && s < nq32 && (!CAUSAL || kb <= s);
+      bool ok = inr && s < nq32 && (!CAUSAL || kb <= s);
+      if constexpr (MASK) ok = ok && blk[(int64_t)s * nk32 + kb] != 0;
       const auto rd = __builtin_amdgcn_make_buffer_rsrc((void*)(dsp + (row0[i] + kb) * 1024), (short)0, ok ? 2048 : 0,
                                                         0x00020000);
 #pragma unroll
@@ -169,7 +199,7 @@ __global__ __launch_bounds__(kDqWaves * 64, 2) void dq_ds_kernel(const BwdArgs a
   // ---- main loop: iteration j writes tile j+1 to LDS buffer (j+1)%2, loads tile
   // j+1+kSets into the set it freed, computes tile j from buffer j%2 ------------------
   constexpr int U = kSets == 2 ? 2 : 6;   // lcm(kSets, 2): sets and buffers static per copy
-  int nu = (nstep + U - 1) / U * U;
+  int nu = (nloc + U - 1) / U * U;
   asm volatile("" : "+s"(nu));
   for (int j = 0; j < nu; j += U) {
 #pragma unroll
@@ -183,9 +213,38 @@ __global__ __launch_bounds__(kDqWaves * 64, 2) void dq_ds_kernel(const BwdArgs a
 
   // ---- epilogue: dQ rows of each query step through LDS, coalesced stores --------------
   const float scale = a.scale;
+  const int qrow_l = 16 * (l32 >> 4) + 4 * ((l32 >> 3) & 1) + 8 * ((l32 >> 2) & 1) + (l32 & 3);
+  if constexpr (ATOMIC) {
+    if (nloc == 0) return;   // no key step: nothing to add
+    // fp32 partial rows [32][D] per step, then 64 consecutive floats per atomic instruction
+    float* stf = (float*)smem + wv * 32 * OSF;
+    float* dqa = a.dq_accum + ((int64_t)b * a.Hq + h) * Tq * D;
+#pragma unroll
+    for (int i = 0; i < kDqSteps; ++i) {
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int gi = 0; gi < 4; ++gi) {
+          f32x4 v;
+#pragma unroll
+          for (int t = 0; t < 4; ++t) v[t] = acc[i][nb][gi * 4 + t] * scale;
+          *(FA_LDS f32x4*)(uintptr_t)(stf + qrow_l * OSF + nb * 32 + gi * 8 + hf * 4) = v;
+        }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      const int q0 = (s0 + i) * 32;
+#pragma unroll 4
+      for (int u = 0; u < 32 * D / 64; ++u) {
+        const int idx = lane + u * 64, r = idx / D, c = idx % D;
+        const float v = *(const FA_LDS float*)(uintptr_t)(stf + r * OSF + c);
+        if (q0 + r < Tq) unsafeAtomicAdd(dqa + (int64_t)(q0 + r) * D + c, v);
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    }
+    return;
+  }
   T* stg = (T*)smem + wv * 32 * OS;
   T* dqp = (T*)a.dq + b * a.dqsb + h * a.dqsh;
-  const int qrow = 16 * (l32 >> 4) + 4 * ((l32 >> 3) & 1) + 8 * ((l32 >> 2) & 1) + (l32 & 3);
+  const int qrow = qrow_l;
 #pragma unroll
   for (int i = 0; i < kDqSteps; ++i) {
 #pragma unroll
@@ -207,11 +266,17 @@ __global__ __launch_bounds__(kDqWaves * 64, 2) void dq_ds_kernel(const BwdArgs a
   }
 }
 
+template <typename T, int D, bool CAUSAL, bool ATOMIC>
+hipError_t launch_a(const BwdArgs& a, hipStream_t s) {
+  const dim3 grid((unsigned)(a.B * a.Hq * a.nqt * (ATOMIC ? a.dq_split : 1))), block(kDqWaves * 64);
+  if (a.mask) hipLaunchKernelGGL((dq_ds_kernel<T, D, CAUSAL, true, ATOMIC>), grid, block, 0, s, a);
+  else hipLaunchKernelGGL((dq_ds_kernel<T, D, CAUSAL, false, ATOMIC>), grid, block, 0, s, a);
+  return hipGetLastError();
+}
+
 template <typename T, int D, bool CAUSAL>
 hipError_t launch_t(const BwdArgs& a, hipStream_t s) {
-  const dim3 grid((unsigned)(a.B * a.Hq * a.nqt)), block(kDqWaves * 64);
-  hipLaunchKernelGGL((dq_ds_kernel<T, D, CAUSAL>), grid, block, 0, s, a);
-  return hipGetLastError();
+  return a.do_dq ? launch_a<T, D, CAUSAL, true>(a, s) : launch_a<T, D, CAUSAL, false>(a, s);
 }
 
 }  // namespace

@@ -56,6 +56,7 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
   static_assert(UQ >= 1, "tile split");
   static_assert(DOFF + kNBuf * QTILE <= 65536, "buffer offsets fit the DS immediate");
   static_assert(kKvWaves * 32 * OS * 2 <= 2 * kNBuf * QTILE, "epilogue staging fits");
+  static_assert(kKvKeys == kKv2Keys && kStep == 32, "prepared-mask lists are built for this shape");
   __shared__ __attribute__((aligned(1024))) char smem[LOFF + kNBuf * LBUF];
 
   // ---- which (batch, kv-head, split, key block) ------------------------------
@@ -92,11 +93,43 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
   }
 
   // ---- iteration space: (head of the group split, 32-row step) ---------------
+  // Without a mask: every step from qstart on, for each head.  With a mask: per
+  // head, the live steps of the prepared list of this key block (causality
+  // folded in), ascending.
   const int gsz = a.G / a.split;
   const int g0 = sp * gsz;
-  const int qstart = CAUSAL ? (kt0 / kStep) * kStep : 0;   // rows above the block are masked
+  const int h_first = kvh * a.G + g0, h_end = h_first + gsz;
+  const int qstart = CAUSAL && !MASK ? (kt0 / kStep) * kStep : 0;   // rows above the block are masked
   const int nst = qstart < Tq ? (Tq - qstart + kStep - 1) / kStep : 0;
-  const int n = gsz * nst;
+  auto kv_list = [&](int h) __attribute__((always_inline)) -> const int32_t* {
+    const int pm = mask_plane(a.ml, b, h);
+    return (const int32_t*)(a.mws + a.ml.lkv + pm * a.ml.plkv) + (int64_t)kt * (1 + a.ml.nq32);
+  };
+  int n = gsz * nst;
+  if constexpr (MASK) {
+    n = 0;
+    if (a.ml.Hm == 1) n = gsz * kv_list(h_first)[0];
+    else for (int h = h_first; h < h_end; ++h) n += kv_list(h)[0];
+  }
+  // List cursor (MASK): head h, position idx in that head's list of cnt
+  // steps; seek() moves past exhausted and empty lists.
+  struct Cursor { int h, idx, cnt; const int32_t* lst; };
+  auto seek = [&](Cursor& c) __attribute__((always_inline)) {
+    while (c.idx >= c.cnt && c.h < h_end) {
+      ++c.h;
+      c.idx = 0;
+      if (c.h < h_end) { c.lst = kv_list(c.h); c.cnt = c.lst[0]; }
+    }
+  };
+  auto cursor0 = [&]() __attribute__((always_inline)) -> Cursor {
+    Cursor c{h_first, 0, 0, nullptr};
+    if constexpr (MASK) {
+      c.lst = kv_list(h_first);
+      c.cnt = c.lst[0];
+      seek(c);
+    }
+    return c;
+  };
 
   // ---- LDS addresses -----------------------------------------------------------
   const uint32_t lds0 = (uint32_t)(uintptr_t)(FA_LDS char*)smem;
@@ -145,6 +178,7 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
   const uint32_t so_q0 = (uint32_t)qstart * (uint32_t)a.qst * 2, so_d0 = (uint32_t)qstart * (uint32_t)a.dst * 2;
   int ld_it = 0, ld_h = kvh * a.G + g0, ld_qs = qstart;
   uint32_t so_q = so_q0, so_d = so_d0, so_l = (uint32_t)qstart * 4;
+  Cursor ldc = cursor0();
   const T* q_head = (const T*)a.q + b * a.qsb + (int64_t)ld_h * a.qsh;
   const T* d_head = (const T*)a.dout + b * a.dsb + (int64_t)ld_h * a.dsh;
   const float* l_head = a.lse + ((int64_t)b * a.Hq + ld_h) * Tq;
@@ -152,6 +186,18 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
   auto load_next = [&](auto Sc) __attribute__((always_inline)) {
     constexpr int S = decltype(Sc)::value;
     const bool live = ld_it < n;
+    if constexpr (MASK) {
+      // position the loads at the cursor's step (rows past Tq read as zeros)
+      ld_h = min(ldc.h, h_end - 1);
+      ld_qs = live ? kStep * ldc.lst[1 + ldc.idx] : 0;
+      so_q = (uint32_t)ld_qs * (uint32_t)a.qst * 2;
+      so_d = (uint32_t)ld_qs * (uint32_t)a.dst * 2;
+      so_l = (uint32_t)ld_qs * 4;
+      q_head = (const T*)a.q + b * a.qsb + (int64_t)ld_h * a.qsh;
+      d_head = (const T*)a.dout + b * a.dsb + (int64_t)ld_h * a.dsh;
+      l_head = a.lse + ((int64_t)b * a.Hq + ld_h) * Tq;
+      e_head = a.delta + ((int64_t)b * a.Hq + ld_h) * Tq;
+    }
     const auto rq = __builtin_amdgcn_make_buffer_rsrc((void*)q_head, (short)0, live ? (int)q_rec : 0, 0x00020000);
     const auto rd = __builtin_amdgcn_make_buffer_rsrc((void*)d_head, (short)0, live ? (int)d_rec : 0, 0x00020000);
 #pragma unroll
@@ -167,6 +213,13 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
     }
     st_rows[S] = live ? min(kStep, Tq - ld_qs) : 0;
     ++ld_it;
+    if constexpr (MASK) {
+      if (live) {
+        ++ldc.idx;
+        seek(ldc);
+      }
+      return;
+    }
     ld_qs += kStep;
     so_q += inc_q;
     so_d += inc_d;
@@ -200,22 +253,32 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
 
   // ---- step being computed: head it_h, first row it_qs (advanced per step) -----------
   int it_h = kvh * a.G + g0, it_qs = qstart;
+  Cursor itc = cursor0();
+  if constexpr (MASK) {
+    it_h = min(itc.h, h_end - 1);
+    it_qs = n > 0 ? kStep * itc.lst[1] : 0;
+  }
 
   // ---- mask / score of a step (lane's 16 query rows at its key) -----------------
-  uint32_t mreg[MASK ? 4 : 1];
+  // mask: the step's word of the transposed bits at this lane's key, shifted
+  // so that bit 8 gi + t is row 8 gi + 4 hf + t of the step.
+  uint32_t mreg = 0;
   float sreg[SCORE ? 16 : 1];
   auto load_ms = [&](bool live) __attribute__((always_inline)) {
-    if constexpr (MASK || SCORE) {
+    if constexpr (MASK) {
+      mreg = 0;
+      if (live) {
+        const uint32_t* bt = (const uint32_t*)(a.mws + a.ml.bitsT + mask_plane(a.ml, b, it_h) * a.ml.pbitsT);
+        mreg = bt[(int64_t)kc * a.ml.wq + (it_qs >> 5)] >> (4 * hf);
+      }
+    }
+    if constexpr (SCORE) {
       // padding steps reread the last real step's rows (harmless)
       const int h = live ? it_h : kvh * a.G + g0 + gsz - 1;
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int q = min(it_qs + 8 * (i >> 2) + 4 * hf + (i & 3), Tq - 1);
-        if constexpr (MASK) {
-          const uint32_t m = a.mask[b * a.msb + h * a.msh + (int64_t)q * a.msq + kc] != 0;
-          if ((i & 3) == 0) mreg[i >> 2] = m; else mreg[i >> 2] |= m << (8 * (i & 3));
-        }
-        if constexpr (SCORE) sreg[i] = a.score[b * a.ssb + h * a.ssh + (int64_t)q * a.ssq + kc];
+        sreg[i] = a.score[b * a.ssb + h * a.ssh + (int64_t)q * a.ssq + kc];
       }
     }
   };
@@ -236,6 +299,24 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
   // descriptor of step j's tile, then advance (it_h, it_qs, it_tile) to step j+1
   auto next_step = [&](int j) __attribute__((always_inline)) {
     const int s = it_qs >> 5;
+    if constexpr (MASK) {
+      // tiles of blocks without a kept entry are neither stored nor read
+      bool ok = ds_on && j < n && (!CAUSAL || kb32 <= s);
+      if (ok) {
+        const uint8_t* bl = (const uint8_t*)(a.mws + a.ml.blk + mask_plane(a.ml, b, it_h) * a.ml.pblk);
+        ok = bl[(int64_t)s * a.ml.nk32 + kb32] != 0;
+      }
+      const int64_t tile = ((int64_t)b * a.Hq + it_h) * a.ds_plane + ds_row(s, a.nk32, CAUSAL) + kb32;
+      ds_rs = __builtin_amdgcn_make_buffer_rsrc((void*)((uint16_t*)a.ds + tile * 1024), (short)0, ok ? 2048 : 0,
+                                                0x00020000);
+      if (j < n) {
+        ++itc.idx;
+        seek(itc);
+      }
+      it_h = min(itc.h, h_end - 1);
+      it_qs = j + 1 < n ? kStep * itc.lst[1 + itc.idx] : 0;
+      return;
+    }
     const bool ok = ds_on && j < n && (!CAUSAL || kb32 <= s);
     ds_rs = __builtin_amdgcn_make_buffer_rsrc((void*)((uint16_t*)a.ds + it_tile * 1024), (short)0, ok ? 2048 : 0,
                                               0x00020000);
@@ -314,7 +395,7 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
       if constexpr (EDGE) {
         bool keep = true;
         if constexpr (CAUSAL) keep = dkq <= 8 * gi + t;
-        if constexpr (MASK) keep = keep && ((mreg[gi] >> (8 * t)) & 0xffu) != 0;
+        if constexpr (MASK) keep = keep && ((mreg >> (8 * gi + t)) & 1u) != 0;
         p = keep ? p : 0.f;
       }
       sacc[PJ][i] = p;

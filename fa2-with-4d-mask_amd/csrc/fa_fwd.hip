@@ -65,16 +65,6 @@ template <int D> __device__ __forceinline__ int swz_v(int r) {
   return D == 128 ? ((r & 3) << 2) : (((r >> 1) & 1) << 2);
 }
 
-__device__ __forceinline__ uint32_t load_mask4(const uint8_t* row, int kk, int Tk, bool vec) {
-  // Unconditional loads (addresses clamped into the row): the caller masks
-  // keys >= Tk itself, and the number of memory instructions stays fixed.
-  if (vec && kk + 4 <= Tk) return *(const uint32_t*)(row + kk);
-  uint32_t r = 0;
-#pragma unroll
-  for (int t = 0; t < 4; ++t) r |= (uint32_t)(row[min(kk + t, Tk - 1)] != 0) << (8 * t);
-  return r;
-}
-
 __device__ __forceinline__ f32x4 load_score4(const float* row, int kk, int Tk, bool vec) {
   if (vec && kk + 4 <= Tk) return *(const f32x4*)(row + kk);
   f32x4 r;
@@ -147,6 +137,7 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
   static_assert(kNBuf * TILEB <= 65536, "buffer + row offsets fit the 16-bit DS immediate");
   constexpr int OS = D + 8;             // epilogue O staging stride (elements)
   static_assert(kWaves * 32 * OS * 2 <= 2 * kNBuf * TILEB, "O staging fits in the K/V buffers");
+  static_assert(BM == kFwdRows && BN == kFwdKeys, "prepared-mask lists are built for this tile shape");
   __shared__ __attribute__((aligned(1024))) char smem[2 * kNBuf * TILEB];
 
   // ---- which (batch, head, query tile) -------------------------------------
@@ -188,11 +179,27 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
     }
   };
 
+  // Key tiles of the workgroup: 0 .. nt-1, or with a mask the live tiles of
+  // the prepared list (ascending; bit 31: every entry of the tile is kept).
+  const int qrow_c = min(qrow, Tq - 1);  // clamped row for mask/score reads
+  const int32_t* flist = nullptr;
+  const uint32_t* mbits = nullptr;
+  if constexpr (MASK) {
+    const int pm = mask_plane(a.ml, b, h);
+    flist = (const int32_t*)(a.mws + a.ml.lfwd + pm * a.ml.plfwd) + (int64_t)qt * (1 + a.ml.nft);
+    mbits = (const uint32_t*)(a.mws + a.ml.bits + pm * a.ml.pbits) + (int64_t)qrow_c * a.ml.wk;
+  }
   const int kv_end = CAUSAL ? min(Tk, q0 + BM) : Tk;
-  const int nt = (kv_end + BN - 1) / BN;                       // tiles of the workgroup
+  const int nt = MASK ? flist[0] : (kv_end + BN - 1) / BN;
   // tiles of this wave (opaque: keeps the per-pair guards dynamic, so that
-  // every instantiation gets the same control flow and register assignment)
-  const int nt_w = (int)opaque((uint32_t)(CAUSAL ? min(nt, (min(Tk, q0w + 32) + BN - 1) / BN) : nt));
+  // every instantiation gets the same control flow and register assignment);
+  // with a mask every wave walks the whole list (causality is applied per key)
+  const int nt_w = (int)opaque((uint32_t)(CAUSAL && !MASK ? min(nt, (min(Tk, q0w + 32) + BN - 1) / BN) : nt));
+  // key tile at list position p < nt
+  auto tile_at = [&](int p) __attribute__((always_inline)) -> int {
+    if constexpr (MASK) return flist[1 + p] & 0x7fffffff;
+    else return p;
+  };
 
   const uint32_t lds0 = (uint32_t)(uintptr_t)(FA_LDS char*)smem;
 
@@ -209,15 +216,18 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
     soff_k[u] = opaque(lds0 + KOFF + r * ROWB + ((c ^ swz_k<D>(r)) * 16));
     soff_v[u] = opaque(lds0 + VOFF + r * ROWB + ((c ^ swz_v<D>(r)) * 16));
   }
-  // Tile t's rows [t BN, min(Tk, t BN + BN)); t >= nt gives an empty range
-  // (the loads return zeros).
-  auto rsrc_of = [&](const T* base, int64_t st, int t) __attribute__((always_inline)) {
+  // Tile at list position p: rows [t BN, min(Tk, t BN + BN)) of t = tile_at(p);
+  // p >= nt gives an empty range (the loads return zeros).
+  auto rsrc_of = [&](const T* base, int64_t st, int p) __attribute__((always_inline)) {
     uint32_t nrec = 0;
-    if (t < nt) {
+    const T* tb = base;
+    if (p < nt) {
+      const int t = tile_at(p);
       const int64_t rows = min(Tk - t * BN, BN);
       nrec = (uint32_t)min((rows - 1) * st * 2 + ROWB, (int64_t)0xfffffff0);
+      tb = base + (int64_t)t * BN * st;
     }
-    return __builtin_amdgcn_make_buffer_rsrc((void*)(base + (int64_t)t * BN * st), (short)0, (int)nrec, 0x00020000);
+    return __builtin_amdgcn_make_buffer_rsrc((void*)tb, (short)0, (int)nrec, 0x00020000);
   };
   u32x4 stg[NSTG];   // K slots, then V slots, of the next batch
   // Batch of pair p: K(p+2) -> K buffer (p+2)%3, V(p+1) -> V buffer (p+1)%3.
@@ -266,12 +276,9 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
     vaddr[nb] = opaque(lds0 + VOFF + tr_row * ROWB + ((((c >> 3) ^ swz_v<D>(tr_row))) * 16) + (c & 7) * 2);
   }
 
-  const int qrow_c = min(qrow, Tq - 1);  // clamped row for mask/score reads
-  const uint8_t* mrow = nullptr;
   const float* srow = nullptr;
-  if constexpr (MASK) mrow = a.mask + b * a.msb + h * a.msh + (int64_t)qrow_c * a.msq;
   if constexpr (SCORE) srow = a.score + b * a.ssb + h * a.ssh + (int64_t)qrow_c * a.ssq;
-  const bool mvec = a.mask_vec != 0, svec = a.score_vec != 0;
+  const bool svec = a.score_vec != 0;
   const float c2 = a.scale_log2;
 
   f32x16 oacc[NB];
@@ -281,7 +288,11 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
   V8 pk[4];                        // P(p) packed, B operand of the next M step
 #pragma unroll
   for (int kk = 0; kk < 4; ++kk) pk[kk] = V8{};
-  uint32_t mreg[MASK ? 8 : 1];     // mask bytes of the tile in flight
+  // mask bits of the tile in flight: word kb holds keys 32 kb + 8 gi + t of
+  // this lane (shifted by 4 hf), all ones for a fully kept tile
+  uint32_t mreg[2] = {~0u, ~0u};
+  int tile_cur = 0;                // key tile of the tile in flight
+  bool mpart = false;              // the tile in flight has dropped entries
   f32x4 sreg[SCORE ? 8 : 1];       // score of the tile in flight
   float m_run = kNegInf, l_run = 0.f;
 
@@ -294,15 +305,26 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
     constexpr uint32_t vb_lds = ((KB + 2) % kNBuf) * TILEB;      // V(p-1), relative to V buffer 0
     if constexpr (MASK || SCORE) {
       if (p < nt_w) {
-        const int k0 = p * BN;
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int gi = 0; gi < 4; ++gi) {
-            const int kk = k0 + kb * 32 + gi * 8 + hf * 4;
-            if constexpr (MASK) mreg[kb * 4 + gi] = load_mask4(mrow, kk, Tk, mvec);
-            if constexpr (SCORE) sreg[kb * 4 + gi] = load_score4(srow, kk, Tk, svec);
+        int t = p;
+        if constexpr (MASK) {
+          const int e = flist[1 + p];
+          t = e & 0x7fffffff;
+          mpart = e >= 0;
+          mreg[0] = mreg[1] = ~0u;
+          if (mpart) {
+            const u32x2 w = *(const u32x2*)(mbits + 2 * t);
+            mreg[0] = w[0] >> (4 * hf);
+            mreg[1] = w[1] >> (4 * hf);
           }
+        }
+        tile_cur = t;
+        if constexpr (SCORE) {
+          const int k0 = t * BN;
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int gi = 0; gi < 4; ++gi) sreg[kb * 4 + gi] = load_score4(srow, k0 + kb * 32 + gi * 8 + hf * 4, Tk, svec);
+        }
       }
     }
     __builtin_amdgcn_s_setprio(2);
@@ -362,7 +384,7 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
   // lane's entry (kb, e) is key 64 p + 32 kb + 8 (e/4) + 4 hf + e%4 of row qrow;
   // key slot t of k-step kk (= 2 kb + c) <-> key 32 kb + 16 c + 4 hf + t%4 + 8 (t/4)
   auto v_step = [&](int p, auto&& stage) __attribute__((always_inline)) {
-    const int k0 = p * BN;
+    const int k0 = (MASK || SCORE ? tile_cur : p) * BN;
     if constexpr (SCORE) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
@@ -372,21 +394,19 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
           for (int t = 0; t < 4; ++t)
             sacc[kb][gi * 4 + t] = fmaf(a.qsign, sreg[kb * 4 + gi][t], sacc[kb][gi * 4 + t]);
     }
-    const bool edge = MASK || a.zero_scale || (k0 + BN > Tk) || (CAUSAL && k0 + BN - 1 > q0w);
+    const bool edge = (MASK && mpart) || a.zero_scale || (k0 + BN > Tk) || (CAUSAL && k0 + BN - 1 > q0w);
     if (edge) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
         for (int gi = 0; gi < 4; ++gi) {
           const int kk = k0 + kb * 32 + gi * 8 + hf * 4;
-          uint32_t mb = 0x01010101u;
-          if constexpr (MASK) mb = mreg[kb * 4 + gi];
 #pragma unroll
           for (int t = 0; t < 4; ++t) {
             const int key = kk + t;
             bool keep = key < Tk;
             if constexpr (CAUSAL) keep = keep && (key <= qrow);
-            if constexpr (MASK) keep = keep && (((mb >> (8 * t)) & 0xffu) != 0);
+            if constexpr (MASK) keep = keep && ((mreg[kb] >> (8 * gi + t)) & 1u) != 0;
             const float sv = sacc[kb][gi * 4 + t];
             sacc[kb][gi * 4 + t] = keep ? (a.zero_scale ? 0.f : sv) : kNegInf;
           }

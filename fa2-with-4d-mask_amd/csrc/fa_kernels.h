@@ -6,6 +6,77 @@
 
 namespace fa {
 
+// Work shapes the prepared-mask lists are built for (each kernel asserts its own).
+constexpr int kFwdRows = 256;    // forward: query rows per workgroup
+constexpr int kFwdKeys = 64;     //          keys per tile
+constexpr int kKv2Keys = 128;    // dK/dV (deterministic): keys per workgroup, 32-row steps
+constexpr int kDqDsRows = 256;   // dQ from dS: query rows per workgroup, 32-key steps
+
+// Prepared mask (workspace written by fa_mask_prepare from the bool mask).
+// One plane per (mask batch, mask head): Bm = 1 when the mask's batch stride
+// is 0 (broadcast), else B; Hm likewise over the query heads.  Per plane:
+//   bits   uint32 [Tq][wk]      bit j%32 of word j/32 = keep(i, j); zero past Tk
+//   bitsT  uint32 [Tk][wq]      bit i%32 of word i/32 = keep(i, j); zero past Tq
+//   blk    uint8  [nq32][nk32]  32x32 block: 0 no kept entry, 1 some, 2 all (in bounds)
+//   lfwd   int32  [nfq][1+nft]  per 256-row block: count, then the live 64-key
+//                               tiles ascending, bit 31 set when every block is 2
+//   lkv    int32  [nkb][1+nq32] per 128-key block: count, live 32-row steps
+//   ldq    int32  [ndq][1+nk32] per 256-row block: count, live 32-key steps
+// "Live" folds in causality when the workspace was prepared with is_causal.
+struct MaskLayout {
+  int Bm, Hm;
+  int nq32, nk32, wk, wq;
+  int nfq, nft, nkb, ndq;
+  int64_t bits, bitsT, blk, lfwd, lkv, ldq, total;   // byte offsets of the plane arrays, workspace size
+  int64_t pbits, pbitsT, pblk, plfwd, plkv, pldq;    // per-plane sizes (bytes)
+};
+
+__host__ __device__ inline int64_t align256(int64_t x) { return (x + 255) & ~(int64_t)255; }
+
+__host__ __device__ inline MaskLayout mask_layout(int B, int Hq, int Tq, int Tk, bool bcast_b, bool bcast_h) {
+  MaskLayout m{};
+  m.Bm = bcast_b ? 1 : B;
+  m.Hm = bcast_h ? 1 : Hq;
+  m.nq32 = (Tq + 31) / 32;
+  m.nk32 = (Tk + 31) / 32;
+  m.wk = (m.nk32 + 3) & ~3;
+  m.wq = (m.nq32 + 3) & ~3;
+  m.nfq = (Tq + kFwdRows - 1) / kFwdRows;
+  m.nft = (Tk + kFwdKeys - 1) / kFwdKeys;
+  m.nkb = (Tk + kKv2Keys - 1) / kKv2Keys;
+  m.ndq = (Tq + kDqDsRows - 1) / kDqDsRows;
+  m.pbits = (int64_t)Tq * m.wk * 4;
+  m.pbitsT = (int64_t)Tk * m.wq * 4;
+  m.pblk = (int64_t)m.nq32 * m.nk32;
+  m.plfwd = (int64_t)m.nfq * (1 + m.nft) * 4;
+  m.plkv = (int64_t)m.nkb * (1 + m.nq32) * 4;
+  m.pldq = (int64_t)m.ndq * (1 + m.nk32) * 4;
+  const int64_t np = (int64_t)m.Bm * m.Hm;
+  m.bits = 0;
+  m.bitsT = align256(m.bits + np * m.pbits);
+  m.blk = align256(m.bitsT + np * m.pbitsT);
+  m.lfwd = align256(m.blk + np * m.pblk);
+  m.lkv = align256(m.lfwd + np * m.plfwd);
+  m.ldq = align256(m.lkv + np * m.plkv);
+  m.total = align256(m.ldq + np * m.pldq);
+  return m;
+}
+
+// Plane of (batch b, query head h).
+__host__ __device__ inline int mask_plane(const MaskLayout& m, int b, int h) {
+  return (m.Bm == 1 ? 0 : b) * m.Hm + (m.Hm == 1 ? 0 : h);
+}
+
+struct MaskArgs {
+  const uint8_t* mask;
+  int64_t msb, msh, msq;
+  int Tq, Tk;
+  int is_causal;
+  int vec16;            // rows 16-byte aligned: 128-bit loads allowed
+  char* ws;
+  MaskLayout ml;
+};
+
 struct FwdArgs {
   const void* q; const void* k; const void* v; void* o; float* lse;
   const uint8_t* mask; const float* score;
@@ -18,6 +89,8 @@ struct FwdArgs {
   int zero_scale;       // scale == 0: every kept logit is 0
   int mask_vec;         // mask rows 4-byte aligned: 32-bit loads allowed
   int score_vec;        // score rows 16-byte aligned: 128-bit loads allowed
+  const char* mws;      // prepared mask (with a mask)
+  MaskLayout ml;
 };
 
 struct PreArgs {
@@ -40,7 +113,9 @@ struct BwdArgs {
   int nkt;              // key tiles per (b, kv-head)
   int nqt;              // query tiles per (b, h) (dQ kernel)
   int split;            // query-head-group split of the dK/dV kernel
-  int do_dq;            // dK/dV kernel also accumulates dQ with fp32 atomics
+  int do_dq;            // dQ accumulated with fp32 atomics into dq_accum (fused in the dK/dV
+                        // kernel, or by the dQ-from-dS kernel over dq_split key ranges)
+  int dq_split;         // key ranges of the atomic dQ-from-dS kernel
   float scale;          // softmax scale (dS multiplier)
   float scale_log2;     // |scale| * log2(e)  (1 when zero_scale)
   float qsign;
@@ -53,6 +128,8 @@ struct BwdArgs {
   void* ds;
   int64_t ds_plane;     // tiles per (b, h)
   int nq32, nk32;       // 32-row / 32-key steps
+  const char* mws;      // prepared mask (with a mask; the deterministic kernels read it)
+  MaskLayout ml;
 };
 
 // First tile of query step s in a (b, h) plane of dS tiles: causal planes
@@ -83,5 +160,7 @@ int dkdv2_block_keys();
 hipError_t launch_bwd_dq_ds(const BwdArgs& a, int D, int dtype, bool causal, hipStream_t s);
 int dq_ds_block_rows();
 hipError_t launch_convert(const CvtArgs& a, int dtype, hipStream_t s);
+// Bool mask -> prepared mask workspace (bits, transposed bits, block states, lists).
+hipError_t launch_mask_prepare(const MaskArgs& a, hipStream_t s);
 
 }  // namespace fa

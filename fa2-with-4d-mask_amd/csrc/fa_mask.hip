@@ -1,0 +1,201 @@
+// Prepared mask for the gfx950 attention kernels: one pass over the bool
+// keep-mask (the reference streams it per tile inside every kernel,
+// python/fa2.py:107-114, 261-280) producing
+//   * the mask as bits, row-major (forward, dQ) and transposed (dK/dV), so the
+//     attention kernels read 1 bit per (row, key) instead of 1 byte;
+//   * the state of every 32x32 block (no kept entry / some / all);
+//   * per kernel work unit, the list of tiles that hold a kept entry (with
+//     causality folded in), so dead tiles cost neither loads nor MFMAs.
+// Layout: MaskLayout (fa_kernels.h).
+#include "fa_common.h"
+#include "fa_kernels.h"
+
+namespace fa {
+namespace {
+
+constexpr int kRows = 128;   // rows per workgroup of the bits kernel
+constexpr int kKeys = 256;   // keys per workgroup
+
+// Bit j of the result = (byte j of x) != 0, for the 4 bytes of x.
+__device__ __forceinline__ uint32_t nz4(uint32_t x) {
+  uint32_t t = x | (x >> 4);
+  t |= t >> 2;
+  t |= t >> 1;
+  t &= 0x01010101u;                      // bit 8 j = byte j != 0
+  return ((t * 0x01020408u) >> 24) & 0xfu;  // gathered into bits 0..3 (no carries)
+}
+
+// Grid (key chunk of 256, row chunk of 128, plane).  Thread t handles rows
+// 32 rr + t/8 (rr = 0..3) x keys 32 (t%8) .. +31 of the chunk: 256 contiguous
+// bytes per 8 threads.
+__global__ __launch_bounds__(256) void mask_bits_kernel(const MaskArgs a) {
+  __shared__ uint32_t words[kRows][9];
+  const MaskLayout& ml = a.ml;
+  const int tid = threadIdx.x;
+  const int kc0 = blockIdx.x * kKeys, r0 = blockIdx.y * kRows, pm = blockIdx.z;
+  const int bb = pm / ml.Hm, hh = pm - bb * ml.Hm;
+  const uint8_t* src = a.mask + bb * a.msb + hh * a.msh;
+  const int Tq = a.Tq, Tk = a.Tk;
+  uint32_t* bits = (uint32_t*)(a.ws + ml.bits + pm * ml.pbits);
+  uint32_t* bitsT = (uint32_t*)(a.ws + ml.bitsT + pm * ml.pbitsT);
+  uint8_t* blk = (uint8_t*)(a.ws + ml.blk + pm * ml.pblk);
+
+  const int c = tid & 7, kbase = kc0 + 32 * c, wcol = kc0 / 32 + c;
+#pragma unroll
+  for (int rr = 0; rr < 4; ++rr) {
+    const int rl = 32 * rr + (tid >> 3), row = r0 + rl;
+    uint32_t w = 0;
+    if (row < Tq && kbase < Tk) {
+      const uint8_t* p = src + row * a.msq + kbase;
+      if (a.vec16 && kbase + 32 <= Tk) {
+        const u32x4 x0 = *(const u32x4*)p, x1 = *(const u32x4*)(p + 16);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) w |= nz4(x0[j]) << (4 * j);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) w |= nz4(x1[j]) << (16 + 4 * j);
+      } else {
+        const int n = min(32, Tk - kbase);
+        for (int j = 0; j < n; ++j) w |= (uint32_t)(p[j] != 0) << j;
+      }
+    }
+    words[rl][c] = w;
+    if (row < Tq && wcol < ml.wk) bits[(int64_t)row * ml.wk + wcol] = w;   // padding words are written as 0
+  }
+  __syncthreads();
+
+  // transposed: thread t = key kc0 + t, words of rows r0 .. r0 + 127 (4 words)
+  {
+    const int kk = kc0 + tid;
+    if (kk < Tk) {
+      u32x4 out;
+#pragma unroll
+      for (int rw = 0; rw < 4; ++rw) {
+        uint32_t w = 0;
+#pragma unroll 8
+        for (int r = 0; r < 32; ++r) w |= ((words[32 * rw + r][tid >> 5] >> (tid & 31)) & 1u) << r;
+        out[rw] = w;
+      }
+      *(u32x4*)(bitsT + (int64_t)kk * ml.wq + r0 / 32) = out;
+    }
+  }
+
+  // block states: thread t < 32 -> row block rw = t/8, key block c = t%8
+  if (tid < 32) {
+    const int rw = tid >> 3, cb = tid & 7;
+    const int rb = r0 / 32 + rw, kb = kc0 / 32 + cb;
+    if (rb < ml.nq32 && kb < ml.nk32) {
+      const int nk = min(32, Tk - 32 * kb);
+      const uint32_t vm = nk >= 32 ? 0xffffffffu : ((1u << nk) - 1u);
+      const int nr = min(32, Tq - 32 * rb);
+      uint32_t any = 0, all = vm;
+      for (int r = 0; r < nr; ++r) {
+        const uint32_t w = words[32 * rw + r][cb] & vm;
+        any |= w;
+        all &= w;
+      }
+      blk[(int64_t)rb * ml.nk32 + kb] = any == 0 ? 0 : (all == vm ? 2 : 1);
+    }
+  }
+}
+
+// One wave per list; lanes test 64 candidates at a time and compact the live
+// ones in ascending order.
+__global__ __launch_bounds__(256) void mask_lists_kernel(const MaskArgs a) {
+  const MaskLayout& ml = a.ml;
+  const int lane = threadIdx.x & 63;
+  const int64_t np = (int64_t)ml.Bm * ml.Hm;
+  int64_t gw = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int Tq = a.Tq;
+  const bool causal = a.is_causal != 0;
+  int kind;
+  if (gw < np * ml.nfq) kind = 0;
+  else if ((gw -= np * ml.nfq) < np * ml.nkb) kind = 1;
+  else if ((gw -= np * ml.nkb) < np * ml.ndq) kind = 2;
+  else return;
+  const int per = kind == 0 ? ml.nfq : (kind == 1 ? ml.nkb : ml.ndq);
+  const int pm = (int)(gw / per), unit = (int)(gw - (int64_t)pm * per);
+  const uint8_t* blk = (const uint8_t*)(a.ws + ml.blk + pm * ml.pblk);
+  int32_t* lst;
+  int ncand;
+  if (kind == 0) {
+    lst = (int32_t*)(a.ws + ml.lfwd + pm * ml.plfwd) + (int64_t)unit * (1 + ml.nft);
+    ncand = ml.nft;
+  } else if (kind == 1) {
+    lst = (int32_t*)(a.ws + ml.lkv + pm * ml.plkv) + (int64_t)unit * (1 + ml.nq32);
+    ncand = ml.nq32;
+  } else {
+    lst = (int32_t*)(a.ws + ml.ldq + pm * ml.pldq) + (int64_t)unit * (1 + ml.nk32);
+    ncand = ml.nk32;
+  }
+  int count = 0;
+  for (int base = 0; base < ncand; base += 64) {
+    const int cand = base + lane;
+    bool live = false, full = true;
+    if (cand < ncand) {
+      // every block state is loaded before any is tested (predicated loads,
+      // issued together: the scan is latency-bound otherwise)
+      if (kind == 0) {
+        // 256 rows x 64 keys: row blocks 8 unit .. +7, key blocks 2 cand, +1
+        const int q_last = min(Tq - 1, kFwdRows * unit + kFwdRows - 1);
+        if (!causal || kFwdKeys * cand <= q_last) {
+          uint8_t st[8][2];
+#pragma unroll
+          for (int r = 0; r < 8; ++r)
+#pragma unroll
+            for (int c = 0; c < 2; ++c) {
+              const int rb = 8 * unit + r, kb = 2 * cand + c;
+              st[r][c] = (rb < ml.nq32 && kb < ml.nk32) ? blk[(int64_t)rb * ml.nk32 + kb] : 2;
+            }
+#pragma unroll
+          for (int r = 0; r < 8; ++r)
+#pragma unroll
+            for (int c = 0; c < 2; ++c) {
+              const int rb = 8 * unit + r, kb = 2 * cand + c;
+              if (rb < ml.nq32 && kb < ml.nk32) live |= st[r][c] != 0;
+              full &= st[r][c] == 2;
+            }
+        }
+      } else if (kind == 1) {
+        // 128 keys x 32 rows: key blocks 4 unit .. +3, row block cand
+        if (!causal || min(Tq - 1, 32 * cand + 31) >= kKv2Keys * unit) {
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            const int kb = 4 * unit + c;
+            if (kb < ml.nk32) live |= blk[(int64_t)cand * ml.nk32 + kb] != 0;
+          }
+        }
+      } else {
+        // 256 rows x 32 keys: row blocks 8 unit .. +7, key block cand
+        const int q_last = min(Tq - 1, kDqDsRows * unit + kDqDsRows - 1);
+        if (!causal || 32 * cand <= q_last) {
+#pragma unroll
+          for (int r = 0; r < 8; ++r) {
+            const int rb = 8 * unit + r;
+            if (rb < ml.nq32) live |= blk[(int64_t)rb * ml.nk32 + cand] != 0;
+          }
+        }
+      }
+    }
+    const uint64_t bal = __builtin_amdgcn_ballot_w64(live);
+    const int pos = count + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+    if (live) lst[1 + pos] = (kind == 0 && full) ? (int32_t)(0x80000000u | (uint32_t)cand) : cand;
+    count += __builtin_popcountll(bal);
+  }
+  if (lane == 0) lst[0] = count;
+}
+
+}  // namespace
+
+hipError_t launch_mask_prepare(const MaskArgs& a, hipStream_t s) {
+  const MaskLayout& ml = a.ml;
+  const dim3 g1((unsigned)((a.Tk + kKeys - 1) / kKeys), (unsigned)((a.Tq + kRows - 1) / kRows),
+                (unsigned)(ml.Bm * ml.Hm));
+  hipLaunchKernelGGL(mask_bits_kernel, g1, dim3(256), 0, s, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const int64_t nl = (int64_t)ml.Bm * ml.Hm * (ml.nfq + ml.nkb + ml.ndq);
+  hipLaunchKernelGGL(mask_lists_kernel, dim3((unsigned)((nl + 3) / 4)), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+}  // namespace fa

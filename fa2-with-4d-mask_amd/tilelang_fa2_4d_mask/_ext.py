@@ -19,7 +19,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must be loaded before the HIP library, see above)
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libfa2_4d_mask.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 FA_DTYPE_BF16 = 0
 FA_DTYPE_FP16 = 1
@@ -45,7 +45,7 @@ class FaFwdParams(ctypes.Structure):
         ("batch seqlen_q seqlen_k heads_q heads_k head_dim", _i32),
         ("scale", ctypes.c_float),
         ("is_causal dtype", _i32),
-        ("stream", _vp),
+        ("stream mask_ws", _vp),
     )
 
 
@@ -62,6 +62,16 @@ class FaBwdParams(ctypes.Structure):
         ("is_causal atomic_dq kv_split dtype", _i32),
         ("stream ds_tiles", _vp),
         ("ds_limit_bytes", _i64),
+        ("mask_ws", _vp),
+    )
+
+
+class FaMaskParams(ctypes.Structure):
+    _fields_ = _fields(
+        ("mask", _vp),
+        ("mask_stride_b mask_stride_h mask_stride_q", _i64),
+        ("batch seqlen_q seqlen_k heads_q is_causal", _i32),
+        ("workspace stream", _vp),
     )
 
 
@@ -72,11 +82,13 @@ class FaBwdPlan(ctypes.Structure):
         ("dq_accum_elems", _i64),
         ("dkv_accum_elems", _i64),
         ("ds_elems", _i64),
+        ("dkv_accum_zeroed", _i32),
+        ("dq_split", _i32),
     ]
 
 
-EXPORTED = ("fa_fwd", "fa_bwd_preprocess", "fa_bwd", "fa_bwd_finalize", "fa_bwd_plan", "fa_last_error",
-            "fa_abi_version")
+EXPORTED = ("fa_fwd", "fa_bwd_preprocess", "fa_bwd", "fa_bwd_finalize", "fa_bwd_plan", "fa_mask_plan",
+            "fa_mask_prepare", "fa_last_error", "fa_abi_version")
 
 _lib = None
 _lock = threading.Lock()
@@ -107,6 +119,10 @@ def load_library(path: os.PathLike | None = None) -> ctypes.CDLL:
         lib.fa_bwd_finalize.restype = ctypes.c_int
         lib.fa_bwd_plan.argtypes = [ctypes.POINTER(FaBwdParams), ctypes.POINTER(FaBwdPlan)]
         lib.fa_bwd_plan.restype = ctypes.c_int
+        lib.fa_mask_plan.argtypes = [ctypes.POINTER(FaMaskParams), ctypes.POINTER(ctypes.c_int64)]
+        lib.fa_mask_plan.restype = ctypes.c_int
+        lib.fa_mask_prepare.argtypes = [ctypes.POINTER(FaMaskParams)]
+        lib.fa_mask_prepare.restype = ctypes.c_int
         lib.fa_last_error.argtypes = []
         lib.fa_last_error.restype = ctypes.c_char_p
         lib.fa_abi_version.argtypes = []

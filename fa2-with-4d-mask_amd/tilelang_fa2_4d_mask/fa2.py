@@ -14,8 +14,14 @@ What differs on purpose:
 * Mask/Score may be broadcast views ([B|1, Hq|1, Tq, Tk] with stride 0);
 * dQ/dK/dV come back in the input dtype directly (the reference returns fp32
   dQ and lets autograd cast it, python/fa2.py:527,556);
-* ``use_atomic_backward=False`` selects a deterministic dQ kernel (the
-  reference's "reduce" path still adds dQ atomically, python/fa2.py:420-421).
+* dQ goes through dS tiles the dK/dV kernel stores: ``use_atomic_backward``
+  (default) adds fp32 partials over a few key ranges atomically, ``False``
+  writes dQ in one deterministic pass (the reference adds a partial per
+  64-key block atomically in both modes, python/fa2.py:295-297, 420-421);
+* a mask is prepared once per call (``fa_mask_prepare``: bits, block states,
+  live-tile lists) and the workspace is kept for the backward, so the kernels
+  skip tiles without a kept entry (the reference streams every tile's mask
+  bytes, python/fa2.py:107-114, 261-280).
 """
 
 from __future__ import annotations
@@ -77,6 +83,25 @@ def _kernel_side(x: Optional[torch.Tensor], dtype: Optional[torch.dtype], B: int
 
 def _stream(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
+
+
+def _prepare_mask(mask: torch.Tensor, mst: tuple, B: int, Hq: int, Tq: int, Tk: int, is_causal: bool,
+                  device: torch.device) -> torch.Tensor:
+    """Prepared-mask workspace of ``mask`` (a broadcastable [B|1, Hq|1, Tq, Tk]
+    bool view), written on the current stream."""
+    lib = _ext.load_library()
+    mp = _ext.FaMaskParams()
+    mp.mask = mask.data_ptr()
+    mp.mask_stride_b, mp.mask_stride_h, mp.mask_stride_q = mst
+    mp.batch, mp.seqlen_q, mp.seqlen_k, mp.heads_q = B, Tq, Tk, Hq
+    mp.is_causal = 1 if is_causal else 0
+    nbytes = ctypes.c_int64(0)
+    _ext.check(lib.fa_mask_plan(ctypes.byref(mp), ctypes.byref(nbytes)), "fa_mask_plan", lib)
+    ws = torch.empty((nbytes.value,), dtype=torch.uint8, device=device)
+    mp.workspace = ws.data_ptr()
+    mp.stream = _stream(device)
+    _call(lib, "fa_mask_prepare", mp)
+    return ws
 
 
 class KernelEventLog:
@@ -160,6 +185,7 @@ class _flash_attention_with_4d_mask(torch.autograd.Function):
 
         O = torch.empty((B, Tq, Hq, D), dtype=q.dtype, device=q.device)
         LSE = torch.empty((B, Hq, Tq), dtype=torch.float32, device=q.device)
+        mask_ws = None
         if B * Tq * Hq > 0:
             if Tk == 0:
                 O.zero_()
@@ -168,6 +194,8 @@ class _flash_attention_with_4d_mask(torch.autograd.Function):
                 q = _kernel_operand(q)
                 k = _kernel_operand(k)
                 v = _kernel_operand(v)
+                if mask is not None:
+                    mask_ws = _prepare_mask(mask, mst, B, Hq, Tq, Tk, bool(is_causal), q.device)
                 p = _ext.FaFwdParams()
                 p.q, p.k, p.v, p.o, p.lse = q.data_ptr(), k.data_ptr(), v.data_ptr(), O.data_ptr(), LSE.data_ptr()
                 p.mask, p.score = _ext.ptr(mask), _ext.ptr(score)
@@ -182,9 +210,10 @@ class _flash_attention_with_4d_mask(torch.autograd.Function):
                 p.is_causal = 1 if is_causal else 0
                 p.dtype = code
                 p.stream = _stream(q.device)
+                p.mask_ws = _ext.ptr(mask_ws)
                 _call(_ext.load_library(), "fa_fwd", p)
 
-        ctx.save_for_backward(q, k, v, O, LSE, mask, score)
+        ctx.save_for_backward(q, k, v, O, LSE, mask, score, mask_ws)
         ctx.scale = scale
         ctx.is_causal = bool(is_causal)
         ctx.use_atomic_backward = bool(use_atomic_backward)
@@ -195,7 +224,7 @@ class _flash_attention_with_4d_mask(torch.autograd.Function):
     @staticmethod
     @once_differentiable
     def backward(ctx, dO: torch.Tensor):
-        q, k, v, O, LSE, mask, score = ctx.saved_tensors
+        q, k, v, O, LSE, mask, score, mask_ws = ctx.saved_tensors
         do = dO.transpose(1, 2) if ctx.bhsd_input else dO
         B, Tq, Hq, D = q.shape
         _, Tk, Hk, _ = k.shape
@@ -227,16 +256,17 @@ class _flash_attention_with_4d_mask(torch.autograd.Function):
             dq_acc = torch.empty((B, Tq, Hq, D), dtype=torch.float32, device=dev) if plan.needs_dq_accum else None
             dk_acc = dv_acc = None
             if plan.kv_split > 1:
-                # atomic path: zeroed accumulators; deterministic path: one fully
+                # fused atomic kernel: zeroed accumulators; otherwise one fully
                 # overwritten fp32 slab per head-group split.
-                alloc = torch.zeros if ctx.use_atomic_backward else torch.empty
+                alloc = torch.zeros if plan.dkv_accum_zeroed else torch.empty
                 dk_acc = alloc((plan.dkv_accum_elems,), dtype=torch.float32, device=dev)
                 dv_acc = alloc((plan.dkv_accum_elems,), dtype=torch.float32, device=dev)
 
             p.q, p.k, p.v, p.o, p.dout = q.data_ptr(), k.data_ptr(), v.data_ptr(), O.data_ptr(), do.data_ptr()
             p.lse, p.delta, p.dead_flags = LSE.data_ptr(), delta.data_ptr(), dead.data_ptr()
             p.mask, p.score = _ext.ptr(mask), _ext.ptr(score)
-            # deterministic path: dS tiles handed from the dK/dV kernel to the dQ kernel
+            p.mask_ws = _ext.ptr(mask_ws)
+            # dS tiles handed from the dK/dV kernel to the dQ kernel
             ds = torch.empty((plan.ds_elems,), dtype=q.dtype, device=dev) if plan.ds_elems else None
             p.dq_accum, p.dk_accum, p.dv_accum = _ext.ptr(dq_acc), _ext.ptr(dk_acc), _ext.ptr(dv_acc)
             p.ds_tiles = _ext.ptr(ds)

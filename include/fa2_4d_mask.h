@@ -15,6 +15,10 @@
  *  - Mask is bool (1 byte, 0 = drop, nonzero = keep) and Score is fp32, both
  *    logically [B, Hq, Tq, Tk] with the key dimension contiguous; a batch or
  *    head stride of 0 broadcasts (e.g. a [B, 1, Tq, Tk] mask).
+ *  - A mask is first turned into a prepared-mask workspace by fa_mask_prepare
+ *    (bits, 32x32 block states, lists of live tiles); fa_fwd and fa_bwd take
+ *    that workspace (mask_ws) beside the mask and skip tiles without a kept
+ *    entry.
  *  - LSE is fp32 [B, Hq, Tq] contiguous, base-2 log-sum-exp of the scaled
  *    logits; +inf marks a row with no kept key.  Internal fwd->bwd contract.
  *  - Every entry point validates its arguments before touching the GPU and
@@ -32,7 +36,7 @@
 extern "C" {
 #endif
 
-#define FA_ABI_VERSION 2
+#define FA_ABI_VERSION 3
 
 enum FaDtype { FA_DTYPE_BF16 = 0, FA_DTYPE_FP16 = 1 };
 
@@ -68,6 +72,7 @@ typedef struct FaFwdParams {
   int32_t is_causal;             /* keep j <= i (top-left aligned) */
   int32_t dtype;                 /* enum FaDtype */
   void* stream;                  /* hipStream_t; NULL = default stream */
+  const void* mask_ws;           /* prepared mask (fa_mask_prepare of this mask); required with a mask */
 } FaFwdParams;
 
 /* Backward problem.  Reuses the forward's inputs plus O, LSE and dO. */
@@ -80,7 +85,7 @@ typedef struct FaBwdParams {
   int32_t* dead_flags;           /* workspace [B * Hk] int32, zeroed by the caller */
   const uint8_t* mask; const float* score;
   float* dq_accum;               /* workspace [B, Hq, Tq, D] fp32 contiguous, head-major (atomic dQ) */
-  float* dk_accum;               /* workspace [B, Tk, Hk, D] fp32 zeroed, only when plan.kv_split > 1 */
+  float* dk_accum;               /* workspace of plan.dkv_accum_elems fp32, only when plan.kv_split > 1 */
   float* dv_accum;               /* idem */
   void* dq; void* dk; void* dv;  /* outputs, dtype, strided like q/k/v */
   int64_t q_stride_b, q_stride_t, q_stride_h;
@@ -102,7 +107,23 @@ typedef struct FaBwdParams {
   void* stream;
   void* ds_tiles;                /* workspace of plan.ds_elems 16-bit values (deterministic path), else unused */
   int64_t ds_limit_bytes;        /* largest dS workspace the caller accepts; 0 = 8 GiB, < 0 = none */
+  const void* mask_ws;           /* prepared mask, as for fa_fwd; required with a mask */
 } FaBwdParams;
+
+/* Mask preparation: the bool mask of a problem turned into the workspace the
+ * attention kernels read (the mask as bits, row-major and transposed; the
+ * state of every 32x32 block; per work unit of each kernel the list of tiles
+ * holding a kept entry, causality included).  The workspace depends on the
+ * mask's contents, its batch/head broadcast (stride 0), the sizes and
+ * is_causal, and serves every fa_fwd / fa_bwd call with those. */
+typedef struct FaMaskParams {
+  const uint8_t* mask;           /* logical [B, Hq, Tq, Tk] by strides, key axis contiguous */
+  int64_t mask_stride_b, mask_stride_h, mask_stride_q;
+  int32_t batch, seqlen_q, seqlen_k, heads_q;
+  int32_t is_causal;
+  void* workspace;               /* fa_mask_plan bytes, 256-byte aligned, written by fa_mask_prepare */
+  void* stream;
+} FaMaskParams;
 
 /* What fa_bwd will do for a problem, so the caller can size workspaces. */
 typedef struct FaBwdPlan {
@@ -110,9 +131,22 @@ typedef struct FaBwdPlan {
   int32_t needs_dq_accum;        /* 1 if dq_accum is used */
   int64_t dq_accum_elems;        /* B*Tq*Hq*D when used, else 0 */
   int64_t dkv_accum_elems;       /* B*Tk*Hk*D when kv_split > 1, else 0 */
-  int64_t ds_elems;              /* atomic_dq = 0: size of ds_tiles (dS of every kept 32x32 block, 16-bit),
-                                    0 when it would exceed ds_limit_bytes (dQ is then recomputed) */
+  int64_t ds_elems;              /* size of ds_tiles (dS of every stored 32x32 block, 16-bit), 0 when it
+                                    would exceed ds_limit_bytes: dQ is then recomputed (atomic_dq = 0) or
+                                    added per key block by the fused dK/dV kernel (atomic_dq = 1) */
+  int32_t dkv_accum_zeroed;      /* 1: dk_accum/dv_accum must be zeroed by the caller (fused atomic kernel) */
+  int32_t dq_split;              /* atomic_dq = 1 with dS tiles: key ranges whose dQ partials are added */
 } FaBwdPlan;
+
+/* Size in bytes of the prepared-mask workspace for *p (no launch, no GPU access). */
+int fa_mask_plan(const FaMaskParams* p, int64_t* workspace_bytes);
+
+/* Writes the prepared-mask workspace.  Replaces the per-tile mask loads of the
+ * reference kernels (python/fa2.py:107-114, 261-280, 385-404) with one pass over the
+ * mask; the reference materialises the broadcast mask instead
+ * (python/modeling_attention.py:48-59).  Must precede the fa_fwd / fa_bwd calls that
+ * read the workspace on the same stream. */
+int fa_mask_prepare(const FaMaskParams* p);
 
 /* Forward.  Replaces the reference's `flash_attention_fwd_with_4d_mask`
  * (python/fa2.py:22-139) as launched by `_flash_attention_with_4d_mask.forward`
@@ -128,20 +162,24 @@ int fa_bwd_preprocess(const FaBwdParams* p);
 /* Backward main pass.  Replaces `flash_attention_bwd_with_4d_mask_atomic`
  * (python/fa2.py:181-302, launched at :530-534) when atomic_dq = 1 and
  * `flash_attention_bwd_with_4d_mask_reduce` (python/fa2.py:305-426, launched at
- * :543-547) when atomic_dq = 0.  atomic_dq = 1: one kernel; dK/dV are written in
- * dtype (kv_split = 1) or added to dk_accum/dv_accum, dQ is added to dq_accum.
- * atomic_dq = 0: the dK/dV kernel only (dK/dV in dtype or per-split slabs); with
- * plan.ds_elems > 0 it also stores dS into ds_tiles for fa_bwd_finalize.
- * Must follow fa_bwd_preprocess on the same stream. */
+ * :543-547) when atomic_dq = 0.  With plan.ds_elems > 0 (both modes): the dK/dV
+ * kernel, writing dK/dV in dtype (kv_split = 1) or per-split fp32 slabs, and
+ * storing dS into ds_tiles for fa_bwd_finalize.  With plan.ds_elems = 0 and
+ * atomic_dq = 1: one fused kernel that also adds dQ into dq_accum with fp32
+ * atomics (dK/dV added into zeroed dk_accum/dv_accum when kv_split > 1); with
+ * atomic_dq = 0: the dK/dV kernel only.  Must follow fa_bwd_preprocess on the
+ * same stream. */
 int fa_bwd(const FaBwdParams* p);
 
-/* Backward finalisation.  atomic_dq = 1: dq from the fp32 dq_accum; atomic_dq = 0:
- * the deterministic dQ kernel writing dq in dtype (dQ = scale dS K over ds_tiles
- * when plan.ds_elems > 0, otherwise recomputing S, P and dP).  Both: dk, dv from
- * dk_accum/dv_accum when kv_split > 1.  Replaces the casts of python/fa2.py:535-536,
- * the group sum of python/fa2.py:548-549 and autograd's cast of the fp32 dQ the
- * reference returns (python/fa2.py:527, 556); the deterministic dQ replaces the dQ
- * atomics of python/fa2.py:295-297, 420-421.  Must follow fa_bwd on the same stream. */
+/* Backward finalisation.  dQ: from ds_tiles, dQ = scale dS K, written in dtype
+ * (atomic_dq = 0) or added as fp32 partials over plan.dq_split key ranges into
+ * dq_accum with atomics and converted (atomic_dq = 1); without ds_tiles,
+ * recomputed from S, P and dP (atomic_dq = 0) or converted from the dq_accum the
+ * fused kernel filled (atomic_dq = 1).  dk, dv from dk_accum/dv_accum when
+ * kv_split > 1.  Replaces the casts of python/fa2.py:535-536, the group sum of
+ * python/fa2.py:548-549 and autograd's cast of the fp32 dQ the reference returns
+ * (python/fa2.py:527, 556); the dS-based dQ replaces the per-64-key dQ atomics of
+ * python/fa2.py:295-297, 420-421.  Must follow fa_bwd on the same stream. */
 int fa_bwd_finalize(const FaBwdParams* p);
 
 /* Fills *plan for the problem in *p (no launch, no GPU access). */

@@ -61,7 +61,7 @@ def test_struct_layout_matches_header(tmp_path):
     ext = _ext()
     lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void) {"]
     for cname, cls in (("FaFwdParams", ext.FaFwdParams), ("FaBwdParams", ext.FaBwdParams),
-                       ("FaBwdPlan", ext.FaBwdPlan)):
+                       ("FaBwdPlan", ext.FaBwdPlan), ("FaMaskParams", ext.FaMaskParams)):
         lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
         for fname, _ in cls._fields_:
             lines.append(f'printf("{cname} {fname} %zu\\n", offsetof({cname}, {fname}));')
@@ -77,7 +77,7 @@ def test_struct_layout_matches_header(tmp_path):
             parts = line.split()
             got[(parts[0], parts[1])] = int(parts[2])
     for cname, cls in (("FaFwdParams", ext.FaFwdParams), ("FaBwdParams", ext.FaBwdParams),
-                       ("FaBwdPlan", ext.FaBwdPlan)):
+                       ("FaBwdPlan", ext.FaBwdPlan), ("FaMaskParams", ext.FaMaskParams)):
         assert got[(cname, "size")] == ctypes.sizeof(cls), cname
         for fname, _ in cls._fields_:
             assert got[(cname, fname)] == getattr(cls, fname).offset, (cname, fname)
@@ -134,6 +134,8 @@ FWD_ERRORS = [
     (dict(lse=None), 1, "lse is NULL"),
     (dict(mask=FAKE, mask_stride_q=-1), 5, "non-negative"),
     (dict(score=FAKE, score_stride_h=-4), 5, "non-negative"),
+    (dict(mask=FAKE), 8, "prepared workspace"),
+    (dict(mask=FAKE, mask_ws=FAKE + 16), 5, "mask_ws must be 256-byte aligned"),
 ]
 
 
@@ -149,6 +151,8 @@ def test_null_params(lib):
     assert lib.fa_bwd_preprocess(None) == 1
     assert lib.fa_bwd_finalize(None) == 1
     assert lib.fa_bwd_plan(None, None) == 1
+    assert lib.fa_mask_plan(None, None) == 1
+    assert lib.fa_mask_prepare(None) == 1
 
 
 BWD_ERRORS = [
@@ -160,6 +164,8 @@ BWD_ERRORS = [
     (dict(dead_flags=None), 1, "dead_flags is NULL"),
     (dict(dk_stride_h=100), 5, "multiples of 8"),
     (dict(head_dim=32), 3, "head_dim 32"),
+    (dict(mask=FAKE, ds_tiles=FAKE), 8, "prepared workspace"),
+    (dict(ds_tiles=None), 8, "needs ds_tiles"),
 ]
 
 
@@ -188,7 +194,13 @@ def test_plan_headline_needs_no_split(lib):
 def test_plan_ds_tiles(lib):
     # causal 8192 x 8192: 256 query steps x 256 key steps, lower triangle with
     # the diagonal = 256 * 257 / 2 tiles of 32 x 32 per head
-    assert _plan(lib).ds_elems == 0    # atomic path: no dS tiles
+    # both modes hand dS over when it fits; the atomic one splits the key range
+    plan = _plan(lib)
+    assert plan.ds_elems == 32 * 256 * 256 * 1024 and plan.dq_split == 2
+    assert _plan(lib, atomic_dq=0).dq_split == 1
+    # ... and falls back to the fused atomic kernel when it does not
+    plan = _plan(lib, ds_limit_bytes=-1)
+    assert plan.ds_elems == 0 and plan.dq_split == 1
     plan = _plan(lib, atomic_dq=0, is_causal=1)
     assert plan.ds_elems == 32 * (256 * 257 // 2) * 1024
     plan = _plan(lib, atomic_dq=0)
@@ -215,10 +227,13 @@ def test_det_path_needs_ds_tiles(lib):
 def test_plan_mqa_splits_the_group(lib):
     # BASELINE config M: B1 Tq2048 Tk16384 Hq32 Hk1 D64 -> 128 key tiles; split 4 -> 512 workgroups
     m = dict(seqlen_q=2048, seqlen_k=16384, heads_q=32, heads_k=1, head_dim=64)
-    plan = _plan(lib, **m)
-    assert plan.kv_split == 4 and plan.dkv_accum_elems == 16384 * 64
-    plan = _plan(lib, atomic_dq=0, **m)
-    assert plan.kv_split == 4 and plan.dkv_accum_elems == 4 * 16384 * 64
+    for atomic in (0, 1):   # pipelined dK/dV kernel: one slab per split, no zeroing
+        plan = _plan(lib, atomic_dq=atomic, **m)
+        assert plan.kv_split == 4 and plan.dkv_accum_elems == 4 * 16384 * 64 and plan.dkv_accum_zeroed == 0
+    assert _plan(lib, **m).dq_split == 4   # 256 dQ workgroups -> 4 key ranges
+    # fused atomic kernel (no dS workspace): one zeroed accumulator
+    plan = _plan(lib, ds_limit_bytes=-1, **m)
+    assert plan.kv_split == 4 and plan.dkv_accum_elems == 16384 * 64 and plan.dkv_accum_zeroed == 1
     plan = _plan(lib, kv_split=8, **m)
     assert plan.kv_split == 8
 
@@ -226,3 +241,66 @@ def test_plan_mqa_splits_the_group(lib):
 def test_missing_library_fails_loudly(tmp_path):
     with pytest.raises(RuntimeError, match="not built"):
         _ext().load_library(tmp_path / "nope.so")
+
+
+def mask_params(**over):
+    ext = _ext()
+    p = ext.FaMaskParams()
+    p.mask = FAKE
+    p.mask_stride_b, p.mask_stride_h, p.mask_stride_q = 0, 0, 4096
+    p.batch, p.seqlen_q, p.seqlen_k, p.heads_q = 2, 4096, 4096, 32
+    for k, v in over.items():
+        setattr(p, k, v)
+    return p
+
+
+def _mask_bytes(lib, **over):
+    n = ctypes.c_int64(-1)
+    assert lib.fa_mask_plan(ctypes.byref(mask_params(**over)), ctypes.byref(n)) == 0
+    return n.value
+
+
+def _a256(x):
+    return (x + 255) // 256 * 256
+
+
+def test_mask_plan_sizes(lib):
+    # config P: mask [2, 1, 4096, 4096] -> batch kept (stride != 0), heads broadcast: 2 planes
+    T = 4096
+    per = dict(bits=T * 128 * 4, bitsT=T * 128 * 4, blk=128 * 128, lfwd=16 * 65 * 4, lkv=32 * 129 * 4,
+               ldq=16 * 129 * 4)
+    off = 0
+    for k in ("bits", "bitsT", "blk", "lfwd", "lkv", "ldq"):
+        off = _a256(off + 2 * per[k])
+    assert _mask_bytes(lib, mask_stride_b=T * T) == off
+    # broadcast over batch too: one plane; full head extent: 64 planes
+    assert _mask_bytes(lib) < _mask_bytes(lib, mask_stride_b=T * T)
+    assert _mask_bytes(lib, mask_stride_b=32 * T * T, mask_stride_h=T * T) > 30 * _mask_bytes(lib, mask_stride_b=T * T)
+    # ragged sizes: words padded to 16 bytes per row
+    n = _mask_bytes(lib, batch=1, seqlen_q=33, seqlen_k=65, heads_q=1)
+    bits = 33 * 4 * 4          # nk32 = 3 -> wk = 4
+    bitsT = _a256(bits) + 65 * 4 * 4
+    assert n >= bitsT
+
+
+MASK_ERRORS = [
+    (dict(batch=0), 2, "sizes must be"),
+    (dict(seqlen_k=0), 2, "sizes must be"),
+    (dict(mask=None), 1, "mask is NULL"),
+    (dict(mask_stride_q=-1), 5, "non-negative"),
+]
+
+
+@pytest.mark.parametrize("over,code,msg", MASK_ERRORS, ids=[e[2] for e in MASK_ERRORS])
+def test_mask_validation(lib, over, code, msg):
+    n = ctypes.c_int64(0)
+    assert lib.fa_mask_plan(ctypes.byref(mask_params(**over)), ctypes.byref(n)) == code
+    assert msg in lib.fa_last_error().decode()
+    assert lib.fa_mask_prepare(ctypes.byref(mask_params(**over))) == code
+
+
+def test_mask_prepare_needs_aligned_workspace(lib):
+    assert lib.fa_mask_prepare(ctypes.byref(mask_params())) == 8
+    assert "workspace is NULL" in lib.fa_last_error().decode()
+    assert lib.fa_mask_prepare(ctypes.byref(mask_params(workspace=FAKE + 64))) == 5
+    assert "256-byte aligned" in lib.fa_last_error().decode()

@@ -131,9 +131,11 @@ SMALL = [
 ]
 
 
-# backward modes: fp32-atomic dQ; deterministic with dQ from the stored dS
+# backward modes: fp32-atomic dQ over key ranges of the stored dS (default);
+# fp32-atomic dQ fused into the dK/dV kernel (no dS workspace); deterministic
+# with dQ from the stored dS
 # tiles; deterministic with dQ recomputed (no dS workspace allowed)
-MODES = {"atomic": (True, 0), "det_ds": (False, 0), "det_recompute": (False, -1)}
+MODES = {"atomic": (True, 0), "atomic_fused": (True, -1), "det_ds": (False, 0), "det_recompute": (False, -1)}
 
 
 @pytest.mark.parametrize("mode", list(MODES))
