@@ -269,7 +269,7 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
       mreg = 0;
       if (live) {
         const uint32_t* bt = (const uint32_t*)(a.mws + a.ml.bitsT + mask_plane(a.ml, b, it_h) * a.ml.pbitsT);
-        mreg = bt[(int64_t)kc * a.ml.wq + (it_qs >> 5)] >> (4 * hf);
+        mreg = bt[((int64_t)(kc >> 5) * a.ml.wq + (it_qs >> 5)) * 32 + (kc & 31)] >> (4 * hf);
       }
     }
     if constexpr (SCORE) {

@@ -16,7 +16,8 @@ constexpr int kDqDsRows = 256;   // dQ from dS: query rows per workgroup, 32-key
 // One plane per (mask batch, mask head): Bm = 1 when the mask's batch stride
 // is 0 (broadcast), else B; Hm likewise over the query heads.  Per plane:
 //   bits   uint32 [Tq][wk]      bit j%32 of word j/32 = keep(i, j); zero past Tk
-//   bitsT  uint32 [Tk][wq]      bit i%32 of word i/32 = keep(i, j); zero past Tq
+//   bitsT  uint32 [nk32][wq][32] word (j/32, i/32, j%32): bit i%32 = keep(i, j);
+//                               zero past Tq (32 keys of one row word: one 128-byte line)
 //   blk    uint8  [nq32][nk32]  32x32 block: 0 no kept entry, 1 some, 2 all (in bounds)
 //   lfwd   int32  [nfq][1+nft]  per 256-row block: count, then the live 64-key
 //                               tiles ascending, bit 31 set when every block is 2
@@ -46,7 +47,7 @@ __host__ __device__ inline MaskLayout mask_layout(int B, int Hq, int Tq, int Tk,
   m.nkb = (Tk + kKv2Keys - 1) / kKv2Keys;
   m.ndq = (Tq + kDqDsRows - 1) / kDqDsRows;
   m.pbits = (int64_t)Tq * m.wk * 4;
-  m.pbitsT = (int64_t)Tk * m.wq * 4;
+  m.pbitsT = (int64_t)m.nk32 * m.wq * 32 * 4;
   m.pblk = (int64_t)m.nq32 * m.nk32;
   m.plfwd = (int64_t)m.nfq * (1 + m.nft) * 4;
   m.plkv = (int64_t)m.nkb * (1 + m.nq32) * 4;

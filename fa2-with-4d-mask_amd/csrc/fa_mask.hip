@@ -13,8 +13,8 @@
 namespace fa {
 namespace {
 
-constexpr int kRows = 128;   // rows per workgroup of the bits kernel
-constexpr int kKeys = 256;   // keys per workgroup
+constexpr int kRows = 32;     // rows per workgroup of the bits kernel (one row word)
+constexpr int kKeys = 1024;   // keys per workgroup (1 KB of each row)
 
 // Bit j of the result = (byte j of x) != 0, for the 4 bytes of x.
 __device__ __forceinline__ uint32_t nz4(uint32_t x) {
@@ -25,11 +25,12 @@ __device__ __forceinline__ uint32_t nz4(uint32_t x) {
   return ((t * 0x01020408u) >> 24) & 0xfu;  // gathered into bits 0..3 (no carries)
 }
 
-// Grid (key chunk of 256, row chunk of 128, plane).  Thread t handles rows
-// 32 rr + t/8 (rr = 0..3) x keys 32 (t%8) .. +31 of the chunk: 256 contiguous
-// bytes per 8 threads.
+// Grid (key chunk of 1024, row block of 32, plane).  Thread t reads rows
+// t/32 + 8 i (i = 0..3), keys 32 (t%32) .. +31 of the chunk: a wave reads two
+// whole 1 KB row segments per instruction pair, and every word written (bits
+// row-major, bitsT per key block) lands in full 128-byte lines.
 __global__ __launch_bounds__(256) void mask_bits_kernel(const MaskArgs a) {
-  __shared__ uint32_t words[kRows][9];
+  __shared__ uint32_t words[kRows][kKeys / 32 + 1];
   const MaskLayout& ml = a.ml;
   const int tid = threadIdx.x;
   const int kc0 = blockIdx.x * kKeys, r0 = blockIdx.y * kRows, pm = blockIdx.z;
@@ -40,60 +41,68 @@ __global__ __launch_bounds__(256) void mask_bits_kernel(const MaskArgs a) {
   uint32_t* bitsT = (uint32_t*)(a.ws + ml.bitsT + pm * ml.pbitsT);
   uint8_t* blk = (uint8_t*)(a.ws + ml.blk + pm * ml.pblk);
 
-  const int c = tid & 7, kbase = kc0 + 32 * c, wcol = kc0 / 32 + c;
+  const int c = tid & 31, kbase = kc0 + 32 * c, wcol = kc0 / 32 + c;
+  // all rows' bytes are loaded before any word is stored (the stores could
+  // alias the mask as far as the compiler knows)
+  const bool vec = a.vec16 && kbase + 32 <= Tk;
+  u32x4 x[4][2];
 #pragma unroll
-  for (int rr = 0; rr < 4; ++rr) {
-    const int rl = 32 * rr + (tid >> 3), row = r0 + rl;
-    uint32_t w = 0;
-    if (row < Tq && kbase < Tk) {
+  for (int i = 0; i < 4; ++i) {
+    const int row = r0 + (tid >> 5) + 8 * i;
+    x[i][0] = x[i][1] = u32x4{0, 0, 0, 0};
+    if (vec && row < Tq) {
       const uint8_t* p = src + row * a.msq + kbase;
-      if (a.vec16 && kbase + 32 <= Tk) {
-        const u32x4 x0 = *(const u32x4*)p, x1 = *(const u32x4*)(p + 16);
+      x[i][0] = *(const u32x4*)p;
+      x[i][1] = *(const u32x4*)(p + 16);
+    }
+  }
 #pragma unroll
-        for (int j = 0; j < 4; ++j) w |= nz4(x0[j]) << (4 * j);
+  for (int i = 0; i < 4; ++i) {
+    const int rl = (tid >> 5) + 8 * i, row = r0 + rl;
+    uint32_t w = 0;
+    if (vec) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) w |= nz4(x1[j]) << (16 + 4 * j);
-      } else {
-        const int n = min(32, Tk - kbase);
-        for (int j = 0; j < n; ++j) w |= (uint32_t)(p[j] != 0) << j;
-      }
+      for (int j = 0; j < 4; ++j) w |= nz4(x[i][0][j]) << (4 * j);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) w |= nz4(x[i][1][j]) << (16 + 4 * j);
+    } else if (row < Tq && kbase < Tk) {
+      const uint8_t* p = src + row * a.msq + kbase;
+      const int n = min(32, Tk - kbase);
+      for (int j = 0; j < n; ++j) w |= (uint32_t)(p[j] != 0) << j;
     }
     words[rl][c] = w;
     if (row < Tq && wcol < ml.wk) bits[(int64_t)row * ml.wk + wcol] = w;   // padding words are written as 0
   }
   __syncthreads();
 
-  // transposed: thread t = key kc0 + t, words of rows r0 .. r0 + 127 (4 words)
-  {
-    const int kk = kc0 + tid;
-    if (kk < Tk) {
-      u32x4 out;
+  // transposed: thread t -> keys kc0 + t + 256 j (j = 0..3), the row word of
+  // this block's 32 rows; the 32 keys of a key block fill one 128-byte line
+  const int s = r0 / 32;
 #pragma unroll
-      for (int rw = 0; rw < 4; ++rw) {
-        uint32_t w = 0;
+  for (int j = 0; j < 4; ++j) {
+    const int kl = tid + 256 * j, kk = kc0 + kl;
+    if (kk < Tk) {
+      uint32_t w = 0;
 #pragma unroll 8
-        for (int r = 0; r < 32; ++r) w |= ((words[32 * rw + r][tid >> 5] >> (tid & 31)) & 1u) << r;
-        out[rw] = w;
-      }
-      *(u32x4*)(bitsT + (int64_t)kk * ml.wq + r0 / 32) = out;
+      for (int r = 0; r < 32; ++r) w |= ((words[r][kl >> 5] >> (kl & 31)) & 1u) << r;
+      bitsT[((int64_t)(kk >> 5) * ml.wq + s) * 32 + (kk & 31)] = w;
     }
   }
 
-  // block states: thread t < 32 -> row block rw = t/8, key block c = t%8
+  // block states of the 32 key blocks: thread t < 32 -> key block kc0/32 + t
   if (tid < 32) {
-    const int rw = tid >> 3, cb = tid & 7;
-    const int rb = r0 / 32 + rw, kb = kc0 / 32 + cb;
-    if (rb < ml.nq32 && kb < ml.nk32) {
+    const int kb = kc0 / 32 + tid;
+    if (kb < ml.nk32) {
       const int nk = min(32, Tk - 32 * kb);
       const uint32_t vm = nk >= 32 ? 0xffffffffu : ((1u << nk) - 1u);
-      const int nr = min(32, Tq - 32 * rb);
+      const int nr = min(32, Tq - r0);
       uint32_t any = 0, all = vm;
       for (int r = 0; r < nr; ++r) {
-        const uint32_t w = words[32 * rw + r][cb] & vm;
+        const uint32_t w = words[r][tid] & vm;
         any |= w;
         all &= w;
       }
-      blk[(int64_t)rb * ml.nk32 + kb] = any == 0 ? 0 : (all == vm ? 2 : 1);
+      blk[(int64_t)s * ml.nk32 + kb] = any == 0 ? 0 : (all == vm ? 2 : 1);
     }
   }
 }

@@ -267,7 +267,7 @@ def _a256(x):
 def test_mask_plan_sizes(lib):
     # config P: mask [2, 1, 4096, 4096] -> batch kept (stride != 0), heads broadcast: 2 planes
     T = 4096
-    per = dict(bits=T * 128 * 4, bitsT=T * 128 * 4, blk=128 * 128, lfwd=16 * 65 * 4, lkv=32 * 129 * 4,
+    per = dict(bits=T * 128 * 4, bitsT=128 * 128 * 32 * 4, blk=128 * 128, lfwd=16 * 65 * 4, lkv=32 * 129 * 4,
                ldq=16 * 129 * 4)
     off = 0
     for k in ("bits", "bitsT", "blk", "lfwd", "lkv", "ldq"):
@@ -279,7 +279,7 @@ def test_mask_plan_sizes(lib):
     # ragged sizes: words padded to 16 bytes per row
     n = _mask_bytes(lib, batch=1, seqlen_q=33, seqlen_k=65, heads_q=1)
     bits = 33 * 4 * 4          # nk32 = 3 -> wk = 4
-    bitsT = _a256(bits) + 65 * 4 * 4
+    bitsT = _a256(bits) + 3 * 4 * 32 * 4   # nk32 = 3 key blocks x wq = 4 words x 32 keys
     assert n >= bitsT
 
 

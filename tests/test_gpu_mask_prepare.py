@@ -27,7 +27,7 @@ def layout(B, Hq, Tq, Tk, bcast_b, bcast_h):
     m["nfq"], m["nft"] = cdiv(Tq, FWD_ROWS), cdiv(Tk, FWD_KEYS)
     m["nkb"], m["ndq"] = cdiv(Tk, KV_KEYS), cdiv(Tq, DQ_ROWS)
     m["pbits"] = Tq * m["wk"] * 4
-    m["pbitsT"] = Tk * m["wq"] * 4
+    m["pbitsT"] = m["nk32"] * m["wq"] * 32 * 4
     m["pblk"] = m["nq32"] * m["nk32"]
     m["plfwd"] = m["nfq"] * (1 + m["nft"]) * 4
     m["plkv"] = m["nkb"] * (1 + m["nq32"]) * 4
@@ -57,7 +57,7 @@ def expected(plane_mask, Tq, Tk, causal, m):
     """Expected arrays of one plane from its [Tq, Tk] bool mask."""
     keep = plane_mask
     bits = pack_bits(keep)                      # [Tq, nk32]
-    bitsT = pack_bits(keep.t().contiguous())    # [Tk, nq32]
+    bitsT = pack_bits(keep.t().contiguous())    # [Tk, nq32]: word i/32 of key j
     nq32, nk32 = m["nq32"], m["nk32"]
     blk = torch.zeros((nq32, nk32), dtype=torch.uint8)
     for rb in range(nq32):
@@ -165,8 +165,10 @@ def test_prepared_mask_matches_definition(cuda, B, Hq, Hm, Tq, Tk, causal, kind)
         got_bits = ws32[(m["bits"] + pm * m["pbits"]) // 4:][: Tq * m["wk"]].view(Tq, m["wk"]).long() & 0xFFFFFFFF
         assert torch.equal(got_bits[:, : m["nk32"]], bits), f"bits plane {pm}"
         assert not got_bits[:, m["nk32"]:].any(), "padding words"
-        got_t = ws32[(m["bitsT"] + pm * m["pbitsT"]) // 4:][: Tk * m["wq"]].view(Tk, m["wq"]).long() & 0xFFFFFFFF
-        assert torch.equal(got_t[:, : m["nq32"]], bitsT), f"bitsT plane {pm}"
+        # [nk32][wq][32 keys] -> [key][word]
+        got_t = ws32[(m["bitsT"] + pm * m["pbitsT"]) // 4:][: m["nk32"] * m["wq"] * 32]
+        got_t = got_t.view(m["nk32"], m["wq"], 32).permute(0, 2, 1).reshape(m["nk32"] * 32, m["wq"])[:Tk]
+        assert torch.equal(got_t.long()[:, : m["nq32"]] & 0xFFFFFFFF, bitsT), f"bitsT plane {pm}"
         got_blk = ws_cpu[m["blk"] + pm * m["pblk"]:][: m["pblk"]].view(m["nq32"], m["nk32"])
         assert torch.equal(got_blk, blk), f"blk plane {pm}"
         assert read_lists(ws32, m["lfwd"] + pm * m["plfwd"], m["nfq"], 1 + m["nft"]) == lf, f"fwd lists plane {pm}"
