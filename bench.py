@@ -271,7 +271,12 @@ def main() -> int:
                 log(f"{name} {mode:15s} {ms:8.3f} ms  {entry[mode]['tflops_dense_conv']:8.1f} TFLOPS (dense conv.)"
                     f"  {entry[mode]['gbps']:8.1f} GB/s of {nbytes / 1e9:.3f} GB algorithmic  kernels {kern}")
             if x["mask"] is not None:
-                entry["mask_keep_fraction"] = round(x["mask"].float().mean().item(), 4)
+                # useful work: the dense-convention FLOPs scaled by the kept fraction of
+                # (row, key) pairs (dead tiles are skipped, so the dense figure overstates)
+                keep = x["mask"].float().mean().item()
+                entry["mask_keep_fraction"] = round(keep, 4)
+                for mode in ("fwd", "fwd_bwd", "fwd_bwd_atomic"):
+                    entry[mode]["tflops_useful"] = round(entry[mode]["tflops_dense_conv"] * keep, 2)
             entry["config"] = {"B": bq, "Tq": tq, "Tk": tk, "Hq": hq, "Hk": hk, "D": d, "layout": x["layout"],
                                "mask": None if x["mask"] is None else list(x["mask"].shape),
                                "score": None if x["score"] is None else list(x["score"].shape)}

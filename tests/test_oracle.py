@@ -294,3 +294,35 @@ def test_make_case_layouts_are_bthd_backed():
     c2 = I.make_case(cfg2, seed=0)
     assert c2["q"].shape == (2, 16, 4, 64) and c2["q"].is_contiguous()
     assert torch.equal(c2["q"].transpose(1, 2), c["q"])
+
+
+def test_dtype_probabilities_bound_the_mean_error_at_config_P():
+    """Why the strict north-star mean bar (mean_abs <= 1e-4) is out of reach at
+    config P for any kernel that feeds P to the PV product in the input dtype, as
+    the reference kernel does (python/fa2.py:128-129, acc_s cast to dtype before
+    the GEMM) and as this build does: with the maths otherwise exact (float64),
+    rounding only P to bf16 already gives mean_abs ~1.25e-4 against the bf16
+    cast of the exact output on the packed-document mask, where short documents
+    make |O| ~ 0.1.  At the headline shape the same rounding stays far below the
+    bar (long rows average the rounding out)."""
+    cfg = I.CONFIGS["P"].scaled(B=1, Hq=2, Hk=1)
+    case = I.make_case(cfg, seed=0, with_grad=False)
+
+    def mean_err(case, groups):
+        q = case["q_bhsd"].double()
+        k = case["k_bhsd"].double().repeat_interleave(groups, 1)
+        v = case["v_bhsd"].double().repeat_interleave(groups, 1)
+        s = (q @ k.transpose(-1, -2)) * q.shape[-1] ** -0.5
+        if case["mask"] is not None:
+            s = s.masked_fill(~case["mask"], float("-inf"))
+        p = torch.exp(s - s.amax(-1, keepdim=True))
+        exact = ((p @ v) / p.sum(-1, keepdim=True)).float().to(torch.bfloat16).float()
+        pb = p.to(torch.bfloat16).double()
+        rounded = ((pb @ v) / pb.sum(-1, keepdim=True)).float().to(torch.bfloat16).float()
+        return (rounded - exact).abs().mean().item()
+
+    err_p = mean_err(case, 2)
+    assert 1.1e-4 < err_p < 1.5e-4, err_p
+    hcfg = I.CONFIGS["H"].scaled(Hq=1, Hk=1, Tq=512)     # headline rows (Tk 8192), a 512-row slice
+    err_h = mean_err(I.make_case(hcfg, seed=0, with_grad=False), 1)
+    assert err_h < 3e-5, err_h
