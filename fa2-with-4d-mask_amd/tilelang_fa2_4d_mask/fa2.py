@@ -149,7 +149,128 @@ def _call(lib, entry: str, params) -> None:
     _ext.check(status, entry, lib)
 
 
+def _check_qkv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> None:
+    if not q.is_cuda:
+        raise ValueError("flash_attention_with_4d_mask runs on the GPU: inputs must be HIP/CUDA tensors")
+    if k.device != q.device or v.device != q.device:
+        raise ValueError("query, key and value must be on the same device")
+    if k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError("query, key, and value must have the same dtype")
+    _ext.dtype_code(q.dtype)
+
+
+def _forward_impl(q, k, v, Mask, Score, scale: float, is_causal: bool):
+    """Host side of the forward (python/fa2.py:438-488) on logical [B, T, H, D]
+    operands: O [B, Tq, Hq, D], LSE [B, Hq, Tq] and the prepared mask (or None),
+    plus the operands as the kernels saw them."""
+    B, Tq, Hq, D = q.shape
+    _, Tk, Hk, _ = k.shape
+    mask, mst = _kernel_side(Mask, torch.bool, B, Hq, Tq, Tk, "mask", q.device)
+    score, sst = _kernel_side(Score, torch.float32, B, Hq, Tq, Tk, "score", q.device)
+    O = torch.empty((B, Tq, Hq, D), dtype=q.dtype, device=q.device)
+    LSE = torch.empty((B, Hq, Tq), dtype=torch.float32, device=q.device)
+    mask_ws = None
+    if B * Tq * Hq > 0:
+        if Tk == 0:
+            O.zero_()
+            LSE.fill_(float("-inf"))
+        else:
+            q = _kernel_operand(q)
+            k = _kernel_operand(k)
+            v = _kernel_operand(v)
+            if mask is not None:
+                mask_ws = _prepare_mask(mask, mst, B, Hq, Tq, Tk, bool(is_causal), q.device)
+            p = _ext.FaFwdParams()
+            p.q, p.k, p.v, p.o, p.lse = q.data_ptr(), k.data_ptr(), v.data_ptr(), O.data_ptr(), LSE.data_ptr()
+            p.mask, p.score = _ext.ptr(mask), _ext.ptr(score)
+            p.q_stride_b, p.q_stride_t, p.q_stride_h = _bthd_strides(q)
+            p.k_stride_b, p.k_stride_t, p.k_stride_h = _bthd_strides(k)
+            p.v_stride_b, p.v_stride_t, p.v_stride_h = _bthd_strides(v)
+            p.o_stride_b, p.o_stride_t, p.o_stride_h = _bthd_strides(O)
+            p.mask_stride_b, p.mask_stride_h, p.mask_stride_q = mst
+            p.score_stride_b, p.score_stride_h, p.score_stride_q = sst
+            p.batch, p.seqlen_q, p.seqlen_k, p.heads_q, p.heads_k, p.head_dim = B, Tq, Tk, Hq, Hk, D
+            p.scale = scale
+            p.is_causal = 1 if is_causal else 0
+            p.dtype = _ext.dtype_code(q.dtype)
+            p.stream = _stream(q.device)
+            p.mask_ws = _ext.ptr(mask_ws)
+            _call(_ext.load_library(), "fa_fwd", p)
+    return O, LSE, mask_ws, (q, k, v, mask, score, mst, sst)
+
+
+def _backward_impl(do, q, k, v, O, LSE, mask, score, mask_ws, mst, sst, scale: float, is_causal: bool,
+                   use_atomic_backward: bool):
+    """Host side of the backward (python/fa2.py:490-556) on logical [B, T, H, D]
+    operands as the forward's kernels saw them; returns dQ, dK, dV in the
+    input dtype, [B, T, H, D] contiguous."""
+    B, Tq, Hq, D = q.shape
+    _, Tk, Hk, _ = k.shape
+    dev = q.device
+    dQ = torch.empty((B, Tq, Hq, D), dtype=q.dtype, device=dev)
+    dK = torch.empty((B, Tk, Hk, D), dtype=q.dtype, device=dev)
+    dV = torch.empty((B, Tk, Hk, D), dtype=q.dtype, device=dev)
+    if B * Tq * Hq == 0 or Tk == 0:
+        dQ.zero_()
+        dK.zero_()
+        dV.zero_()
+        return dQ, dK, dV
+    do = _kernel_operand(do.to(q.dtype))
+    p = _ext.FaBwdParams()
+    p.batch, p.seqlen_q, p.seqlen_k, p.heads_q, p.heads_k, p.head_dim = B, Tq, Tk, Hq, Hk, D
+    p.scale = scale
+    p.is_causal = 1 if is_causal else 0
+    p.atomic_dq = 1 if use_atomic_backward else 0
+    p.kv_split = 0
+    p.dtype = _ext.dtype_code(q.dtype)
+    p.ds_limit_bytes = DS_LIMIT_BYTES
+    lib = _ext.load_library()
+    plan = _ext.FaBwdPlan()
+    _ext.check(lib.fa_bwd_plan(ctypes.byref(p), ctypes.byref(plan)), "fa_bwd_plan", lib)
+    p.kv_split = plan.kv_split
+
+    delta = torch.empty((B, Hq, Tq), dtype=torch.float32, device=dev)
+    dead = torch.zeros((B * Hk,), dtype=torch.int32, device=dev)
+    dq_acc = torch.empty((B, Tq, Hq, D), dtype=torch.float32, device=dev) if plan.needs_dq_accum else None
+    dk_acc = dv_acc = None
+    if plan.kv_split > 1:
+        # fused atomic kernel: zeroed accumulators; otherwise one fully
+        # overwritten fp32 slab per head-group split.
+        alloc = torch.zeros if plan.dkv_accum_zeroed else torch.empty
+        dk_acc = alloc((plan.dkv_accum_elems,), dtype=torch.float32, device=dev)
+        dv_acc = alloc((plan.dkv_accum_elems,), dtype=torch.float32, device=dev)
+
+    p.q, p.k, p.v, p.o, p.dout = q.data_ptr(), k.data_ptr(), v.data_ptr(), O.data_ptr(), do.data_ptr()
+    p.lse, p.delta, p.dead_flags = LSE.data_ptr(), delta.data_ptr(), dead.data_ptr()
+    p.mask, p.score = _ext.ptr(mask), _ext.ptr(score)
+    p.mask_ws = _ext.ptr(mask_ws)
+    # dS tiles handed from the dK/dV kernel to the dQ kernel
+    ds = torch.empty((plan.ds_elems,), dtype=q.dtype, device=dev) if plan.ds_elems else None
+    p.dq_accum, p.dk_accum, p.dv_accum = _ext.ptr(dq_acc), _ext.ptr(dk_acc), _ext.ptr(dv_acc)
+    p.ds_tiles = _ext.ptr(ds)
+    p.dq, p.dk, p.dv = dQ.data_ptr(), dK.data_ptr(), dV.data_ptr()
+    p.q_stride_b, p.q_stride_t, p.q_stride_h = _bthd_strides(q)
+    p.k_stride_b, p.k_stride_t, p.k_stride_h = _bthd_strides(k)
+    p.v_stride_b, p.v_stride_t, p.v_stride_h = _bthd_strides(v)
+    p.o_stride_b, p.o_stride_t, p.o_stride_h = _bthd_strides(O)
+    p.do_stride_b, p.do_stride_t, p.do_stride_h = _bthd_strides(do)
+    p.dq_stride_b, p.dq_stride_t, p.dq_stride_h = _bthd_strides(dQ)
+    p.dk_stride_b, p.dk_stride_t, p.dk_stride_h = _bthd_strides(dK)
+    p.dv_stride_b, p.dv_stride_t, p.dv_stride_h = _bthd_strides(dV)
+    p.mask_stride_b, p.mask_stride_h, p.mask_stride_q = mst
+    p.score_stride_b, p.score_stride_h, p.score_stride_q = sst
+    p.stream = _stream(dev)
+    _call(lib, "fa_bwd_preprocess", p)
+    _call(lib, "fa_bwd", p)
+    _call(lib, "fa_bwd_finalize", p)
+    return dQ, dK, dV
+
+
 class _flash_attention_with_4d_mask(torch.autograd.Function):
+    """The reference's autograd Function (python/fa2.py:437-558), kept with its
+    positional signature; ``flash_attention_with_4d_mask`` below reaches the
+    same host code through the registered custom ops instead."""
+
     @staticmethod
     def forward(
         ctx,
@@ -167,52 +288,11 @@ class _flash_attention_with_4d_mask(torch.autograd.Function):
         q = Q.transpose(1, 2) if bhsd_input else Q
         k = K.transpose(1, 2) if bhsd_input else K
         v = V.transpose(1, 2) if bhsd_input else V
-        B, Tq, Hq, D = q.shape
-        _, Tk, Hk, _ = k.shape
         if scale is None:
-            scale = D ** -0.5
+            scale = q.shape[3] ** -0.5
         scale = float(scale)
-        if not q.is_cuda:
-            raise ValueError("flash_attention_with_4d_mask runs on the GPU: inputs must be HIP/CUDA tensors")
-        if k.device != q.device or v.device != q.device:
-            raise ValueError("query, key and value must be on the same device")
-        if k.dtype != q.dtype or v.dtype != q.dtype:
-            raise ValueError("query, key, and value must have the same dtype")
-        code = _ext.dtype_code(q.dtype)
-
-        mask, mst = _kernel_side(Mask, torch.bool, B, Hq, Tq, Tk, "mask", q.device)
-        score, sst = _kernel_side(Score, torch.float32, B, Hq, Tq, Tk, "score", q.device)
-
-        O = torch.empty((B, Tq, Hq, D), dtype=q.dtype, device=q.device)
-        LSE = torch.empty((B, Hq, Tq), dtype=torch.float32, device=q.device)
-        mask_ws = None
-        if B * Tq * Hq > 0:
-            if Tk == 0:
-                O.zero_()
-                LSE.fill_(float("-inf"))
-            else:
-                q = _kernel_operand(q)
-                k = _kernel_operand(k)
-                v = _kernel_operand(v)
-                if mask is not None:
-                    mask_ws = _prepare_mask(mask, mst, B, Hq, Tq, Tk, bool(is_causal), q.device)
-                p = _ext.FaFwdParams()
-                p.q, p.k, p.v, p.o, p.lse = q.data_ptr(), k.data_ptr(), v.data_ptr(), O.data_ptr(), LSE.data_ptr()
-                p.mask, p.score = _ext.ptr(mask), _ext.ptr(score)
-                p.q_stride_b, p.q_stride_t, p.q_stride_h = _bthd_strides(q)
-                p.k_stride_b, p.k_stride_t, p.k_stride_h = _bthd_strides(k)
-                p.v_stride_b, p.v_stride_t, p.v_stride_h = _bthd_strides(v)
-                p.o_stride_b, p.o_stride_t, p.o_stride_h = _bthd_strides(O)
-                p.mask_stride_b, p.mask_stride_h, p.mask_stride_q = mst
-                p.score_stride_b, p.score_stride_h, p.score_stride_q = sst
-                p.batch, p.seqlen_q, p.seqlen_k, p.heads_q, p.heads_k, p.head_dim = B, Tq, Tk, Hq, Hk, D
-                p.scale = scale
-                p.is_causal = 1 if is_causal else 0
-                p.dtype = code
-                p.stream = _stream(q.device)
-                p.mask_ws = _ext.ptr(mask_ws)
-                _call(_ext.load_library(), "fa_fwd", p)
-
+        _check_qkv(q, k, v)
+        O, LSE, mask_ws, (q, k, v, mask, score, mst, sst) = _forward_impl(q, k, v, Mask, Score, scale, bool(is_causal))
         ctx.save_for_backward(q, k, v, O, LSE, mask, score, mask_ws)
         ctx.scale = scale
         ctx.is_causal = bool(is_causal)
@@ -226,71 +306,32 @@ class _flash_attention_with_4d_mask(torch.autograd.Function):
     def backward(ctx, dO: torch.Tensor):
         q, k, v, O, LSE, mask, score, mask_ws = ctx.saved_tensors
         do = dO.transpose(1, 2) if ctx.bhsd_input else dO
-        B, Tq, Hq, D = q.shape
-        _, Tk, Hk, _ = k.shape
-        dev = q.device
-        dQ = torch.empty((B, Tq, Hq, D), dtype=q.dtype, device=dev)
-        dK = torch.empty((B, Tk, Hk, D), dtype=q.dtype, device=dev)
-        dV = torch.empty((B, Tk, Hk, D), dtype=q.dtype, device=dev)
-        if B * Tq * Hq == 0 or Tk == 0:
-            dQ.zero_()
-            dK.zero_()
-            dV.zero_()
-        else:
-            do = _kernel_operand(do.to(q.dtype))
-            p = _ext.FaBwdParams()
-            p.batch, p.seqlen_q, p.seqlen_k, p.heads_q, p.heads_k, p.head_dim = B, Tq, Tk, Hq, Hk, D
-            p.scale = ctx.scale
-            p.is_causal = 1 if ctx.is_causal else 0
-            p.atomic_dq = 1 if ctx.use_atomic_backward else 0
-            p.kv_split = 0
-            p.dtype = _ext.dtype_code(q.dtype)
-            p.ds_limit_bytes = DS_LIMIT_BYTES
-            lib = _ext.load_library()
-            plan = _ext.FaBwdPlan()
-            _ext.check(lib.fa_bwd_plan(ctypes.byref(p), ctypes.byref(plan)), "fa_bwd_plan", lib)
-            p.kv_split = plan.kv_split
-
-            delta = torch.empty((B, Hq, Tq), dtype=torch.float32, device=dev)
-            dead = torch.zeros((B * Hk,), dtype=torch.int32, device=dev)
-            dq_acc = torch.empty((B, Tq, Hq, D), dtype=torch.float32, device=dev) if plan.needs_dq_accum else None
-            dk_acc = dv_acc = None
-            if plan.kv_split > 1:
-                # fused atomic kernel: zeroed accumulators; otherwise one fully
-                # overwritten fp32 slab per head-group split.
-                alloc = torch.zeros if plan.dkv_accum_zeroed else torch.empty
-                dk_acc = alloc((plan.dkv_accum_elems,), dtype=torch.float32, device=dev)
-                dv_acc = alloc((plan.dkv_accum_elems,), dtype=torch.float32, device=dev)
-
-            p.q, p.k, p.v, p.o, p.dout = q.data_ptr(), k.data_ptr(), v.data_ptr(), O.data_ptr(), do.data_ptr()
-            p.lse, p.delta, p.dead_flags = LSE.data_ptr(), delta.data_ptr(), dead.data_ptr()
-            p.mask, p.score = _ext.ptr(mask), _ext.ptr(score)
-            p.mask_ws = _ext.ptr(mask_ws)
-            # dS tiles handed from the dK/dV kernel to the dQ kernel
-            ds = torch.empty((plan.ds_elems,), dtype=q.dtype, device=dev) if plan.ds_elems else None
-            p.dq_accum, p.dk_accum, p.dv_accum = _ext.ptr(dq_acc), _ext.ptr(dk_acc), _ext.ptr(dv_acc)
-            p.ds_tiles = _ext.ptr(ds)
-            p.dq, p.dk, p.dv = dQ.data_ptr(), dK.data_ptr(), dV.data_ptr()
-            p.q_stride_b, p.q_stride_t, p.q_stride_h = _bthd_strides(q)
-            p.k_stride_b, p.k_stride_t, p.k_stride_h = _bthd_strides(k)
-            p.v_stride_b, p.v_stride_t, p.v_stride_h = _bthd_strides(v)
-            p.o_stride_b, p.o_stride_t, p.o_stride_h = _bthd_strides(O)
-            p.do_stride_b, p.do_stride_t, p.do_stride_h = _bthd_strides(do)
-            p.dq_stride_b, p.dq_stride_t, p.dq_stride_h = _bthd_strides(dQ)
-            p.dk_stride_b, p.dk_stride_t, p.dk_stride_h = _bthd_strides(dK)
-            p.dv_stride_b, p.dv_stride_t, p.dv_stride_h = _bthd_strides(dV)
-            p.mask_stride_b, p.mask_stride_h, p.mask_stride_q = ctx.mst
-            p.score_stride_b, p.score_stride_h, p.score_stride_q = ctx.sst
-            p.stream = _stream(dev)
-            _call(lib, "fa_bwd_preprocess", p)
-            _call(lib, "fa_bwd", p)
-            _call(lib, "fa_bwd_finalize", p)
-
+        dQ, dK, dV = _backward_impl(do, q, k, v, O, LSE, mask, score, mask_ws, ctx.mst, ctx.sst, ctx.scale,
+                                    ctx.is_causal, ctx.use_atomic_backward)
         if ctx.bhsd_input:
             dQ, dK, dV = dQ.transpose(1, 2), dK.transpose(1, 2), dV.transpose(1, 2)
         return dQ, dK, dV, None, None, None, None, None, None
 
 
-flash_attention_with_4d_mask = _flash_attention_with_4d_mask.apply
+def flash_attention_with_4d_mask(Q, K, V, Mask=None, Score=None, scale=None, is_causal=False,
+                                 use_atomic_backward=True, bhsd_input=True):
+    """``flash_attention_with_4d_mask(Q, K, V, Mask, Score, scale, is_causal,
+    use_atomic_backward, bhsd_input)`` (python/fa2.py:558): same positional
+    signature, defaults, checks and autograd behaviour as the reference's
+    ``Function.apply``; the work runs in the registered custom ops
+    ``tilelang_fa2_4d_mask::fwd`` / ``::bwd`` (ops.py), which torch.compile and
+    graph capture can trace."""
+    from . import ops
+
+    assert Q.dim() == 4 and K.dim() == 4 and V.dim() == 4
+    q = Q.transpose(1, 2) if bhsd_input else Q
+    k = K.transpose(1, 2) if bhsd_input else K
+    v = V.transpose(1, 2) if bhsd_input else V
+    if scale is None:
+        scale = q.shape[3] ** -0.5
+    _check_qkv(q, k, v)
+    O = ops.attention(q, k, v, Mask, Score, float(scale), bool(is_causal), bool(use_atomic_backward))
+    return O.transpose(1, 2) if bhsd_input else O
+
 
 __all__ = ["flash_attention_with_4d_mask", "record_kernel_events", "KernelEventLog"]

@@ -1,0 +1,55 @@
+"""The custom ops' fake (meta) implementations on the CPU (no GPU, no kernel
+runs): output shapes and dtypes, and the prepared-mask workspace size, which
+must equal what fa_mask_plan reports for the same mask view."""
+
+import ctypes
+
+import pytest
+import torch
+from torch._subclasses.fake_tensor import FakeTensorMode
+
+
+def _mods():
+    from tilelang_fa2_4d_mask import _ext, fa2, ops  # noqa: F401
+
+    return _ext, fa2, ops
+
+
+@pytest.mark.parametrize("mask_heads,mask_batch", [(1, 1), (1, 2), (8, 2)])
+def test_fake_shapes(mask_heads, mask_batch):
+    _ext, fa2, _ = _mods()
+    B, Hq, Hk, Tq, Tk, D = 2, 8, 2, 300, 500, 64
+    with FakeTensorMode():
+        q = torch.empty(B, Tq, Hq, D, dtype=torch.bfloat16, device="cuda")
+        k = torch.empty(B, Tk, Hk, D, dtype=torch.bfloat16, device="cuda")
+        mask = torch.empty(mask_batch, mask_heads, Tq, Tk, dtype=torch.bool, device="cuda")
+        O, L, ws = torch.ops.tilelang_fa2_4d_mask.fwd(q, k, k, mask, None, 0.125, True, True)
+        assert O.shape == (B, Tq, Hq, D) and O.dtype == torch.bfloat16
+        assert L.shape == (B, Hq, Tq) and L.dtype == torch.float32
+        nws = ws.shape[0]
+        dq, dk, dv = torch.ops.tilelang_fa2_4d_mask.bwd(O, q, k, k, O, L, mask, None, ws, 0.125, True, False)
+        assert dq.shape == q.shape and dk.shape == k.shape and dv.shape == k.shape
+        O2, _, ws2 = torch.ops.tilelang_fa2_4d_mask.fwd(q, k, k, None, None, 0.125, False, True)
+        assert ws2.shape == (0,)
+    # same size from the C ABI for the same broadcast
+    lib = _ext.load_library()
+    mp = _ext.FaMaskParams()
+    mp.mask = 256
+    mp.mask_stride_b = 0 if mask_batch == 1 else mask_heads * Tq * Tk
+    mp.mask_stride_h = 0 if mask_heads == 1 else Tq * Tk
+    mp.mask_stride_q = Tk
+    mp.batch, mp.seqlen_q, mp.seqlen_k, mp.heads_q, mp.is_causal = B, Tq, Tk, Hq, 1
+    n = ctypes.c_int64(0)
+    assert lib.fa_mask_plan(ctypes.byref(mp), ctypes.byref(n)) == 0
+    assert nws == n.value
+
+
+def test_public_wrapper_routes_through_the_op():
+    _, fa2, ops = _mods()
+    import inspect
+
+    src = inspect.getsource(fa2.flash_attention_with_4d_mask)
+    assert "ops.attention" in src
+    sig = inspect.signature(fa2.flash_attention_with_4d_mask)
+    assert list(sig.parameters) == ["Q", "K", "V", "Mask", "Score", "scale", "is_causal", "use_atomic_backward",
+                                    "bhsd_input"]
