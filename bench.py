@@ -17,7 +17,7 @@ fwd+bwd 14*..., x0.5 when causal.  Peak: MI355X dense bf16 MFMA 2.5 PFLOP/s.
 by ``fa_bwd`` on the deterministic path: 4 GEMMs (S, dP, dV, dK), i.e.
 8*B*Hq*Tq*Tk*D algorithmic FLOPs per launch, timed with HIP events on the
 launch stream inside the timed region.  ``traffic`` (HBM bytes per launch) is
-read from profiles/dkdv2_H_traffic.json, written from rocprofv3 FETCH_SIZE /
+read from profiles/traffic_H_S.json, written from rocprofv3 FETCH_SIZE /
 WRITE_SIZE runs scaled by a copy-kernel calibration.  ``cpu_baseline`` times
 this repository's eager fp32 oracle on the host cores on a bounded sample.
 
@@ -302,13 +302,16 @@ def main() -> int:
         if "fa_bwd" in km:
             bwd_ms = km["fa_bwd"] + km.get("fa_bwd_finalize", 0.0)
             r["bwd_tflops"] = round(10.0 * (0.5 if causal else 1.0) * B * HQ * T * T * D / (bwd_ms * 1e-3) * 1e-12, 2)
-    traffic = None
-    tpath = ROOT / "profiles" / "dkdv2_H_traffic.json"
+    traffic = traffic_fwd = traffic_dq = None
+    tpath = ROOT / "profiles" / "traffic_H_S.json"
     if tpath.exists():
         try:
-            traffic = json.loads(tpath.read_text()).get("bytes_per_launch")
-        except (OSError, ValueError):
-            traffic = None
+            kern = json.loads(tpath.read_text())["kernels"]
+            traffic = kern["dkdv2_kernel<bf16,128> H (fa_bwd, deterministic)"]["bytes_per_launch"]
+            traffic_fwd = kern["fwd_kernel<bf16,128> H (fa_fwd, non-causal)"]["bytes_per_launch"]
+            traffic_dq = kern["dq_ds_kernel<bf16,128> H (fa_bwd_finalize, deterministic)"]["bytes_per_launch"]
+        except (OSError, ValueError, KeyError):
+            traffic = traffic_fwd = traffic_dq = None
 
     line = {
         "metric": METRIC,
@@ -342,10 +345,10 @@ def main() -> int:
             "avg_launch_ms": round(dkdv_ms, 4),
             "flops_per_launch": dkdv_flops,
             "fwd_kernel": {"achieved": round(fwd_achieved, 2), "frac": round(fwd_achieved / PEAK_TFLOPS, 4),
-                           "avg_launch_ms": round(fwd_kernel_ms, 4), "unit": "TFLOP/s"},
+                           "avg_launch_ms": round(fwd_kernel_ms, 4), "unit": "TFLOP/s", "traffic": traffic_fwd},
             "dq_kernel": {"bound": "hbm", "achieved": round(dq_bytes / (dq_ms * 1e-3) * 1e-9, 1), "peak": 8000.0,
                           "unit": "GB/s", "frac": round(dq_bytes / (dq_ms * 1e-3) * 1e-9 / 8000.0, 4),
-                          "avg_launch_ms": round(dq_ms, 4), "bytes_per_launch": dq_bytes},
+                          "avg_launch_ms": round(dq_ms, 4), "bytes_per_launch": dq_bytes, "traffic": traffic_dq},
         },
     }
     if not args.no_cpu_baseline:
