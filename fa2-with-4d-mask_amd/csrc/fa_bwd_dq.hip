@@ -10,9 +10,13 @@
 // dS tile (b, h, s, kb): 32 keys x 32 query rows, row "key" of 64 bytes whose
 // 16-bit entries hold, at position p, query row
 //   perm(p) = 16 (p / 16) + 4 ((p / 8) % 2) + 8 ((p / 4) % 2) + p % 4
-// (the order in which the dK/dV kernel's lanes hold them).  ds_read_b64_tr_b16
-// over that [key][p] tile yields the B operand of dQ^T = K^T dS^T with lane
-// l = position p directly, so perm only matters when dQ rows are stored.
+// (the order in which the dK/dV kernel's lanes hold them).  In memory the
+// tile is chunk-major: 16-byte chunk c of key row k at byte c 512 + k 16 (the
+// dK/dV kernel then writes whole lines); the staging writes restore the
+// [key][64 bytes] rows in LDS, chunk c of row k at physical chunk
+// c ^ ((k / 4) % 4) (conflict-free 16-lane writes).  ds_read_b64_tr_b16 over
+// that tile yields the B operand of dQ^T = K^T dS^T with lane l = position p
+// directly, so perm only matters when dQ rows are stored.
 //
 // Work decomposition: one workgroup of 4 waves per (256 query rows, head,
 // batch[, key split]); wave w owns query steps 8 qb + 2 w, + 1 (64 rows) and
@@ -113,7 +117,9 @@ __global__ __launch_bounds__(kDqWaves * 64, 2) void dq_ds_kernel(const BwdArgs a
   // B = dS^T (transpose reads of the wave's [key][p] tiles, 64-byte rows, unswizzled)
   uint32_t bd[2];
 #pragma unroll
-  for (int hi = 0; hi < 2; ++hi) bd[hi] = opaque(lds0 + KTILE + wv * DSW + (4 * hf + rr + 8 * hi) * 64 + tr_col * 2);
+  for (int hi = 0; hi < 2; ++hi)   // rows 4 hf + rr + 8 hi (+16): chunk swizzle (row / 4) % 4 = (hf + 2 hi) % 4
+    bd[hi] = opaque(lds0 + KTILE + wv * DSW + (4 * hf + rr + 8 * hi) * 64 +
+                    ((((tr_col >> 3) ^ ((hf + 2 * hi) & 3))) * 16) + (tr_col & 7) * 2);
 
   // ---- staging -----------------------------------------------------------------------
   const T* __restrict__ kbase = (const T*)a.k + b * a.ksb + kvh * a.ksh;
@@ -124,7 +130,12 @@ __global__ __launch_bounds__(kDqWaves * 64, 2) void dq_ds_kernel(const BwdArgs a
     gk[u] = (uint32_t)(r * a.kst * 2 + c * 16);
     swk[u] = opaque(lds0 + r * ROWB + ((c ^ swz_q<D>(r)) * 16));
   }
-  const uint32_t sd = opaque(lds0 + KTILE + wv * DSW + lane * 16);   // + 1024 u
+  // staging chunk u' (bytes lane 16 + u' 1024 of a tile) = chunk lane/32 + 2 u' of key lane%32
+  const int skey = lane & 31;
+  uint32_t sd[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+    sd[u] = opaque(lds0 + KTILE + wv * DSW + skey * 64 + ((((lane >> 5) + 2 * u) ^ ((skey >> 2) & 3)) * 16));
   const uint16_t* __restrict__ dsp = (const uint16_t*)a.ds;
   const int64_t plane = ((int64_t)b * a.Hq + h) * a.ds_plane;
   int64_t row0[kDqSteps];
@@ -160,7 +171,7 @@ __global__ __launch_bounds__(kDqWaves * 64, 2) void dq_ds_kernel(const BwdArgs a
 #pragma unroll
     for (int u = 0; u < UK; ++u) lds_wr16(swk[u] + BUF * BUFB, stk[S][u]);
 #pragma unroll
-    for (int u = 0; u < UD; ++u) lds_wr16(sd + BUF * BUFB + u * 1024, std_[S][u]);
+    for (int u = 0; u < UD; ++u) lds_wr16(sd[u & 1] + BUF * BUFB + (u >> 1) * 2048, std_[S][u]);
   };
 
   // ---- accumulators: dQ^T [32 nb + 8 (e/4) + 4 hf + e%4][position l32] per query step ----

@@ -292,7 +292,9 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
   // it_tile: tile of (it_h, step it_qs / 32) and this wave's keys.
   const int kb32 = __builtin_amdgcn_readfirstlane(kw0) >> 5;
   const bool ds_on = a.ds != nullptr && kb32 < a.nk32;
-  const uint32_t ds_vo = (uint32_t)(l32 * 64 + hf * 16);
+  // tile bytes are chunk-major (chunk c of key row k at c 512 + k 16): store t
+  // writes chunks 2 t + hf, i.e. one contiguous kilobyte of whole lines
+  const uint32_t ds_vo = (uint32_t)(hf * 512 + l32 * 16);
   const int64_t ds_h0 = ((int64_t)b * a.Hq + it_h) * a.ds_plane + ds_row(qstart >> 5, a.nk32, CAUSAL) + kb32;
   int64_t it_tile = ds_h0;
   auto ds_rs = __builtin_amdgcn_make_buffer_rsrc((void*)a.ds, (short)0, 0, 0x00020000);
@@ -425,7 +427,7 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
       if ((t & 1) == 0) sacc[PN] = mfma32(as_vec8<T>(xs[t % AHEAD]), kf[t >> 1], (t >> 1) == 0 ? f32x16{} : sacc[PN]);
       else pacc[PN] = mfma32(as_vec8<T>(xs[t % AHEAD]), vf[t >> 1], (t >> 1) == 0 ? nd_next : pacc[PN]);
       // dS of step j-1 out to its tile (non-temporal: read once, by the dQ kernel)
-      if (t < 2) __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, dspk[PN][t]), ds_rs, ds_vo + 32 * t, 0, 2);
+      if (t < 2) __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, dspk[PN][t]), ds_rs, ds_vo + 1024 * t, 0, 2);
       // stream 2: dV / dK of step j-1 (c, nb)
       {
         const int c = t / (2 * NB), nb = (t / 2) % NB;

@@ -122,10 +122,11 @@ struct BwdArgs {
   float qsign;
   int zero_scale;
   int mask_vec, score_vec;
-  // dS tiles of the deterministic path (written by the dK/dV kernel, read by
-  // the dQ kernel); null when dQ is recomputed instead.  Tile (b, h, s, kb)
-  // holds dS / scale of query rows 32 s.. and keys 32 kb.. as [key][32] 16-bit
-  // values, element offset ((b Hq + h) ds_plane + ds_row(s) + kb) * 1024.
+  // dS tiles (written by the dK/dV kernel, read by the dQ kernel); null when
+  // dQ is recomputed instead.  Tile (b, h, s, kb) holds dS / scale of query
+  // rows 32 s.. and keys 32 kb.. as 32 key rows of 32 16-bit values stored
+  // chunk-major (16-byte chunk c of key row k at byte c 512 + k 16), element
+  // offset of the tile ((b Hq + h) ds_plane + ds_row(s) + kb) * 1024.
   void* ds;
   int64_t ds_plane;     // tiles per (b, h)
   int nq32, nk32;       // 32-row / 32-key steps
