@@ -35,7 +35,9 @@
 // conflict-free.
 //
 // Softmax fast path: p = exp2(s c - m_run) with the running maximum m_run
-// left unchanged, and the row sum taken over the packed P with v_dot2.  Only
+// left unchanged, and the row sum taken over the fp32 p with plain adds
+// (v_dot2 would issue to the matrix pipe, where it waits behind the other
+// wave's MFMAs and delays them).  Only
 // when some p exceeds 2^8 (the lane's partial sum tells, conservatively) or
 // m_run is still -inf does the slow path compute the tile maximum, rescale
 // O and l, and redo P.  That is exact (O and l always share one reference)
@@ -79,22 +81,6 @@ __device__ __forceinline__ u32x2 pack4(float x0, float x1, float x2, float x3) {
   T4 v;
   v[0] = (T)x0; v[1] = (T)x1; v[2] = (T)x2; v[3] = (T)x3;
   return __builtin_bit_cast(u32x2, v);
-}
-
-// Sum of the 8 packed values of x (fp32 accumulate), one v_dot2 per pair.
-__device__ __forceinline__ float dot_ones(bf16x8 x, float acc) {
-  typedef __bf16 b2 __attribute__((ext_vector_type(2)));
-  const b2 one = {(__bf16)1.0f, (__bf16)1.0f};
-#pragma unroll
-  for (int j = 0; j < 4; ++j) acc = __builtin_amdgcn_fdot2_f32_bf16(b2{x[2 * j], x[2 * j + 1]}, one, acc, false);
-  return acc;
-}
-__device__ __forceinline__ float dot_ones(f16x8 x, float acc) {
-  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-  const h2 one = {(_Float16)1.0f, (_Float16)1.0f};
-#pragma unroll
-  for (int j = 0; j < 4; ++j) acc = __builtin_amdgcn_fdot2(h2{x[2 * j], x[2 * j + 1]}, one, acc, false);
-  return acc;
 }
 
 // Hides x's value from the optimiser (keeps an address in one register).
@@ -375,7 +361,7 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
 #pragma unroll
       for (int t = 0; t < 8; ++t) x[t] = exp2_fast(fmaf(sacc[kb][8 * c + t], c2, mneg));
       pk[kk] = pack8<T>(x[0], x[1], x[2], x[3], x[4], x[5], x[6], x[7]);
-      lsum = dot_ones(pk[kk], lsum);
+      lsum += ((x[0] + x[1]) + (x[2] + x[3])) + ((x[4] + x[5]) + (x[6] + x[7]));
     }
     return lsum;
   };
