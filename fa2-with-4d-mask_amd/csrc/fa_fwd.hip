@@ -216,13 +216,42 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
     return __builtin_amdgcn_make_buffer_rsrc((void*)tb, (short)0, (int)nrec, 0x00020000);
   };
   u32x4 stg[NSTG];   // K slots, then V slots, of the next batch
-  // Batch of pair p: K(p+2) -> K buffer (p+2)%3, V(p+1) -> V buffer (p+1)%3.
-  auto load_batch = [&](int p) __attribute__((always_inline)) {
-    const auto rk = rsrc_of(kp, a.kst, p + 2), rv = rsrc_of(vp, a.vst, p + 1);
+  // Without a mask, list position = key tile, and the batch descriptors come
+  // from running tile pointers and three record counts (full tile, the last
+  // partial tile, none) instead of a 64-bit multiply per tile: the loads are
+  // issued in the softmax phase, whose instruction issue bounds the step.
+  const int nt_full = min(nt, Tk / BN);   // tiles [0, nt_full) are whole
+  auto nrec_of = [&](int64_t st) __attribute__((always_inline)) -> uint32_t {
+    return (uint32_t)min((int64_t)(BN - 1) * st * 2 + ROWB, (int64_t)0xfffffff0);
+  };
+  const uint32_t nrec_k = nrec_of(a.kst), nrec_v = nrec_of(a.vst);
+  const uint32_t tail_k = (uint32_t)((int64_t)(Tk - nt_full * BN - 1) * a.kst * 2 + ROWB);
+  const uint32_t tail_v = (uint32_t)((int64_t)(Tk - nt_full * BN - 1) * a.vst * 2 + ROWB);
+  const T* kb_run = kp + (int64_t)2 * BN * a.kst;   // K(p+2) of the batch loaded next
+  const T* vb_run = vp + (int64_t)BN * a.vst;       // V(p+1)
+  auto rsrc_run = [&](const T* tb, uint32_t full, uint32_t tail, int t) __attribute__((always_inline)) {
+    const uint32_t nrec = t < nt_full ? full : (t < nt ? tail : 0u);
+    return __builtin_amdgcn_make_buffer_rsrc((void*)tb, (short)0, (int)nrec, 0x00020000);
+  };
+  // Descriptors of the batch of pair p: K(p+2) -> K buffer (p+2)%3, V(p+1) ->
+  // V buffer (p+1)%3.  Called once per pair, in pair order, outside the
+  // per-group branches (the running pointers stay in scalar registers).
+  struct Rs2 { __amdgpu_buffer_rsrc_t k, v; };
+  auto batch_rsrc = [&](int p) __attribute__((always_inline)) -> Rs2 {
+    if constexpr (MASK) {
+      return Rs2{rsrc_of(kp, a.kst, p + 2), rsrc_of(vp, a.vst, p + 1)};
+    } else {
+      const Rs2 r{rsrc_run(kb_run, nrec_k, tail_k, p + 2), rsrc_run(vb_run, nrec_v, tail_v, p + 1)};
+      kb_run += (int64_t)BN * a.kst;
+      vb_run += (int64_t)BN * a.vst;
+      return r;
+    }
+  };
+  auto load_batch = [&](const Rs2& r) __attribute__((always_inline)) {
 #pragma unroll
     for (int u = 0; u < IPW; ++u) {
-      stg[u] = __builtin_amdgcn_raw_buffer_load_b128(rk, goff_k[u], 0, 0);
-      stg[IPW + u] = __builtin_amdgcn_raw_buffer_load_b128(rv, goff_v[u], 0, 0);
+      stg[u] = __builtin_amdgcn_raw_buffer_load_b128(r.k, goff_k[u], 0, 0);
+      stg[IPW + u] = __builtin_amdgcn_raw_buffer_load_b128(r.v, goff_v[u], 0, 0);
     }
   };
   auto store_batch = [&](int kbuf, int vbuf) __attribute__((always_inline)) {
@@ -435,7 +464,7 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
   put_tile(true, 0, 0);
   put_tile(true, 1, 1);
   put_tile(false, 0, 0);
-  load_batch(0);
+  load_batch(batch_rsrc(0));
   lds_barrier();
 
   // ---- main loop over phase pairs p = 0 .. nt ------------------------------------
@@ -447,9 +476,10 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
   // barriers that follow make the tiles visible before pair p+2 reads them.
   auto pair = [&](auto KBc, int p) __attribute__((always_inline)) {
     constexpr int KB = decltype(KBc)::value;
+    const Rs2 rs = batch_rsrc(p + 1);
     auto stage = [&]() __attribute__((always_inline)) {
       store_batch((KB + 2) % kNBuf, (KB + 1) % kNBuf);
-      load_batch(p + 1);
+      load_batch(rs);
     };
     if (grp == 0) {
       if (p <= nt_w) m_step(KBc, p);
