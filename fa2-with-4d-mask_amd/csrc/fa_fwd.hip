@@ -19,8 +19,8 @@
 //   M(p): S(p) = K(p) Q^T and O += V(p-1)^T P(p-1)      (MFMA phase)
 //   V(p): softmax of S(p) -> P(p)                        (VALU phase)
 // Waves w and w+4 share a SIMD, so while one issues MFMAs the other issues
-// VALU work; a workgroup barrier separates the phases.  The MFMA wave runs at
-// a raised issue priority so that the softmax wave fills the gaps.
+// VALU work; a workgroup barrier ends each pair of phases.  The MFMA wave runs
+// at a raised issue priority so that the softmax wave fills the gaps.
 //
 // K/V staging: three LDS buffers each for K and V.  In its softmax phase each
 // wave writes its share of the tiles loaded one phase pair earlier (16 bytes
@@ -474,6 +474,9 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
   // (K(p+2), V(p+1), loaded during pair p-1) and loads its share of batch
   // p+1.  The buffers written are free (last read in pair p-1), and the
   // barriers that follow make the tiles visible before pair p+2 reads them.
+  // One barrier per pair is all the buffers need; the two phases of a pair
+  // are not separated by one (the waves of a SIMD settle into the
+  // alternation by themselves, and a phase that ends early does not wait).
   auto pair = [&](auto KBc, int p) __attribute__((always_inline)) {
     constexpr int KB = decltype(KBc)::value;
     const Rs2 rs = batch_rsrc(p + 1);
@@ -487,7 +490,6 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
       if (p >= 1 && p - 1 < nt_w) v_step(p - 1, stage);
       else stage();
     }
-    lds_barrier();
     if (grp == 0) {
       if (p < nt_w) v_step(p, stage);
       else stage();
