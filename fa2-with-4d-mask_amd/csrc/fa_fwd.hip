@@ -22,7 +22,7 @@
 // VALU work; a workgroup barrier ends each pair of phases.  The MFMA wave runs
 // at a raised issue priority so that the softmax wave fills the gaps.
 //
-// K/V staging: three LDS buffers each for K and V.  In its softmax phase each
+// K/V staging: three or four LDS buffers each for K and V.  In its softmax phase each
 // wave writes its share of the tiles loaded one phase pair earlier (16 bytes
 // per lane per chunk, held in registers meanwhile) and loads its share of the
 // next ones, with buffer loads whose per-lane offsets are loop-invariant and
@@ -52,7 +52,6 @@ constexpr int kWaves = 8;               // two groups of four
 constexpr int kBM = kWaves * 32;        // query rows per workgroup
 constexpr int kBN = 64;                 // keys per tile
 constexpr int kThreads = kWaves * 64;
-constexpr int kNBuf = 3;                // LDS buffers per tile kind
 constexpr float kFastSumMax = 256.0f;   // lane partial sum bound of the fast path
 
 template <int N> struct IC { static constexpr int value = N; };
@@ -118,13 +117,17 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
   constexpr int IPW = NI / kWaves;      // ... staged by each wave
   constexpr int RPI = 1024 / ROWB;      // tile rows per slot
   constexpr int NSTG = 2 * IPW;         // staging registers (x 16 bytes) per lane: K + V
-  constexpr int KOFF = 0, VOFF = kNBuf * TILEB;
+  // LDS buffers per tile kind: with four, a workgroup barrier every second
+  // phase pair suffices; causal workgroups (short, ragged key ranges) run
+  // faster with three and a barrier every pair.
+  constexpr int NBUF = CAUSAL ? 3 : 4;
+  constexpr int KOFF = 0, VOFF = NBUF * TILEB;
   static_assert(NI % kWaves == 0 && IPW >= 1, "staging split");
-  static_assert(kNBuf * TILEB <= 65536, "buffer + row offsets fit the 16-bit DS immediate");
+  static_assert(NBUF * TILEB <= 65536, "buffer + row offsets fit the 16-bit DS immediate");
   constexpr int OS = D + 8;             // epilogue O staging stride (elements)
-  static_assert(kWaves * 32 * OS * 2 <= 2 * kNBuf * TILEB, "O staging fits in the K/V buffers");
+  static_assert(kWaves * 32 * OS * 2 <= 2 * NBUF * TILEB, "O staging fits in the K/V buffers");
   static_assert(BM == kFwdRows && BN == kFwdKeys, "prepared-mask lists are built for this tile shape");
-  __shared__ __attribute__((aligned(1024))) char smem[2 * kNBuf * TILEB];
+  __shared__ __attribute__((aligned(1024))) char smem[2 * NBUF * TILEB];
 
   // ---- which (batch, head, query tile) -------------------------------------
   // Logical order (b, kv-head, [query tile descending, head in group]); with
@@ -317,7 +320,7 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
   auto m_step = [&](auto KBc, int p) __attribute__((always_inline)) {
     constexpr int KB = decltype(KBc)::value;
     constexpr uint32_t kb_lds = KB * TILEB;                      // K(p), relative to K buffer 0
-    constexpr uint32_t vb_lds = ((KB + 2) % kNBuf) * TILEB;      // V(p-1), relative to V buffer 0
+    constexpr uint32_t vb_lds = ((KB + NBUF - 1) % NBUF) * TILEB;  // V(p-1), relative to V buffer 0
     if constexpr (MASK || SCORE) {
       if (p < nt_w) {
         int t = p;
@@ -453,10 +456,10 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
     l_run += lsum;
   };
 
-  // ---- prologue: zero V buffer 2 (read as V(-1) with P = 0), K(0), K(1), V(0)
-  // to LDS, batch 0 (K(2), V(1)) into the staging registers.
+  // ---- prologue: zero the last V buffer (read as V(-1) with P = 0), K(0),
+  // K(1), V(0) to LDS, batch 0 (K(2), V(1)) into the staging registers.
   {
-    char* z = smem + VOFF + 2 * TILEB;
+    char* z = smem + VOFF + (NBUF - 1) * TILEB;
 #pragma unroll
     for (int u = 0; u < TILEB / (kThreads * 16); ++u) lds_write16(z + (tid + u * kThreads) * 16, u32x4{0, 0, 0, 0});
   }
@@ -472,16 +475,19 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
   //         phase 2p+1 group 0: V(p)   group 1: M(p)
   // In its softmax phase of pair p each wave stores its share of batch p
   // (K(p+2), V(p+1), loaded during pair p-1) and loads its share of batch
-  // p+1.  The buffers written are free (last read in pair p-1), and the
-  // barriers that follow make the tiles visible before pair p+2 reads them.
-  // One barrier per pair is all the buffers need; the two phases of a pair
-  // are not separated by one (the waves of a SIMD settle into the
-  // alternation by themselves, and a phase that ends early does not wait).
+  // p+1 (pair p writes K buffer (p+2)%NBUF and V buffer (p+1)%NBUF).  With
+  // three buffers those were last read in pair p-1 and a barrier ends every
+  // pair; with four they were last read in pair p-2 and a barrier ends every
+  // odd pair.  Either way a barrier lies between each write and the first
+  // read, in pair p+2.  The two phases of a pair are not separated by a
+  // barrier (the waves of a SIMD settle into the alternation by themselves,
+  // and a phase that ends early does not wait).
   auto pair = [&](auto KBc, int p) __attribute__((always_inline)) {
-    constexpr int KB = decltype(KBc)::value;
+    constexpr int KB = decltype(KBc)::value;   // p % NBUF
+    constexpr bool BAR = NBUF == 3 || (KB & 1) != 0;
     const Rs2 rs = batch_rsrc(p + 1);
     auto stage = [&]() __attribute__((always_inline)) {
-      store_batch((KB + 2) % kNBuf, (KB + 1) % kNBuf);
+      store_batch((KB + 2) % NBUF, (KB + 1) % NBUF);
       load_batch(rs);
     };
     if (grp == 0) {
@@ -496,15 +502,20 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
     } else {
       if (p <= nt_w) m_step(KBc, p);
     }
-    lds_barrier();
+    if constexpr (BAR) lds_barrier();
   };
-  for (int p = 0; p <= nt; p += 3) {
+  for (int p = 0; p <= nt; p += NBUF) {
     pair(IC<0>{}, p);
     if (p + 1 > nt) break;
     pair(IC<1>{}, p + 1);
     if (p + 2 > nt) break;
     pair(IC<2>{}, p + 2);
+    if constexpr (NBUF == 4) {
+      if (p + 3 > nt) break;
+      pair(IC<3>{}, p + 3);
+    }
   }
+  if constexpr (NBUF == 4) lds_barrier();   // all waves are done with the K/V buffers
 
   // ---- epilogue: O = acc / l (NaN for a row with no kept key), LSE ----------------
   const float l_tot = half_sum(l_run);
