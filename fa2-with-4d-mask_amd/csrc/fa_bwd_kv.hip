@@ -183,6 +183,16 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
   const T* d_head = (const T*)a.dout + b * a.dsb + (int64_t)ld_h * a.dsh;
   const float* l_head = a.lse + ((int64_t)b * a.Hq + ld_h) * Tq;
   const float* e_head = a.delta + ((int64_t)b * a.Hq + ld_h) * Tq;
+  // Without a mask the descriptors change only at a head switch (the rows
+  // advance through the scalar offsets), so they are kept across steps and
+  // rebuilt there, with no records once the heads are exhausted (padding
+  // steps): the loads cost no scalar work per step.
+  auto rs_of = [&](const void* base, uint32_t rec, bool lv) __attribute__((always_inline)) {
+    return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, lv ? (int)rec : 0, 0x00020000);
+  };
+  const bool live0 = n > 0;
+  auto rq_c = rs_of(q_head, q_rec, live0), rd_c = rs_of(d_head, d_rec, live0);
+  auto rl_c = rs_of(l_head, (uint32_t)Tq * 4, live0), re_c = rs_of(e_head, (uint32_t)Tq * 4, live0);
   auto load_next = [&](auto Sc) __attribute__((always_inline)) {
     constexpr int S = decltype(Sc)::value;
     const bool live = ld_it < n;
@@ -198,16 +208,16 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
       l_head = a.lse + ((int64_t)b * a.Hq + ld_h) * Tq;
       e_head = a.delta + ((int64_t)b * a.Hq + ld_h) * Tq;
     }
-    const auto rq = __builtin_amdgcn_make_buffer_rsrc((void*)q_head, (short)0, live ? (int)q_rec : 0, 0x00020000);
-    const auto rd = __builtin_amdgcn_make_buffer_rsrc((void*)d_head, (short)0, live ? (int)d_rec : 0, 0x00020000);
+    const auto rq = MASK ? rs_of(q_head, q_rec, live) : rq_c;
+    const auto rd = MASK ? rs_of(d_head, d_rec, live) : rd_c;
 #pragma unroll
     for (int u = 0; u < UQ; ++u) {
       stq[S][u] = __builtin_amdgcn_raw_buffer_load_b128(rq, gq[u], so_q, 0);
       std_[S][u] = __builtin_amdgcn_raw_buffer_load_b128(rd, gd[u], so_d, 0);
     }
     if (wv == 0) {  // lanes 0-31: LSE rows, 32-63: Delta rows
-      const auto rl = __builtin_amdgcn_make_buffer_rsrc((void*)l_head, (short)0, live ? Tq * 4 : 0, 0x00020000);
-      const auto re = __builtin_amdgcn_make_buffer_rsrc((void*)e_head, (short)0, live ? Tq * 4 : 0, 0x00020000);
+      const auto rl = MASK ? rs_of(l_head, (uint32_t)Tq * 4, live) : rl_c;
+      const auto re = MASK ? rs_of(e_head, (uint32_t)Tq * 4, live) : re_c;
       stl[S] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rl, (uint32_t)l32 * 4, so_l, 0));
       std_l[S] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(re, (uint32_t)l32 * 4, so_l, 0));
     }
@@ -234,6 +244,11 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
       d_head += a.dsh;
       l_head += Tq;
       e_head += Tq;
+      const bool lv = ld_h < h_end;
+      rq_c = rs_of(q_head, q_rec, lv);
+      rd_c = rs_of(d_head, d_rec, lv);
+      rl_c = rs_of(l_head, (uint32_t)Tq * 4, lv);
+      re_c = rs_of(e_head, (uint32_t)Tq * 4, lv);
     }
   };
   auto store_tile = [&](int buf, auto Sc) __attribute__((always_inline)) {
@@ -289,14 +304,15 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
   // packed values of rows 16 c + 4 hf + {0..3, 8..11}.  Stores of step j-1
   // are issued in iteration j; a descriptor with no records drops them
   // (padding steps, tiles above the causal diagonal, keys past Tk, no dS).
-  // it_tile: tile of (it_h, step it_qs / 32) and this wave's keys.
+  // it_ptr: tile of (it_h, step it_qs / 32) and this wave's keys (a running
+  // pointer: no 64-bit multiply per step).
   const int kb32 = __builtin_amdgcn_readfirstlane(kw0) >> 5;
   const bool ds_on = a.ds != nullptr && kb32 < a.nk32;
   // tile bytes are chunk-major (chunk c of key row k at c 512 + k 16): store t
   // writes chunks 2 t + hf, i.e. one contiguous kilobyte of whole lines
   const uint32_t ds_vo = (uint32_t)(hf * 512 + l32 * 16);
   const int64_t ds_h0 = ((int64_t)b * a.Hq + it_h) * a.ds_plane + ds_row(qstart >> 5, a.nk32, CAUSAL) + kb32;
-  int64_t it_tile = ds_h0;
+  const uint16_t* it_ptr = (const uint16_t*)a.ds + ds_h0 * 1024;
   auto ds_rs = __builtin_amdgcn_make_buffer_rsrc((void*)a.ds, (short)0, 0, 0x00020000);
   // descriptor of step j's tile, then advance (it_h, it_qs, it_tile) to step j+1
   auto next_step = [&](int j) __attribute__((always_inline)) {
@@ -320,14 +336,13 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
       return;
     }
     const bool ok = ds_on && j < n && (!CAUSAL || kb32 <= s);
-    ds_rs = __builtin_amdgcn_make_buffer_rsrc((void*)((uint16_t*)a.ds + it_tile * 1024), (short)0, ok ? 2048 : 0,
-                                              0x00020000);
+    ds_rs = __builtin_amdgcn_make_buffer_rsrc((void*)it_ptr, (short)0, ok ? 2048 : 0, 0x00020000);
     it_qs += kStep;
-    it_tile += CAUSAL ? min(s + 1, a.nk32) : a.nk32;
+    it_ptr += (int64_t)(CAUSAL ? min(s + 1, a.nk32) : a.nk32) * 1024;
     if (it_qs >= Tq) {
       ++it_h;
       it_qs = qstart;
-      it_tile = ds_h0 + (int64_t)(it_h - (kvh * a.G + g0)) * a.ds_plane;
+      it_ptr = (const uint16_t*)a.ds + (ds_h0 + (int64_t)(it_h - (kvh * a.G + g0)) * a.ds_plane) * 1024;
     }
   };
 
