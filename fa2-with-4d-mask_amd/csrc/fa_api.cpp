@@ -5,6 +5,7 @@
 // validation paths run (and are tested) on machines without a GPU.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -91,15 +92,31 @@ int launch_status(hipError_t e, const char* what) {
 }
 
 // dS tiles (16-bit, every stored 32x32 block; causal: blocks on or below the
-// diagonal) handed from the dK/dV kernel to the dQ kernel, when they fit the
-// caller's limit.
-int64_t ds_elems(const FaBwdParams* p) {
-  const int64_t limit = p->ds_limit_bytes == 0 ? (int64_t)8 << 30 : p->ds_limit_bytes;
-  if (limit < 0) return 0;
+// diagonal) handed from the dK/dV kernel to the dQ kernel.  The workspace
+// holds the planes of a slice of (batch, kv-head) units, as many as fit the
+// caller's limit (all of them when they fit), in as few slices of nearly
+// equal size as that allows: the backward then runs the two kernels once per
+// slice.  0 units: not even one unit fits.
+int64_t ds_unit_elems(const FaBwdParams* p) {
   const int64_t nq32 = (p->seqlen_q + 31) / 32, nk32 = (p->seqlen_k + 31) / 32;
   const int64_t plane = fa::ds_row(nq32, nk32, p->is_causal != 0);
-  const int64_t elems = (int64_t)p->batch * p->heads_q * plane * 1024;
-  return 2 * elems <= limit ? elems : 0;
+  return (int64_t)(p->heads_q / p->heads_k) * plane * 1024;   // one unit: the group's planes
+}
+int64_t ds_slice_units(const FaBwdParams* p) {
+  const int64_t limit = p->ds_limit_bytes == 0 ? (int64_t)8 << 30 : p->ds_limit_bytes;
+  if (limit < 0) return 0;
+  const int64_t units = (int64_t)p->batch * p->heads_k, unit = ds_unit_elems(p);
+  if (unit <= 0) return units;
+  const int64_t most = std::min(units, limit / (2 * unit));
+  if (most <= 0) return 0;
+  // as few slices as the limit allows, of (nearly) equal size
+  const int64_t slices = (units + most - 1) / most;
+  return (units + slices - 1) / slices;
+}
+int64_t ds_elems(const FaBwdParams* p) { return ds_slice_units(p) * ds_unit_elems(p); }
+int ds_slices(const FaBwdParams* p) {
+  const int64_t per = ds_slice_units(p);
+  return per > 0 ? (int)(((int64_t)p->batch * p->heads_k + per - 1) / per) : 0;
 }
 
 // How the backward runs.  With the dS tiles: the pipelined dK/dV kernel
@@ -118,7 +135,9 @@ Route route_of(const FaBwdParams* p) {
 // is below ~1024 workgroups and each range keeps >= 4 key steps.
 int dq_split_of(const FaBwdParams* p) {
   if (route_of(p) != kDsAtomic) return 1;
-  const int64_t nblk = (int64_t)p->batch * p->heads_q * ((p->seqlen_q + fa::dq_ds_block_rows() - 1) / fa::dq_ds_block_rows());
+  // workgroups of one launch (one slice of units)
+  const int64_t nblk = ds_slice_units(p) * (p->heads_q / p->heads_k) *
+                       ((p->seqlen_q + fa::dq_ds_block_rows() - 1) / fa::dq_ds_block_rows());
   const int nks = (p->seqlen_k + 31) / 32;
   if (nks < 2) return 1;
   int split = 2;
@@ -131,8 +150,16 @@ int choose_split(const FaBwdParams* p) {
   const int G = p->heads_q / p->heads_k;
   const int kb = route_of(p) == kFusedAtomic ? fa::dkdv_block_keys() : fa::dkdv2_block_keys();
   const int nkt = (p->seqlen_k + kb - 1) / kb;
-  const int64_t base = (int64_t)p->batch * p->heads_k * nkt;
-  const int64_t target = 512;  // two workgroups per CU on a 256-CU part
+  const Route r = route_of(p);
+  const int64_t units = r == kDsAtomic || r == kDsDet ? ds_slice_units(p) : (int64_t)p->batch * p->heads_k;
+  const int64_t base = units * nkt;   // workgroups of one launch without a split
+  // two workgroups per CU on a 256-CU part.  Causal workgroups differ in work
+  // (key block kt walks the rows from kt on); when the backward runs in slices
+  // (long sequences) twice as many keep each slice's tail short (measured:
+  // T 16384 causal 10.1 -> 8.9 ms), while a single launch at the headline
+  // size is faster without the split's fp32 slabs.
+  const bool sliced = units < (int64_t)p->batch * p->heads_k;
+  const int64_t target = p->is_causal && sliced ? 1024 : 512;
   int split = 1;
   while (split * 2 <= G && G % (split * 2) == 0 && base * split < target) split *= 2;
   return split;
@@ -332,6 +359,8 @@ static fa::BwdArgs bwd_args(const FaBwdParams* p, int split) {
   const int kb = p->atomic_dq ? fa::dkdv_block_keys() : fa::dkdv2_block_keys();
   a.nkt = (p->seqlen_k + kb - 1) / kb;
   a.nqt = (p->seqlen_q + fa::dq_block_rows() - 1) / fa::dq_block_rows();
+  a.bk0 = 0;
+  a.nbk = p->batch * p->heads_k;
   a.split = split;
   a.do_dq = p->atomic_dq ? 1 : 0;
   a.dq_split = dq_split_of(p);
@@ -363,9 +392,23 @@ int fa_bwd(const FaBwdParams* p) {
 
   if (route_of(p) == kFusedAtomic) {
     if ((st = launch_status(fa::launch_bwd_dkdv(a, p->head_dim, p->dtype, causal, s), "dkdv"))) return st;
-  } else {
+  } else if (!a.ds || ds_slices(p) == 1) {
     // pipelined dK/dV (+ dS tiles when the plan has them) here, dQ in fa_bwd_finalize
     if ((st = launch_status(fa::launch_bwd_dkdv2(a, p->head_dim, p->dtype, causal, s), "dkdv"))) return st;
+  } else {
+    // the workspace holds a slice of (batch, kv-head) units: dK/dV and then
+    // dQ of each slice (same stream, so a slice's tiles are consumed before
+    // the next slice overwrites them)
+    const int per = (int)ds_slice_units(p), units = p->batch * p->heads_k;
+    fa::BwdArgs q = a;
+    q.nqt = (p->seqlen_q + fa::dq_ds_block_rows() - 1) / fa::dq_ds_block_rows();
+    for (int u0 = 0; u0 < units; u0 += per) {
+      fa::BwdArgs k = a;
+      k.bk0 = q.bk0 = u0;
+      k.nbk = q.nbk = std::min(per, units - u0);
+      if ((st = launch_status(fa::launch_bwd_dkdv2(k, p->head_dim, p->dtype, causal, s), "dkdv"))) return st;
+      if ((st = launch_status(fa::launch_bwd_dq_ds(q, p->head_dim, p->dtype, causal, s), "dq"))) return st;
+    }
   }
   return FA_OK;
 }
@@ -383,8 +426,10 @@ int fa_bwd_finalize(const FaBwdParams* p) {
     fa::BwdArgs a = bwd_args(p, split);
     const bool causal = p->is_causal != 0;
     if (a.ds) {
+      // sliced: fa_bwd already ran the dQ kernel per slice
       a.nqt = (p->seqlen_q + fa::dq_ds_block_rows() - 1) / fa::dq_ds_block_rows();
-      if ((st = launch_status(fa::launch_bwd_dq_ds(a, p->head_dim, p->dtype, causal, s), "dq"))) return st;
+      if (ds_slices(p) == 1 && (st = launch_status(fa::launch_bwd_dq_ds(a, p->head_dim, p->dtype, causal, s), "dq")))
+        return st;
     } else {
       if ((st = launch_status(fa::launch_bwd_dq(a, p->head_dim, p->dtype, causal, s), "dq"))) return st;
     }

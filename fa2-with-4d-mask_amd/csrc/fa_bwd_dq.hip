@@ -66,13 +66,14 @@ __global__ __launch_bounds__(kDqWaves * 64, 2) void dq_ds_kernel(const BwdArgs a
   // causal blocks first.
   const int nqb = a.nqt;
   const int nsp = ATOMIC ? a.dq_split : 1;
-  const int nblk = a.B * a.Hq * nqb * nsp;
+  const int nblk = a.nbk * a.G * nqb * nsp;
   const int W0 = xcd_remap(blockIdx.x, nblk);
   const int W = ATOMIC ? W0 / nsp : W0;
   const int ksp = ATOMIC ? W0 - W * nsp : 0;        // key split of this workgroup
   const int per_kv = a.G * nqb;
-  const int bk = W / per_kv;
-  const int rem = W - bk * per_kv;
+  const int bkl = W / per_kv;             // unit within this launch's slice
+  const int bk = a.bk0 + bkl;
+  const int rem = W - bkl * per_kv;
   const int qb_rev = rem / a.G;
   const int g = rem - qb_rev * a.G;
   const int qb = nqb - 1 - qb_rev;
@@ -137,7 +138,7 @@ __global__ __launch_bounds__(kDqWaves * 64, 2) void dq_ds_kernel(const BwdArgs a
   for (int u = 0; u < 2; ++u)
     sd[u] = opaque(lds0 + KTILE + wv * DSW + skey * 64 + ((((lane >> 5) + 2 * u) ^ ((skey >> 2) & 3)) * 16));
   const uint16_t* __restrict__ dsp = (const uint16_t*)a.ds;
-  const int64_t plane = ((int64_t)b * a.Hq + h) * a.ds_plane;
+  const int64_t plane = ((int64_t)b * a.Hq + h - (int64_t)a.bk0 * a.G) * a.ds_plane;
   int64_t row0[kDqSteps];
 #pragma unroll
   for (int i = 0; i < kDqSteps; ++i) row0[i] = plane + ds_row(s0 + i, nk32, CAUSAL);
@@ -279,7 +280,7 @@ __global__ __launch_bounds__(kDqWaves * 64, 2) void dq_ds_kernel(const BwdArgs a
 
 template <typename T, int D, bool CAUSAL, bool ATOMIC>
 hipError_t launch_a(const BwdArgs& a, hipStream_t s) {
-  const dim3 grid((unsigned)(a.B * a.Hq * a.nqt * (ATOMIC ? a.dq_split : 1))), block(kDqWaves * 64);
+  const dim3 grid((unsigned)(a.nbk * a.G * a.nqt * (ATOMIC ? a.dq_split : 1))), block(kDqWaves * 64);
   if (a.mask) hipLaunchKernelGGL((dq_ds_kernel<T, D, CAUSAL, true, ATOMIC>), grid, block, 0, s, a);
   else hipLaunchKernelGGL((dq_ds_kernel<T, D, CAUSAL, false, ATOMIC>), grid, block, 0, s, a);
   return hipGetLastError();

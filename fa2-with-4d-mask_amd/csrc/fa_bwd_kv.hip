@@ -60,11 +60,12 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
   __shared__ __attribute__((aligned(1024))) char smem[LOFF + kNBuf * LBUF];
 
   // ---- which (batch, kv-head, split, key block) ------------------------------
-  const int nblk = a.B * a.Hk * a.nkt * a.split;
+  const int nblk = a.nbk * a.nkt * a.split;
   const int W = xcd_remap(blockIdx.x, nblk);
   const int per_bk = a.split * a.nkt;
-  const int bk = W / per_bk;
-  const int rem = W - bk * per_bk;
+  const int bkl = W / per_bk;             // unit within this launch's slice
+  const int bk = a.bk0 + bkl;
+  const int rem = W - bkl * per_bk;
   const int sp = rem / a.nkt;
   const int kt = rem - sp * a.nkt;        // ascending = most causal work first
   const int b = bk / a.Hk, kvh = bk - b * a.Hk;
@@ -307,11 +308,12 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
   // it_ptr: tile of (it_h, step it_qs / 32) and this wave's keys (a running
   // pointer: no 64-bit multiply per step).
   const int kb32 = __builtin_amdgcn_readfirstlane(kw0) >> 5;
+  const int64_t ds_u0 = (int64_t)a.bk0 * a.G;   // first dS plane (b Hq + h) of the workspace
   const bool ds_on = a.ds != nullptr && kb32 < a.nk32;
   // tile bytes are chunk-major (chunk c of key row k at c 512 + k 16): store t
   // writes chunks 2 t + hf, i.e. one contiguous kilobyte of whole lines
   const uint32_t ds_vo = (uint32_t)(hf * 512 + l32 * 16);
-  const int64_t ds_h0 = ((int64_t)b * a.Hq + it_h) * a.ds_plane + ds_row(qstart >> 5, a.nk32, CAUSAL) + kb32;
+  const int64_t ds_h0 = ((int64_t)b * a.Hq + it_h - ds_u0) * a.ds_plane + ds_row(qstart >> 5, a.nk32, CAUSAL) + kb32;
   const uint16_t* it_ptr = (const uint16_t*)a.ds + ds_h0 * 1024;
   auto ds_rs = __builtin_amdgcn_make_buffer_rsrc((void*)a.ds, (short)0, 0, 0x00020000);
   // descriptor of step j's tile, then advance (it_h, it_qs, it_tile) to step j+1
@@ -324,7 +326,7 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
         const uint8_t* bl = (const uint8_t*)(a.mws + a.ml.blk + mask_plane(a.ml, b, it_h) * a.ml.pblk);
         ok = bl[(int64_t)s * a.ml.nk32 + kb32] != 0;
       }
-      const int64_t tile = ((int64_t)b * a.Hq + it_h) * a.ds_plane + ds_row(s, a.nk32, CAUSAL) + kb32;
+      const int64_t tile = ((int64_t)b * a.Hq + it_h - ds_u0) * a.ds_plane + ds_row(s, a.nk32, CAUSAL) + kb32;
       ds_rs = __builtin_amdgcn_make_buffer_rsrc((void*)((uint16_t*)a.ds + tile * 1024), (short)0, ok ? 2048 : 0,
                                                 0x00020000);
       if (j < n) {
@@ -576,7 +578,7 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
 
 template <typename T, int D, bool CAUSAL>
 hipError_t launch_t(const BwdArgs& a, hipStream_t s) {
-  const dim3 grid((unsigned)(a.B * a.Hk * a.nkt * a.split)), block(kKvWaves * 64);
+  const dim3 grid((unsigned)(a.nbk * a.nkt * a.split)), block(kKvWaves * 64);
   const bool m = a.mask != nullptr, sc = a.score != nullptr;
   if (m && sc) hipLaunchKernelGGL((dkdv2_kernel<T, D, CAUSAL, true, true>), grid, block, 0, s, a);
   else if (m) hipLaunchKernelGGL((dkdv2_kernel<T, D, CAUSAL, true, false>), grid, block, 0, s, a);

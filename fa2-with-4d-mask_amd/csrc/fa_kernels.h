@@ -112,6 +112,11 @@ struct BwdArgs {
   int64_t msb, msh, msq, ssb, ssh, ssq;
   int B, Tq, Tk, Hq, Hk, G;
   int nkt;              // key tiles per (b, kv-head)
+  // (batch, kv-head) units bk = b Hk + kv-head of this launch: bk0 ..
+  // bk0 + nbk - 1 of the B Hk.  The dS-tile kernels run in slices of units
+  // when the tiles of all units exceed the workspace; the workspace then
+  // holds the planes of the slice, from unit bk0 on.  Others: 0, B Hk.
+  int bk0, nbk;
   int nqt;              // query tiles per (b, h) (dQ kernel)
   int split;            // query-head-group split of the dK/dV kernel
   int do_dq;            // dQ accumulated with fp32 atomics into dq_accum (fused in the dK/dV

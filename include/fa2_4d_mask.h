@@ -106,7 +106,8 @@ typedef struct FaBwdParams {
   int32_t dtype;
   void* stream;
   void* ds_tiles;                /* workspace of plan.ds_elems 16-bit values (deterministic path), else unused */
-  int64_t ds_limit_bytes;        /* largest dS workspace the caller accepts; 0 = 8 GiB, < 0 = none */
+  int64_t ds_limit_bytes;        /* largest dS workspace the caller accepts; 0 = 8 GiB, < 0 = none
+                                    (below the whole need: the backward runs in slices of units) */
   const void* mask_ws;           /* prepared mask, as for fa_fwd; required with a mask */
 } FaBwdParams;
 
@@ -131,9 +132,12 @@ typedef struct FaBwdPlan {
   int32_t needs_dq_accum;        /* 1 if dq_accum is used */
   int64_t dq_accum_elems;        /* B*Tq*Hq*D when used, else 0 */
   int64_t dkv_accum_elems;       /* B*Tk*Hk*D when kv_split > 1, else 0 */
-  int64_t ds_elems;              /* size of ds_tiles (dS of every stored 32x32 block, 16-bit), 0 when it
-                                    would exceed ds_limit_bytes: dQ is then recomputed (atomic_dq = 0) or
-                                    added per key block by the fused dK/dV kernel (atomic_dq = 1) */
+  int64_t ds_elems;              /* size of ds_tiles (16-bit dS of every stored 32x32 block of a slice of
+                                    (batch, kv-head) units: all units when they fit ds_limit_bytes, else
+                                    as many as fit, in nearly equal slices that fa_bwd runs one after the
+                                    other); 0 when not even one unit fits: dQ is then recomputed
+                                    (atomic_dq = 0) or added per key block by the fused dK/dV kernel
+                                    (atomic_dq = 1) */
   int32_t dkv_accum_zeroed;      /* 1: dk_accum/dv_accum must be zeroed by the caller (fused atomic kernel) */
   int32_t dq_split;              /* atomic_dq = 1 with dS tiles: key ranges whose dQ partials are added */
 } FaBwdPlan;
@@ -164,7 +168,9 @@ int fa_bwd_preprocess(const FaBwdParams* p);
  * `flash_attention_bwd_with_4d_mask_reduce` (python/fa2.py:305-426, launched at
  * :543-547) when atomic_dq = 0.  With plan.ds_elems > 0 (both modes): the dK/dV
  * kernel, writing dK/dV in dtype (kv_split = 1) or per-split fp32 slabs, and
- * storing dS into ds_tiles for fa_bwd_finalize.  With plan.ds_elems = 0 and
+ * storing dS into ds_tiles for fa_bwd_finalize (when ds_tiles holds a slice of the
+ * (batch, kv-head) units, fa_bwd runs the dK/dV and the dQ kernel per slice and
+ * fa_bwd_finalize only converts).  With plan.ds_elems = 0 and
  * atomic_dq = 1: one fused kernel that also adds dQ into dq_accum with fp32
  * atomics (dK/dV added into zeroed dk_accum/dv_accum when kv_split > 1); with
  * atomic_dq = 0: the dK/dV kernel only.  Must follow fa_bwd_preprocess on the

@@ -209,8 +209,17 @@ def test_plan_ds_tiles(lib):
     plan = _plan(lib, atomic_dq=0, is_causal=1, seqlen_q=333, seqlen_k=130, heads_q=4, heads_k=2)
     nq, nk = 11, 5
     assert plan.ds_elems == 4 * (nk * (nk + 1) // 2 + (nq - nk) * nk) * 1024
-    # caller limits: below the need, or none at all -> dQ recomputed
-    assert _plan(lib, atomic_dq=0, ds_limit_bytes=1 << 30).ds_elems == 0
+    # caller limits below the need: the workspace holds as many (batch,
+    # kv-head) units (the group's 4 planes, 512 MiB here) as fit, and the dS
+    # kernels run slice by slice; below one unit, or none at all -> dQ
+    # recomputed
+    unit = 4 * 256 * 256 * 1024
+    assert _plan(lib, atomic_dq=0, ds_limit_bytes=1 << 29).ds_elems == unit
+    assert _plan(lib, atomic_dq=0, ds_limit_bytes=1 << 30).ds_elems == 2 * unit
+    # 5 units would fit: 8 units run as 2 slices of 4 (balanced)
+    assert _plan(lib, atomic_dq=0, ds_limit_bytes=(3 << 30) - 1).ds_elems == 4 * unit
+    assert _plan(lib, ds_limit_bytes=1 << 29).ds_elems == unit   # atomic mode slices too
+    assert _plan(lib, atomic_dq=0, ds_limit_bytes=(1 << 29) - 2).ds_elems == 0
     assert _plan(lib, atomic_dq=0, is_causal=1, ds_limit_bytes=-1).ds_elems == 0
     assert _plan(lib, atomic_dq=0, is_causal=1, ds_limit_bytes=3 << 30).ds_elems > 0
 

@@ -36,13 +36,23 @@ def _api():
     return api
 
 
+def _one_unit_limit(cfg):
+    """dS workspace bytes of one (batch, kv-head) unit: the group's Hq/Hk planes
+    of 32x32 16-bit tiles (causal: tiles on or below the diagonal)."""
+    nq, nk = -(-cfg.Tq // 32), -(-cfg.Tk // 32)
+    plane = sum(min(s + 1, nk) for s in range(nq)) if cfg.is_causal else nq * nk
+    return 2 * (cfg.Hq // cfg.Hk) * plane * 1024
+
+
 def run_ours(case, cfg, *, atomic=True, scale=None, attention_mask=None, backward=True, ds_limit=0):
-    """ds_limit: dS workspace limit of the deterministic backward (0 = default,
-    dQ from the stored dS tiles; -1 = dQ recomputed from Q, K, V, dO)."""
+    """ds_limit: dS workspace limit of the backward (0 = default, dQ from the
+    stored dS tiles; -1 = no workspace: dQ recomputed (deterministic) or fused
+    fp32 atomics; "unit" = one (batch, kv-head) unit: the dS kernels run once
+    per unit)."""
     api = _api()
     import tilelang_fa2_4d_mask.fa2 as fa2mod
 
-    fa2mod.DS_LIMIT_BYTES = ds_limit
+    fa2mod.DS_LIMIT_BYTES = _one_unit_limit(cfg) if ds_limit == "unit" else ds_limit
     dev = torch.device("cuda:0")
     q = case["q"].to(dev).detach().requires_grad_(backward)
     k = case["k"].to(dev).detach().requires_grad_(backward)
@@ -133,9 +143,11 @@ SMALL = [
 
 # backward modes: fp32-atomic dQ over key ranges of the stored dS (default);
 # fp32-atomic dQ fused into the dK/dV kernel (no dS workspace); deterministic
-# with dQ from the stored dS
-# tiles; deterministic with dQ recomputed (no dS workspace allowed)
-MODES = {"atomic": (True, 0), "atomic_fused": (True, -1), "det_ds": (False, 0), "det_recompute": (False, -1)}
+# with dQ from the stored dS tiles; deterministic with dQ recomputed (no dS
+# workspace allowed); both dS modes with a workspace of one (batch, kv-head)
+# unit, so that the dS kernels run slice by slice
+MODES = {"atomic": (True, 0), "atomic_fused": (True, -1), "det_ds": (False, 0), "det_recompute": (False, -1),
+         "atomic_sliced": (True, "unit"), "det_sliced": (False, "unit")}
 
 
 @pytest.mark.parametrize("mode", list(MODES))
