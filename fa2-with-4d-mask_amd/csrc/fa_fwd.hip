@@ -184,9 +184,27 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
   // every instantiation gets the same control flow and register assignment);
   // with a mask every wave walks the whole list (causality is applied per key)
   const int nt_w = (int)opaque((uint32_t)(CAUSAL && !MASK ? min(nt, (min(Tk, q0w + 32) + BN - 1) / BN) : nt));
+  // List entries: without a score, positions 0..127 sit in two registers
+  // (lane i of ents[w] holds position 64 w + i) and are read with readlane,
+  // so that walking the list costs no scalar-memory waits in the pipeline;
+  // later positions (and the score kernels, which have no registers to
+  // spare) load them.
+  constexpr bool ENTV = MASK && !SCORE;
+  int32_t ents[ENTV ? 2 : 1] = {};
+  if constexpr (ENTV) {
+#pragma unroll
+    for (int w = 0; w < 2; ++w) ents[w] = 64 * w + lane < nt ? flist[1 + 64 * w + lane] : 0;
+  }
+  auto ent_at = [&](int p) __attribute__((always_inline)) -> int32_t {
+    if constexpr (ENTV) {
+      if (p < 64) return __builtin_amdgcn_readlane(ents[0], p);
+      if (p < 128) return __builtin_amdgcn_readlane(ents[1], p - 64);
+    }
+    return flist[1 + p];
+  };
   // key tile at list position p < nt
   auto tile_at = [&](int p) __attribute__((always_inline)) -> int {
-    if constexpr (MASK) return flist[1 + p] & 0x7fffffff;
+    if constexpr (MASK) return ent_at(p) & 0x7fffffff;
     else return p;
   };
 
@@ -311,6 +329,23 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
   uint32_t mreg[2] = {~0u, ~0u};
   int tile_cur = 0;                // key tile of the tile in flight
   bool mpart = false;              // the tile in flight has dropped entries
+  // Mask without a score: the list entry and mask bits of position p+1 are
+  // loaded at the start of M(p) (the "next" set) and become current at the
+  // start of M(p+1), so the softmax phase never waits for them.
+  uint32_t mreg_nx[2] = {~0u, ~0u};
+  int tile_nx = 0;
+  bool mpart_nx = false;
+  auto fetch_mask = [&](int p) __attribute__((always_inline)) {   // position p < nt_w -> next set
+    const int e = ent_at(p);
+    tile_nx = e & 0x7fffffff;
+    mpart_nx = e >= 0;
+    mreg_nx[0] = mreg_nx[1] = ~0u;
+    if (mpart_nx) {
+      const u32x2 w = *(const u32x2*)(mbits + 2 * tile_nx);
+      mreg_nx[0] = w[0] >> (4 * hf);
+      mreg_nx[1] = w[1] >> (4 * hf);
+    }
+  };
   f32x4 sreg[SCORE ? 8 : 1];       // score of the tile in flight
   float m_run = kNegInf, l_run = 0.f;
 
@@ -321,7 +356,15 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
     constexpr int KB = decltype(KBc)::value;
     constexpr uint32_t kb_lds = KB * TILEB;                      // K(p), relative to K buffer 0
     constexpr uint32_t vb_lds = ((KB + NBUF - 1) % NBUF) * TILEB;  // V(p-1), relative to V buffer 0
-    if constexpr (MASK || SCORE) {
+    if constexpr (ENTV) {
+      // position p's set (fetched in M(p-1) or the prologue) becomes current;
+      // fetch position p+1's
+      tile_cur = tile_nx;
+      mpart = mpart_nx;
+      mreg[0] = mreg_nx[0];
+      mreg[1] = mreg_nx[1];
+      if (p + 1 < nt_w) fetch_mask(p + 1);
+    } else if constexpr (MASK || SCORE) {
       if (p < nt_w) {
         int t = p;
         if constexpr (MASK) {
@@ -464,6 +507,9 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
     for (int u = 0; u < TILEB / (kThreads * 16); ++u) lds_write16(z + (tid + u * kThreads) * 16, u32x4{0, 0, 0, 0});
   }
   load_q();
+  if constexpr (ENTV) {
+    if (nt_w > 0) fetch_mask(0);
+  }
   put_tile(true, 0, 0);
   put_tile(true, 1, 1);
   put_tile(false, 0, 0);
