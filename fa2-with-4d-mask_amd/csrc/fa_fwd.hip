@@ -179,7 +179,14 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
     mbits = (const uint32_t*)(a.mws + a.ml.bits + pm * a.ml.pbits) + (int64_t)qrow_c * a.ml.wk;
   }
   const int kv_end = CAUSAL ? min(Tk, q0 + BM) : Tk;
-  const int nt = MASK ? flist[0] : (kv_end + BN - 1) / BN;
+  // with a mask: count and first two entries in one scalar load (the words
+  // past a short list are still inside the workspace; only used when valid)
+  int32_t fl[3] = {0, 0, 0};
+  if constexpr (MASK) {
+#pragma unroll
+    for (int i = 0; i < 3; ++i) fl[i] = flist[i];
+  }
+  const int nt = MASK ? fl[0] : (kv_end + BN - 1) / BN;
   // tiles of this wave (opaque: keeps the per-pair guards dynamic, so that
   // every instantiation gets the same control flow and register assignment);
   // with a mask every wave walks the whole list (causality is applied per key)
@@ -192,8 +199,11 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
   constexpr bool ENTV = MASK && !SCORE;
   int32_t ents[ENTV ? 2 : 1] = {};
   if constexpr (ENTV) {
+    // range-checked loads (positions past the row read 0): no wait on the count
+    const auto rl = __builtin_amdgcn_make_buffer_rsrc((void*)flist, (short)0, (1 + a.ml.nft) * 4, 0x00020000);
 #pragma unroll
-    for (int w = 0; w < 2; ++w) ents[w] = 64 * w + lane < nt ? flist[1 + 64 * w + lane] : 0;
+    for (int w = 0; w < 2; ++w)
+      ents[w] = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(rl, (uint32_t)(1 + 64 * w + lane) * 4, 0, 0);
   }
   auto ent_at = [&](int p) __attribute__((always_inline)) -> int32_t {
     if constexpr (ENTV) {
@@ -225,16 +235,20 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
   }
   // Tile at list position p: rows [t BN, min(Tk, t BN + BN)) of t = tile_at(p);
   // p >= nt gives an empty range (the loads return zeros).
-  auto rsrc_of = [&](const T* base, int64_t st, int p) __attribute__((always_inline)) {
+  // Key tile t (valid: rows [t BN, min(Tk, t BN + BN)); else an empty range:
+  // the loads return zeros).
+  auto rsrc_tile = [&](const T* base, int64_t st, int t, bool valid) __attribute__((always_inline)) {
     uint32_t nrec = 0;
     const T* tb = base;
-    if (p < nt) {
-      const int t = tile_at(p);
+    if (valid) {
       const int64_t rows = min(Tk - t * BN, BN);
       nrec = (uint32_t)min((rows - 1) * st * 2 + ROWB, (int64_t)0xfffffff0);
       tb = base + (int64_t)t * BN * st;
     }
     return __builtin_amdgcn_make_buffer_rsrc((void*)tb, (short)0, (int)nrec, 0x00020000);
+  };
+  auto rsrc_of = [&](const T* base, int64_t st, int p) __attribute__((always_inline)) {
+    return p < nt ? rsrc_tile(base, st, tile_at(p), true) : rsrc_tile(base, st, 0, false);
   };
   u32x4 stg[NSTG];   // K slots, then V slots, of the next batch
   // Without a mask, list position = key tile, and the batch descriptors come
@@ -283,8 +297,10 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
     }
   };
   // Tile written straight through the staging registers (prologue).
-  auto put_tile = [&](bool is_k, int t, int buf) __attribute__((always_inline)) {
-    const auto rs = is_k ? rsrc_of(kp, a.kst, t) : rsrc_of(vp, a.vst, t);
+  // (positions 0 and 1: tiles from the scalar-loaded first entries)
+  auto put_tile = [&](bool is_k, int p, int buf) __attribute__((always_inline)) {
+    const int t = MASK ? (fl[1 + p] & 0x7fffffff) : p;
+    const auto rs = is_k ? rsrc_tile(kp, a.kst, t, p < nt) : rsrc_tile(vp, a.vst, t, p < nt);
 #pragma unroll
     for (int u = 0; u < IPW; ++u) {
       const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(rs, is_k ? goff_k[u] : goff_v[u], 0, 0);
@@ -336,7 +352,7 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
   int tile_nx = 0;
   bool mpart_nx = false;
   auto fetch_mask = [&](int p) __attribute__((always_inline)) {   // position p < nt_w -> next set
-    const int e = ent_at(p);
+    const int e = p == 0 ? fl[1] : ent_at(p);
     tile_nx = e & 0x7fffffff;
     mpart_nx = e >= 0;
     mreg_nx[0] = mreg_nx[1] = ~0u;
