@@ -320,12 +320,12 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
   auto next_step = [&](int j) __attribute__((always_inline)) {
     const int s = it_qs >> 5;
     if constexpr (MASK) {
-      // tiles of blocks without a kept entry are neither stored nor read
-      bool ok = ds_on && j < n && (!CAUSAL || kb32 <= s);
-      if (ok) {
-        const uint8_t* bl = (const uint8_t*)(a.mws + a.ml.blk + mask_plane(a.ml, b, it_h) * a.ml.pblk);
-        ok = bl[(int64_t)s * a.ml.nk32 + kb32] != 0;
-      }
+      // tiles of blocks without a kept entry are neither stored nor read: the
+      // block holds one iff a lane's transposed mask word (loaded for this
+      // step; the lanes of half 0 hold the whole words of the 32 keys) is
+      // not 0 -- the block state the dQ kernel reads, without a scalar load
+      const bool any = __builtin_amdgcn_ballot_w64(mreg != 0u) != 0;
+      const bool ok = ds_on && j < n && (!CAUSAL || kb32 <= s) && any;
       const int64_t tile = ((int64_t)b * a.Hq + it_h - ds_u0) * a.ds_plane + ds_row(s, a.nk32, CAUSAL) + kb32;
       ds_rs = __builtin_amdgcn_make_buffer_rsrc((void*)((uint16_t*)a.ds + tile * 1024), (short)0, ok ? 2048 : 0,
                                                 0x00020000);
