@@ -101,6 +101,31 @@ __global__ __launch_bounds__(kDqWaves * 64, 2) void dq_ds_kernel(const BwdArgs a
   const int chunk = (nstep + nsp - 1) / nsp;
   const int jb = min(nstep, ksp * chunk);
   const int nloc = min(nstep, jb + chunk) - jb;
+  // With a mask, positions jl < 128 of this workgroup's range sit in two
+  // registers (lane i of ents[w]: position 64 w + i), read with readlane:
+  // the key step, and in bits 30 and 31 whether the dK/dV kernel stored the
+  // tile of this wave's query step 0 and 1 (step below Tq, on or below the
+  // causal diagonal, block holding a kept entry).  Later positions use
+  // scalar loads.  (Per-step scalar loads of the list and block states cost
+  // a quarter of the kernel's time at the packed-document config.)
+  int32_t ents[MASK ? 2 : 1] = {};
+  if constexpr (MASK) {
+#pragma unroll
+    for (int w = 0; w < 2; ++w) {
+      const int jl = 64 * w + lane;
+      if (jl < nloc) {
+        const int kb = dql[1 + jb + jl];
+        int32_t e = kb;
+#pragma unroll
+        for (int i = 0; i < kDqSteps; ++i) {
+          const int s = s0 + i;
+          const bool ok = s < nq32 && (!CAUSAL || kb <= s) && blk[(int64_t)s * nk32 + kb] != 0;
+          e |= ok ? (int32_t)(1u << (30 + i)) : 0;
+        }
+        ents[w] = e;
+      }
+    }
+  }
 
   // ---- LDS addresses ---------------------------------------------------------------
   const uint32_t lds0 = (uint32_t)(uintptr_t)(FA_LDS char*)smem;
@@ -150,7 +175,25 @@ __global__ __launch_bounds__(kDqWaves * 64, 2) void dq_ds_kernel(const BwdArgs a
   auto load = [&](int S, int jl) __attribute__((always_inline)) {
     const bool inr = jl < nloc;
     const int j = jb + jl;
-    const int kb = MASK ? (inr ? dql[1 + j] : 0) : j;
+    int kb = j;
+    uint32_t okb = 0;   // with a mask, bit i: the tile of query step s0 + i is stored
+    if constexpr (MASK) {
+      kb = 0;
+      if (inr) {
+        if (jl < 128) {
+          const int32_t e = __builtin_amdgcn_readlane(ents[jl >> 6], jl & 63);
+          kb = e & 0x3fffffff;
+          okb = (uint32_t)e >> 30;
+        } else {
+          kb = dql[1 + j];
+#pragma unroll
+          for (int i = 0; i < kDqSteps; ++i) {
+            const int s = s0 + i;
+            if (s < nq32 && (!CAUSAL || kb <= s) && blk[(int64_t)s * nk32 + kb] != 0) okb |= 1u << i;
+          }
+        }
+      }
+    }
     const int rows = inr ? min(32, Tk - kb * 32) : 0;
     const int nrec = rows > 0 ? (int)((int64_t)(rows - 1) * a.kst * 2 + ROWB) : 0;
     const auto rk = __builtin_amdgcn_make_buffer_rsrc((void*)(kbase + (int64_t)kb * 32 * a.kst), (short)0, nrec, 0x00020000);
@@ -159,8 +202,7 @@ __global__ __launch_bounds__(kDqWaves * 64, 2) void dq_ds_kernel(const BwdArgs a
 #pragma unroll
     for (int i = 0; i < kDqSteps; ++i) {
       const int s = s0 + i;
-      bool ok = inr && s < nq32 && (!CAUSAL || kb <= s);
-      if constexpr (MASK) ok = ok && blk[(int64_t)s * nk32 + kb] != 0;
+      const bool ok = MASK ? ((okb >> i) & 1u) != 0 : inr && s < nq32 && (!CAUSAL || kb <= s);
       const auto rd = __builtin_amdgcn_make_buffer_rsrc((void*)(dsp + (row0[i] + kb) * 1024), (short)0, ok ? 2048 : 0,
                                                         0x00020000);
 #pragma unroll

@@ -199,15 +199,18 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
     const bool live = ld_it < n;
     if constexpr (MASK) {
       // position the loads at the cursor's step (rows past Tq read as zeros)
-      ld_h = min(ldc.h, h_end - 1);
+      const int h_new = min(ldc.h, h_end - 1);
       ld_qs = live ? kStep * ldc.lst[1 + ldc.idx] : 0;
       so_q = (uint32_t)ld_qs * (uint32_t)a.qst * 2;
       so_d = (uint32_t)ld_qs * (uint32_t)a.dst * 2;
       so_l = (uint32_t)ld_qs * 4;
-      q_head = (const T*)a.q + b * a.qsb + (int64_t)ld_h * a.qsh;
-      d_head = (const T*)a.dout + b * a.dsb + (int64_t)ld_h * a.dsh;
-      l_head = a.lse + ((int64_t)b * a.Hq + ld_h) * Tq;
-      e_head = a.delta + ((int64_t)b * a.Hq + ld_h) * Tq;
+      if (h_new != ld_h) {   // head pointers change only with the head
+        ld_h = h_new;
+        q_head = (const T*)a.q + b * a.qsb + (int64_t)ld_h * a.qsh;
+        d_head = (const T*)a.dout + b * a.dsb + (int64_t)ld_h * a.dsh;
+        l_head = a.lse + ((int64_t)b * a.Hq + ld_h) * Tq;
+        e_head = a.delta + ((int64_t)b * a.Hq + ld_h) * Tq;
+      }
     }
     const auto rq = MASK ? rs_of(q_head, q_rec, live) : rq_c;
     const auto rd = MASK ? rs_of(d_head, d_rec, live) : rd_c;
