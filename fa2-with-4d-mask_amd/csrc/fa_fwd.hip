@@ -191,12 +191,12 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
   // every instantiation gets the same control flow and register assignment);
   // with a mask every wave walks the whole list (causality is applied per key)
   const int nt_w = (int)opaque((uint32_t)(CAUSAL && !MASK ? min(nt, (min(Tk, q0w + 32) + BN - 1) / BN) : nt));
-  // List entries: without a score, positions 0..127 sit in two registers
-  // (lane i of ents[w] holds position 64 w + i) and are read with readlane,
-  // so that walking the list costs no scalar-memory waits in the pipeline;
-  // later positions (and the score kernels, which have no registers to
-  // spare) load them.
-  constexpr bool ENTV = MASK && !SCORE;
+  // List entries: positions 0..127 sit in two registers (lane i of ents[w]
+  // holds position 64 w + i) and are read with readlane, so that walking the
+  // list costs no scalar-memory waits in the pipeline; later positions load
+  // them.
+  constexpr bool ENTV = MASK;
+  constexpr bool MPRE = MASK && !SCORE;   // mask bits fetched a pair ahead (no registers to spare with a score)
   int32_t ents[ENTV ? 2 : 1] = {};
   if constexpr (ENTV) {
     // range-checked loads (positions past the row read 0): no wait on the count
@@ -372,7 +372,7 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
     constexpr int KB = decltype(KBc)::value;
     constexpr uint32_t kb_lds = KB * TILEB;                      // K(p), relative to K buffer 0
     constexpr uint32_t vb_lds = ((KB + NBUF - 1) % NBUF) * TILEB;  // V(p-1), relative to V buffer 0
-    if constexpr (ENTV) {
+    if constexpr (MPRE) {
       // position p's set (fetched in M(p-1) or the prologue) becomes current;
       // fetch position p+1's
       tile_cur = tile_nx;
@@ -384,7 +384,7 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
       if (p < nt_w) {
         int t = p;
         if constexpr (MASK) {
-          const int e = flist[1 + p];
+          const int e = ent_at(p);
           t = e & 0x7fffffff;
           mpart = e >= 0;
           mreg[0] = mreg[1] = ~0u;
@@ -523,7 +523,7 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
     for (int u = 0; u < TILEB / (kThreads * 16); ++u) lds_write16(z + (tid + u * kThreads) * 16, u32x4{0, 0, 0, 0});
   }
   load_q();
-  if constexpr (ENTV) {
+  if constexpr (MPRE) {
     if (nt_w > 0) fetch_mask(0);
   }
   put_tile(true, 0, 0);
