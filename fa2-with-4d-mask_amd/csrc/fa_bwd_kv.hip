@@ -112,8 +112,23 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
     if (a.ml.Hm == 1) n = gsz * kv_list(h_first)[0];
     else for (int h = h_first; h < h_end; ++h) n += kv_list(h)[0];
   }
+  // When the workgroup's heads share one list (a mask broadcast over the
+  // heads, or one head per workgroup) of at most 128 steps, it sits in two
+  // registers (lane i of lreg_v[w]: position 64 w + i), read with readlane
+  // instead of a scalar load per step.
+  const bool lreg = MASK && (a.ml.Hm == 1 || gsz == 1) && a.ml.nq32 <= 128;
+  int32_t lreg_v[MASK ? 2 : 1] = {};
+  if constexpr (MASK) {
+    if (lreg) {
+      const int32_t* l0 = kv_list(h_first);
+      const int cnt0 = l0[0];
+#pragma unroll
+      for (int w = 0; w < 2; ++w) lreg_v[w] = 64 * w + lane < cnt0 ? l0[1 + 64 * w + lane] : 0;
+    }
+  }
   // List cursor (MASK): head h, position idx in that head's list of cnt
-  // steps; seek() moves past exhausted and empty lists.
+  // steps; seek() moves past exhausted and empty lists.  list_at(c): the
+  // query step at the cursor.
   struct Cursor { int h, idx, cnt; const int32_t* lst; };
   auto seek = [&](Cursor& c) __attribute__((always_inline)) {
     while (c.idx >= c.cnt && c.h < h_end) {
@@ -121,6 +136,14 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
       c.idx = 0;
       if (c.h < h_end) { c.lst = kv_list(c.h); c.cnt = c.lst[0]; }
     }
+  };
+  auto list_at = [&](const Cursor& c) __attribute__((always_inline)) -> int {
+    if (lreg) {
+      const int lo = __builtin_amdgcn_readlane(lreg_v[0], c.idx & 63);
+      const int hi = __builtin_amdgcn_readlane(lreg_v[1], c.idx & 63);
+      return c.idx < 64 ? lo : hi;
+    }
+    return c.lst[1 + c.idx];
   };
   auto cursor0 = [&]() __attribute__((always_inline)) -> Cursor {
     Cursor c{h_first, 0, 0, nullptr};
@@ -200,7 +223,7 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
     if constexpr (MASK) {
       // position the loads at the cursor's step (rows past Tq read as zeros)
       const int h_new = min(ldc.h, h_end - 1);
-      ld_qs = live ? kStep * ldc.lst[1 + ldc.idx] : 0;
+      ld_qs = live ? kStep * list_at(ldc) : 0;
       so_q = (uint32_t)ld_qs * (uint32_t)a.qst * 2;
       so_d = (uint32_t)ld_qs * (uint32_t)a.dst * 2;
       so_l = (uint32_t)ld_qs * 4;
@@ -275,7 +298,7 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
   Cursor itc = cursor0();
   if constexpr (MASK) {
     it_h = min(itc.h, h_end - 1);
-    it_qs = n > 0 ? kStep * itc.lst[1] : 0;
+    it_qs = n > 0 ? kStep * list_at(itc) : 0;
   }
 
   // ---- mask / score of a step (lane's 16 query rows at its key) -----------------
@@ -337,7 +360,7 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
         seek(itc);
       }
       it_h = min(itc.h, h_end - 1);
-      it_qs = j + 1 < n ? kStep * itc.lst[1 + itc.idx] : 0;
+      it_qs = j + 1 < n ? kStep * list_at(itc) : 0;
       return;
     }
     const bool ok = ds_on && j < n && (!CAUSAL || kb32 <= s);
