@@ -19,11 +19,12 @@
 //   M(p): S(p) = K(p) Q^T and O += V(p-1)^T P(p-1)      (MFMA phase)
 //   V(p): softmax of S(p) -> P(p)                        (VALU phase)
 // Waves w and w+4 share a SIMD, so while one issues MFMAs the other issues
-// VALU work; a workgroup barrier ends each pair of phases.  The MFMA wave runs
-// at a raised issue priority so that the softmax wave fills the gaps.
+// VALU work; a workgroup barrier ends every pair of phases (every second pair
+// with four K/V buffers).  The MFMA wave runs at a raised issue priority so
+// that the softmax wave fills the gaps.
 //
-// K/V staging: three or four LDS buffers each for K and V.  In its softmax phase each
-// wave writes its share of the tiles loaded one phase pair earlier (16 bytes
+// K/V staging: three or four LDS buffers each for K and V.  In its softmax
+// phase each wave writes its share of the tiles loaded one phase pair earlier (16 bytes
 // per lane per chunk, held in registers meanwhile) and loads its share of the
 // next ones, with buffer loads whose per-lane offsets are loop-invariant and
 // whose tile base sits in scalar registers; rows past the end of the keys are
