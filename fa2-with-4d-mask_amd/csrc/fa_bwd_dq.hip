@@ -311,10 +311,18 @@ __global__ __launch_bounds__(kDqWaves * 64, 2) void dq_ds_kernel(const BwdArgs a
       }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     const int q0 = (s0 + i) * 32;
+    // all staging reads first (one wait), then the row-guarded stores
+    constexpr int NU = 32 * CH / 64;
+    u32x4 ov[NU];
 #pragma unroll
-    for (int u = 0; u < 32 * CH / 64; ++u) {
+    for (int u = 0; u < NU; ++u) {
+      const int idx = lane + u * 64;
+      ov[u] = lds_read16(stg + (idx / CH) * OS + (idx % CH) * 8);
+    }
+#pragma unroll
+    for (int u = 0; u < NU; ++u) {
       const int idx = lane + u * 64, r = idx / CH, c = idx % CH;
-      if (q0 + r < Tq) gstore16(dqp + (int64_t)(q0 + r) * a.dqst + c * 8, lds_read16(stg + r * OS + c * 8));
+      if (q0 + r < Tq) gstore16(dqp + (int64_t)(q0 + r) * a.dqst + c * 8, ov[u]);
     }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   }

@@ -571,10 +571,18 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
           lds_write8(stg + l32 * OS + d, v);
         }
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      // all staging reads first (one wait), then the row-guarded stores
+      constexpr int NU = 32 * CH / 64;
+      u32x4 ov[NU];
 #pragma unroll
-      for (int u = 0; u < 32 * CH / 64; ++u) {
+      for (int u = 0; u < NU; ++u) {
+        const int idx = lane + u * 64;
+        ov[u] = lds_read16(stg + (idx / CH) * OS + (idx % CH) * 8);
+      }
+#pragma unroll
+      for (int u = 0; u < NU; ++u) {
         const int idx = lane + u * 64, r = idx / CH, c = idx % CH;
-        if (kw0 + r < Tk) gstore16(dst + (int64_t)(kw0 + r) * dstt + c * 8, lds_read16(stg + r * OS + c * 8));
+        if (kw0 + r < Tk) gstore16(dst + (int64_t)(kw0 + r) * dstt + c * 8, ov[u]);
       }
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     };

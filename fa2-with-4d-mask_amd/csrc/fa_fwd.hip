@@ -595,12 +595,20 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
     }
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // wave-private region: no barrier needed
   T* op = (T*)a.o + b * a.osb + h * a.osh;
+  // all staging reads first (one wait), then the row-guarded stores
+  constexpr int NU = 32 * CH / 64;
+  u32x4 ov[NU];
 #pragma unroll
-  for (int u = 0; u < 32 * CH / 64; ++u) {
+  for (int u = 0; u < NU; ++u) {
+    const int idx = lane + u * 64;
+    ov[u] = lds_read16(os + (idx / CH) * OS + (idx % CH) * 8);
+  }
+#pragma unroll
+  for (int u = 0; u < NU; ++u) {
     const int idx = lane + u * 64;
     const int r = idx / CH, c = idx % CH;
     const int qr = q0w + r;
-    if (qr < Tq) gstore16(op + (int64_t)qr * a.ost + c * 8, lds_read16(os + r * OS + c * 8));
+    if (qr < Tq) gstore16(op + (int64_t)qr * a.ost + c * 8, ov[u]);
   }
   if (hf == 0 && qrow < Tq)
     a.lse[((int64_t)b * a.Hq + h) * Tq + qrow] = (l_tot > 0.f) ? m_run + log2_fast(l_tot) : kPosInf;
