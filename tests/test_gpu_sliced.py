@@ -1,0 +1,67 @@
+"""The backward over slices of (batch, kv-head) units at a long sequence.
+
+At T = 16384 with the headline's heads (B1 Hq32 Hk8 D128) the dS tiles of all
+units (17 GB, 8.6 GB causal) exceed the default 8 GiB workspace, so the
+backward runs the dK/dV and dQ kernels once per slice of units
+(csrc/fa_api.cpp ``ds_slice_units``).  The same call with a limit that holds
+every unit runs them once.  Checks:
+
+* non-causal, deterministic: the sliced and the single-launch gradients are
+  bitwise equal (the same workgroups do the same arithmetic; only the launch
+  they belong to differs);
+* causal, deterministic: sliced launches split each head group in two (fp32
+  dK/dV slabs summed in a fixed order), so dK and dV may round to the
+  neighbouring bf16 value (0.07 % of the entries at this size); dQ is
+  bitwise equal, dK/dV within one bf16 step of the single launch (slicing
+  alone, at an equal split, is bitwise exact);
+* atomic mode, non-causal: sliced and single-launch dQ agree within fp32
+  summation order (dK/dV bitwise).
+
+The parity of the slicing itself against the oracle runs at small shapes in
+tests/test_gpu_parity.py (modes ``det_sliced``, ``atomic_sliced``).
+"""
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def _grads(q, k, v, do, *, causal, atomic, limit):
+    import tilelang_fa2_4d_mask as api
+    import tilelang_fa2_4d_mask.fa2 as fa2mod
+
+    fa2mod.DS_LIMIT_BYTES = limit
+    try:
+        qq, kk, vv = (x.detach().requires_grad_(True) for x in (q, k, v))
+        api.tilelang_flash_attention(qq, kk, vv, is_causal=causal, use_atomic_backward=atomic).backward(do)
+        torch.cuda.synchronize()
+        return qq.grad, kk.grad, vv.grad
+    finally:
+        fa2mod.DS_LIMIT_BYTES = 0
+
+
+@pytest.mark.parametrize("causal,atomic", [(False, False), (True, False), (False, True)],
+                         ids=["det", "det_causal", "atomic"])
+def test_sliced_backward_matches_single_launch(cuda, causal, atomic):
+    T = 16384
+    g = torch.Generator().manual_seed(11)
+    q, k, v, do = (torch.randn(1, T, h, 128, generator=g).to(torch.bfloat16).to(cuda).transpose(1, 2)
+                   for h in (32, 8, 8, 32))
+    print(f"case T={T} causal={causal} atomic={atomic}: sliced (default limit) vs one launch", flush=True)
+    sliced = _grads(q, k, v, do, causal=causal, atomic=atomic, limit=0)
+    single = _grads(q, k, v, do, causal=causal, atomic=atomic, limit=64 << 30)
+    for name, a, b in zip(("dq", "dk", "dv"), sliced, single):
+        assert torch.isfinite(a).all(), name
+        if (name == "dq" and not atomic) or (name != "dq" and not causal):
+            assert torch.equal(a, b), name
+        else:
+            # one bf16 step of the value (fp32 sums in another order, rounded
+            # once); entries near zero after cancellation get an absolute floor
+            bf = b.float()
+            step = bf.abs() * 2.0 ** -7 + 1e-5 * bf.abs().max()
+            diff = (a.float() - bf).abs()
+            assert (diff <= step).all(), f"{name}: max diff {diff.max().item():.3e}"
+        del a, b
+    del sliced, single
+    torch.cuda.empty_cache()
