@@ -146,7 +146,10 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
   const int h = kvh * a.G + g;
 
   const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = tid >> 6, grp = wave >> 2;
+  // D = 64: the softmax phase is over twice the MFMA phase, and the two
+  // groups run in step (no phase offset), which measured 6 % faster there;
+  // D = 128 needs the offset (in step it ran 3x slower)
+  const int wave = tid >> 6, grp = D == 128 ? wave >> 2 : 0;
   const int l32 = lane & 31, hf = lane >> 5;
   const int q0 = qt * BM, q0w = q0 + wave * 32;
   const int qrow = q0w + l32;
