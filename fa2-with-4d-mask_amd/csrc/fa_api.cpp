@@ -133,11 +133,21 @@ Route route_of(const FaBwdParams* p) {
 
 // Key ranges of the atomic dQ-from-dS kernel: at least 2, more while the grid
 // is below ~1024 workgroups and each range keeps >= 4 key steps.
+// query rows per workgroup of the dQ-from-dS kernel: 512 (8 waves sharing
+// each K tile) for the deterministic kernel at head dim 128 without a mask
+// when that still gives every CU a workgroup, else 256
+int dq_rows(const FaBwdParams* p) {
+  if (p->head_dim != 128 || p->mask || p->atomic_dq) return fa::kDqDsRows;
+  const int64_t wide = ds_slice_units(p) * (p->heads_q / p->heads_k) *
+                       ((p->seqlen_q + fa::kDqDsRowsWide - 1) / fa::kDqDsRowsWide);
+  return wide >= 256 ? fa::kDqDsRowsWide : fa::kDqDsRows;
+}
+
 int dq_split_of(const FaBwdParams* p) {
   if (route_of(p) != kDsAtomic) return 1;
   // workgroups of one launch (one slice of units)
   const int64_t nblk = ds_slice_units(p) * (p->heads_q / p->heads_k) *
-                       ((p->seqlen_q + fa::dq_ds_block_rows() - 1) / fa::dq_ds_block_rows());
+                       ((p->seqlen_q + dq_rows(p) - 1) / dq_rows(p));
   const int nks = (p->seqlen_k + 31) / 32;
   if (nks < 2) return 1;
   int split = 2;
@@ -401,7 +411,8 @@ int fa_bwd(const FaBwdParams* p) {
     // the next slice overwrites them)
     const int per = (int)ds_slice_units(p), units = p->batch * p->heads_k;
     fa::BwdArgs q = a;
-    q.nqt = (p->seqlen_q + fa::dq_ds_block_rows() - 1) / fa::dq_ds_block_rows();
+    q.dq_rows = dq_rows(p);
+    q.nqt = (p->seqlen_q + q.dq_rows - 1) / q.dq_rows;
     for (int u0 = 0; u0 < units; u0 += per) {
       fa::BwdArgs k = a;
       k.bk0 = q.bk0 = u0;
@@ -427,7 +438,8 @@ int fa_bwd_finalize(const FaBwdParams* p) {
     const bool causal = p->is_causal != 0;
     if (a.ds) {
       // sliced: fa_bwd already ran the dQ kernel per slice
-      a.nqt = (p->seqlen_q + fa::dq_ds_block_rows() - 1) / fa::dq_ds_block_rows();
+      a.dq_rows = dq_rows(p);
+      a.nqt = (p->seqlen_q + a.dq_rows - 1) / a.dq_rows;
       if (ds_slices(p) == 1 && (st = launch_status(fa::launch_bwd_dq_ds(a, p->head_dim, p->dtype, causal, s), "dq")))
         return st;
     } else {

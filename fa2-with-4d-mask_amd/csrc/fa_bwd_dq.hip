@@ -39,13 +39,18 @@ namespace {
 
 using namespace pipe;
 
-constexpr int kDqWaves = 4;
 constexpr int kDqSteps = 2;                           // 32-row query steps per wave
-constexpr int kDqRows = kDqWaves * kDqSteps * 32;     // query rows per workgroup
 constexpr int kSets = 3;                              // register staging sets: tiles in flight
 
-template <typename T, int D, bool CAUSAL, bool MASK, bool ATOMIC>
-__global__ __launch_bounds__(kDqWaves * 64, 2) void dq_ds_kernel(const BwdArgs a) {
+// NW waves per workgroup, 64 query rows each.  NW = 8 (deterministic, head
+// dim 128, no mask, enough rows to give every CU a workgroup) shares each
+// step's K tile among 512 query rows, which halves its L2 reads (15 % faster
+// at T 8192); else NW = 4 (the prepared-mask lists are built per 256-row
+// block; with atomics 8 waves were 3-5 % slower).
+template <typename T, int D, bool CAUSAL, bool MASK, bool ATOMIC, int NW>
+__global__ __launch_bounds__(NW * 64, 2) void dq_ds_kernel(const BwdArgs a) {
+  constexpr int kDqWaves = NW;
+  constexpr int kDqRows = kDqWaves * kDqSteps * 32;   // query rows per workgroup
   using V8 = typename Vec8<T>::type;
   constexpr int NB = D / 32, CH = D / 8, ROWB = 2 * D;
   constexpr int KTILE = 32 * ROWB;                   // bytes of one K step tile
@@ -56,7 +61,8 @@ __global__ __launch_bounds__(kDqWaves * 64, 2) void dq_ds_kernel(const BwdArgs a
   constexpr int OS = D + 8;                          // epilogue staging stride (elements)
   static_assert(UK >= 1 && UD >= 1, "tile split");
   static_assert(kDqWaves * 32 * OS * 2 <= 2 * BUFB, "epilogue staging fits");
-  static_assert(kDqRows == kDqDsRows, "prepared-mask lists are built for this shape");
+  static_assert(kDqRows == (NW == 8 ? kDqDsRowsWide : kDqDsRows) && (!MASK || NW == 4),
+                "row blocks as the host and the prepared-mask lists assume");
   constexpr int OSF = D + 4;                         // atomic epilogue: fp32 staging stride
   constexpr int SMEM = ATOMIC && kDqWaves * 32 * OSF * 4 > 2 * BUFB ? kDqWaves * 32 * OSF * 4 : 2 * BUFB;
   __shared__ __attribute__((aligned(1024))) char smem[SMEM];
@@ -330,9 +336,15 @@ __global__ __launch_bounds__(kDqWaves * 64, 2) void dq_ds_kernel(const BwdArgs a
 
 template <typename T, int D, bool CAUSAL, bool ATOMIC>
 hipError_t launch_a(const BwdArgs& a, hipStream_t s) {
-  const dim3 grid((unsigned)(a.nbk * a.G * a.nqt * (ATOMIC ? a.dq_split : 1))), block(kDqWaves * 64);
-  if (a.mask) hipLaunchKernelGGL((dq_ds_kernel<T, D, CAUSAL, true, ATOMIC>), grid, block, 0, s, a);
-  else hipLaunchKernelGGL((dq_ds_kernel<T, D, CAUSAL, false, ATOMIC>), grid, block, 0, s, a);
+  const dim3 grid((unsigned)(a.nbk * a.G * a.nqt * (ATOMIC ? a.dq_split : 1)));
+  if (a.mask) {
+    hipLaunchKernelGGL((dq_ds_kernel<T, D, CAUSAL, true, ATOMIC, 4>), grid, dim3(256), 0, s, a);
+  } else if constexpr (D == 128 && !ATOMIC) {
+    if (a.dq_rows == kDqDsRowsWide) hipLaunchKernelGGL((dq_ds_kernel<T, D, CAUSAL, false, ATOMIC, 8>), grid, dim3(512), 0, s, a);
+    else hipLaunchKernelGGL((dq_ds_kernel<T, D, CAUSAL, false, ATOMIC, 4>), grid, dim3(256), 0, s, a);
+  } else {
+    hipLaunchKernelGGL((dq_ds_kernel<T, D, CAUSAL, false, ATOMIC, 4>), grid, dim3(256), 0, s, a);
+  }
   return hipGetLastError();
 }
 
@@ -343,7 +355,6 @@ hipError_t launch_t(const BwdArgs& a, hipStream_t s) {
 
 }  // namespace
 
-int dq_ds_block_rows() { return kDqRows; }
 
 hipError_t launch_bwd_dq_ds(const BwdArgs& a, int D, int dtype, bool causal, hipStream_t s) {
   if (dtype == 0) {

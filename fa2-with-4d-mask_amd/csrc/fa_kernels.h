@@ -11,6 +11,7 @@ constexpr int kFwdRows = 256;    // forward: query rows per workgroup
 constexpr int kFwdKeys = 64;     //          keys per tile
 constexpr int kKv2Keys = 128;    // dK/dV (deterministic): keys per workgroup, 32-row steps
 constexpr int kDqDsRows = 256;   // dQ from dS: query rows per workgroup, 32-key steps
+constexpr int kDqDsRowsWide = 512;   // the same with 8 waves (deterministic, D 128, no mask)
 
 // Prepared mask (workspace written by fa_mask_prepare from the bool mask).
 // One plane per (mask batch, mask head): Bm = 1 when the mask's batch stride
@@ -118,6 +119,7 @@ struct BwdArgs {
   // holds the planes of the slice, from unit bk0 on.  Others: 0, B Hk.
   int bk0, nbk;
   int nqt;              // query tiles per (b, h) (dQ kernel)
+  int dq_rows;          // query rows per dQ-from-dS workgroup: kDqDsRows or kDqDsRowsWide
   int split;            // query-head-group split of the dK/dV kernel
   int do_dq;            // dQ accumulated with fp32 atomics into dq_accum (fused in the dK/dV
                         // kernel, or by the dQ-from-dS kernel over dq_split key ranges)
@@ -165,7 +167,6 @@ hipError_t launch_bwd_dkdv2(const BwdArgs& a, int D, int dtype, bool causal, hip
 int dkdv2_block_keys();
 // dQ = scale * dS K from the dS tiles, 256 query rows per workgroup.
 hipError_t launch_bwd_dq_ds(const BwdArgs& a, int D, int dtype, bool causal, hipStream_t s);
-int dq_ds_block_rows();
 hipError_t launch_convert(const CvtArgs& a, int dtype, hipStream_t s);
 // Bool mask -> prepared mask workspace (bits, transposed bits, block states, lists).
 hipError_t launch_mask_prepare(const MaskArgs& a, hipStream_t s);

@@ -161,6 +161,27 @@ def test_small_vs_oracle(cuda, cfg, mode):
     check(ours, ref, label=f"{cfg.name}/{mode}")
 
 
+# Shapes with enough 512-row query blocks (B Hq ceil(Tq / 512) >= 256) that
+# the deterministic dQ kernel runs its 8-wave workgroups (head dim 128, no
+# mask); ragged Tq and Tk, causal with Tq != Tk, fp16
+WIDE_DQ = [
+    C("wide_dq_ragged", 2, 1000, 900, 64, 8, 128),
+    C("wide_dq_causal", 1, 700, 760, 128, 16, 128, is_causal=True),
+    C("wide_dq_fp16_bshd", 1, 520, 520, 128, 32, 128, torch.float16, layout="bshd"),
+]
+
+
+@pytest.mark.parametrize("mode", ["det_ds"])
+@pytest.mark.parametrize("cfg", WIDE_DQ, ids=[c.name for c in WIDE_DQ])
+def test_wide_dq_vs_oracle(cuda, cfg, mode):
+    case = I.make_case(cfg, seed=5)
+    print(f"case {cfg.name} mode={mode}", flush=True)
+    atomic, ds_limit = MODES[mode]
+    ours = run_ours(case, cfg, atomic=atomic, ds_limit=ds_limit)
+    ref = run_oracle_cpu(case, cfg)
+    check(ours, ref, label=f"{cfg.name}/{mode}")
+
+
 @pytest.mark.parametrize("mode", ["atomic", "det_ds"])
 @pytest.mark.parametrize("scale", [0.05, -0.08, 0.0], ids=["small", "negative", "zero"])
 def test_scale_values(cuda, scale, mode):
