@@ -133,26 +133,40 @@ Route route_of(const FaBwdParams* p) {
 
 // Key ranges of the atomic dQ-from-dS kernel: at least 2, more while the grid
 // is below ~1024 workgroups and each range keeps >= 4 key steps.
-// query rows per workgroup of the dQ-from-dS kernel: 512 (8 waves sharing
-// each K tile) for the deterministic kernel at head dim 128 without a mask
-// when that still gives every CU a workgroup, else 256
-int dq_rows(const FaBwdParams* p) {
-  if (p->head_dim != 128 || p->mask || p->atomic_dq) return fa::kDqDsRows;
-  const int64_t wide = ds_slice_units(p) * (p->heads_q / p->heads_k) *
-                       ((p->seqlen_q + fa::kDqDsRowsWide - 1) / fa::kDqDsRowsWide);
-  return wide >= 256 ? fa::kDqDsRowsWide : fa::kDqDsRows;
+// Workgroups of one dQ-from-dS launch (one slice of units) at `rows` query
+// rows each, and the CU count they are measured against.
+int64_t dq_groups(const FaBwdParams* p, int rows) {
+  return ds_slice_units(p) * (p->heads_q / p->heads_k) * ((p->seqlen_q + rows - 1) / rows);
 }
+constexpr int64_t kCus = 256;
 
+// Atomic mode with the dS tiles: when the 256-row blocks alone give every CU
+// a workgroup, each workgroup owns its rows and writes dQ (split 1: no fp32
+// atomics, no zeroing, no conversion -- 20-70 % faster than adding partials);
+// below that, 2-8 key ranges per block are added with fp32 atomics, more
+// while the grid is below ~1024 workgroups and each range keeps >= 4 steps.
 int dq_split_of(const FaBwdParams* p) {
   if (route_of(p) != kDsAtomic) return 1;
-  // workgroups of one launch (one slice of units)
-  const int64_t nblk = ds_slice_units(p) * (p->heads_q / p->heads_k) *
-                       ((p->seqlen_q + dq_rows(p) - 1) / dq_rows(p));
+  const int64_t nblk = dq_groups(p, fa::kDqDsRows);
   const int nks = (p->seqlen_k + 31) / 32;
-  if (nks < 2) return 1;
+  if (nblk >= kCus || nks < 2) return 1;
   int split = 2;
   while (split < 8 && nblk * split < 1024 && nks / (2 * split) >= 4) split *= 2;
   return split;
+}
+
+// dQ accumulated with fp32 atomics into dq_accum (then converted)
+bool dq_atomics(const FaBwdParams* p) {
+  const Route r = route_of(p);
+  return r == kFusedAtomic || (r == kDsAtomic && dq_split_of(p) > 1);
+}
+
+// query rows per workgroup of the dQ-from-dS kernel: 512 (8 waves sharing
+// each K tile) when dQ is written directly at head dim 128 without a mask and
+// that still gives every CU a workgroup, else 256
+int dq_rows(const FaBwdParams* p) {
+  if (p->head_dim != 128 || p->mask || dq_atomics(p)) return fa::kDqDsRows;
+  return dq_groups(p, fa::kDqDsRowsWide) >= kCus ? fa::kDqDsRowsWide : fa::kDqDsRows;
 }
 
 int choose_split(const FaBwdParams* p) {
@@ -298,8 +312,8 @@ static int check_bwd(const FaBwdParams* p, int split) {
   if (!p->lse) return fail(FA_ERR_NULL, "lse is NULL");
   if (!p->delta) return fail(FA_ERR_NULL, "delta is NULL");
   if (!p->dead_flags) return fail(FA_ERR_NULL, "dead_flags is NULL");
-  if (p->atomic_dq && !p->dq_accum) return fail(FA_ERR_WORKSPACE, "atomic dQ needs dq_accum");
-  if (p->atomic_dq && !aligned16(p->dq_accum)) return fail(FA_ERR_STRIDE, "dq_accum must be 16-byte aligned");
+  if (dq_atomics(p) && !p->dq_accum) return fail(FA_ERR_WORKSPACE, "atomic dQ needs dq_accum (plan.needs_dq_accum)");
+  if (dq_atomics(p) && !aligned16(p->dq_accum)) return fail(FA_ERR_STRIDE, "dq_accum must be 16-byte aligned");
   const int G = p->heads_q / p->heads_k;
   if (split < 1 || G % split != 0) return fail(FA_ERR_SHAPE, "kv_split %d must divide the group size %d", split, G);
   if (split > 1 && (!p->dk_accum || !p->dv_accum))
@@ -322,8 +336,8 @@ int fa_bwd_plan(const FaBwdParams* p, FaBwdPlan* plan) {
   if (split < 1 || G % split != 0) return fail(FA_ERR_SHAPE, "kv_split %d must divide the group size %d", split, G);
   const Route r = route_of(p);
   plan->kv_split = split;
-  plan->needs_dq_accum = p->atomic_dq ? 1 : 0;
-  plan->dq_accum_elems = p->atomic_dq ? (int64_t)p->batch * p->seqlen_q * p->heads_q * p->head_dim : 0;
+  plan->needs_dq_accum = dq_atomics(p) ? 1 : 0;
+  plan->dq_accum_elems = dq_atomics(p) ? (int64_t)p->batch * p->seqlen_q * p->heads_q * p->head_dim : 0;
   // fused atomic kernel: one zeroed fp32 accumulator for dK and one for dV;
   // pipelined dK/dV kernel: one slab per split, fully overwritten.
   plan->dkv_accum_zeroed = split > 1 && r == kFusedAtomic ? 1 : 0;
@@ -341,7 +355,7 @@ int fa_bwd_preprocess(const FaBwdParams* p) {
   if (st) return st;
   fa::PreArgs a{};
   a.o = p->o; a.dout = p->dout; a.lse = p->lse; a.delta = p->delta; a.dead = p->dead_flags;
-  a.dq_accum = p->atomic_dq ? p->dq_accum : nullptr;
+  a.dq_accum = dq_atomics(p) ? p->dq_accum : nullptr;
   a.osb = p->o_stride_b; a.ost = p->o_stride_t; a.osh = p->o_stride_h;
   a.dsb = p->do_stride_b; a.dst = p->do_stride_t; a.dsh = p->do_stride_h;
   a.B = p->batch; a.Tq = p->seqlen_q; a.Hq = p->heads_q; a.Hk = p->heads_k; a.G = p->heads_q / p->heads_k;
@@ -366,13 +380,13 @@ static fa::BwdArgs bwd_args(const FaBwdParams* p, int split) {
   a.ssb = p->score_stride_b; a.ssh = p->score_stride_h; a.ssq = p->score_stride_q;
   a.B = p->batch; a.Tq = p->seqlen_q; a.Tk = p->seqlen_k; a.Hq = p->heads_q; a.Hk = p->heads_k;
   a.G = p->heads_q / p->heads_k;
-  const int kb = p->atomic_dq ? fa::dkdv_block_keys() : fa::dkdv2_block_keys();
+  const int kb = route_of(p) == kFusedAtomic ? fa::dkdv_block_keys() : fa::dkdv2_block_keys();
   a.nkt = (p->seqlen_k + kb - 1) / kb;
   a.nqt = (p->seqlen_q + fa::dq_block_rows() - 1) / fa::dq_block_rows();
   a.bk0 = 0;
   a.nbk = p->batch * p->heads_k;
   a.split = split;
-  a.do_dq = p->atomic_dq ? 1 : 0;
+  a.do_dq = dq_atomics(p) ? 1 : 0;
   a.dq_split = dq_split_of(p);
   a.scale = p->scale;
   float sl2f;
@@ -446,7 +460,7 @@ int fa_bwd_finalize(const FaBwdParams* p) {
       if ((st = launch_status(fa::launch_bwd_dq(a, p->head_dim, p->dtype, causal, s), "dq"))) return st;
     }
   }
-  if (p->atomic_dq) {
+  if (dq_atomics(p)) {
     // dq_accum is head-major [B, Hq, Tq, D]
     const int64_t D = p->head_dim, Tq = p->seqlen_q, Hq = p->heads_q;
     fa::CvtArgs c{p->dq_accum, p->dq, p->dq_stride_b, p->dq_stride_t, p->dq_stride_h,

@@ -156,7 +156,8 @@ def test_null_params(lib):
 
 
 BWD_ERRORS = [
-    (dict(dq_accum=None), 8, "needs dq_accum"),
+    (dict(dq_accum=None, ds_limit_bytes=-1), 8, "needs dq_accum"),   # fused atomic kernel
+    (dict(dq_accum=None, seqlen_q=1024, seqlen_k=1024, heads_q=16, heads_k=2), 8, "needs dq_accum"),
     (dict(kv_split=3), 2, "must divide"),
     (dict(kv_split=2), 8, "needs dk_accum"),
     (dict(dout=None), 1, "dout is NULL"),
@@ -184,9 +185,14 @@ def _plan(lib, **over):
 
 
 def test_plan_headline_needs_no_split(lib):
+    # atomic mode at the headline: 1024 dQ row blocks (>= one per CU) each
+    # own their rows, so no fp32 accumulator; the fused atomic kernel (no dS
+    # workspace) needs one
     plan = _plan(lib)
-    assert plan.kv_split == 1 and plan.needs_dq_accum == 1
-    assert plan.dq_accum_elems == 8192 * 32 * 128 and plan.dkv_accum_elems == 0
+    assert plan.kv_split == 1 and plan.needs_dq_accum == 0 and plan.dq_split == 1
+    assert plan.dq_accum_elems == 0 and plan.dkv_accum_elems == 0
+    plan = _plan(lib, ds_limit_bytes=-1)
+    assert plan.needs_dq_accum == 1 and plan.dq_accum_elems == 8192 * 32 * 128
     plan = _plan(lib, atomic_dq=0)
     assert plan.needs_dq_accum == 0 and plan.dq_accum_elems == 0
 
@@ -194,9 +200,15 @@ def test_plan_headline_needs_no_split(lib):
 def test_plan_ds_tiles(lib):
     # causal 8192 x 8192: 256 query steps x 256 key steps, lower triangle with
     # the diagonal = 256 * 257 / 2 tiles of 32 x 32 per head
-    # both modes hand dS over when it fits; the atomic one splits the key range
+    # both modes hand dS over when it fits; the atomic one splits the key
+    # range (fp32 atomics) only below one 256-row block per CU: 2 x 8 heads x
+    # 8 blocks = 128 -> 8 ranges (1024 workgroups)
     plan = _plan(lib)
-    assert plan.ds_elems == 32 * 256 * 256 * 1024 and plan.dq_split == 2
+    assert plan.ds_elems == 32 * 256 * 256 * 1024 and plan.dq_split == 1
+    small = dict(seqlen_q=2048, seqlen_k=2048, heads_q=16, heads_k=2)
+    plan = _plan(lib, **small)
+    assert plan.dq_split == 8 and plan.needs_dq_accum == 1 and plan.dq_accum_elems == 2048 * 16 * 128
+    assert _plan(lib, atomic_dq=0, **small).dq_split == 1
     assert _plan(lib, atomic_dq=0).dq_split == 1
     # ... and falls back to the fused atomic kernel when it does not
     plan = _plan(lib, ds_limit_bytes=-1)
@@ -239,7 +251,7 @@ def test_plan_mqa_splits_the_group(lib):
     for atomic in (0, 1):   # pipelined dK/dV kernel: one slab per split, no zeroing
         plan = _plan(lib, atomic_dq=atomic, **m)
         assert plan.kv_split == 4 and plan.dkv_accum_elems == 4 * 16384 * 64 and plan.dkv_accum_zeroed == 0
-    assert _plan(lib, **m).dq_split == 4   # 256 dQ workgroups -> 4 key ranges
+    assert _plan(lib, **m).dq_split == 1   # 256 dQ row blocks: one per CU, rows owned, no atomics
     # fused atomic kernel (no dS workspace): one zeroed accumulator
     plan = _plan(lib, ds_limit_bytes=-1, **m)
     assert plan.kv_split == 4 and plan.dkv_accum_elems == 16384 * 64 and plan.dkv_accum_zeroed == 1

@@ -162,8 +162,9 @@ def test_small_vs_oracle(cuda, cfg, mode):
 
 
 # Shapes with enough 512-row query blocks (B Hq ceil(Tq / 512) >= 256) that
-# the deterministic dQ kernel runs its 8-wave workgroups (head dim 128, no
-# mask); ragged Tq and Tk, causal with Tq != Tk, fp16
+# the dQ kernel runs its 8-wave workgroups (head dim 128, no mask), in atomic
+# mode too (row blocks enough for every CU: written directly, no atomics);
+# ragged Tq and Tk, causal with Tq != Tk, fp16
 WIDE_DQ = [
     C("wide_dq_ragged", 2, 1000, 900, 64, 8, 128),
     C("wide_dq_causal", 1, 700, 760, 128, 16, 128, is_causal=True),
@@ -171,7 +172,7 @@ WIDE_DQ = [
 ]
 
 
-@pytest.mark.parametrize("mode", ["det_ds"])
+@pytest.mark.parametrize("mode", ["det_ds", "atomic"])
 @pytest.mark.parametrize("cfg", WIDE_DQ, ids=[c.name for c in WIDE_DQ])
 def test_wide_dq_vs_oracle(cuda, cfg, mode):
     case = I.make_case(cfg, seed=5)
