@@ -129,7 +129,8 @@ typedef struct FaMaskParams {
 /* What fa_bwd will do for a problem, so the caller can size workspaces. */
 typedef struct FaBwdPlan {
   int32_t kv_split;              /* >1: dK/dV accumulate in fp32 dk_accum/dv_accum (zeroed) */
-  int32_t needs_dq_accum;        /* 1 if dq_accum is used */
+  int32_t needs_dq_accum;        /* 1 if dq_accum is used: dQ added with fp32 atomics (atomic_dq = 1 and
+                                    dq_split > 1, or the fused kernel); else dQ is written directly */
   int64_t dq_accum_elems;        /* B*Tq*Hq*D when used, else 0 */
   int64_t dkv_accum_elems;       /* B*Tk*Hk*D when kv_split > 1, else 0 */
   int64_t ds_elems;              /* size of ds_tiles (16-bit dS of every stored 32x32 block of a slice of
@@ -139,7 +140,9 @@ typedef struct FaBwdPlan {
                                     (atomic_dq = 0) or added per key block by the fused dK/dV kernel
                                     (atomic_dq = 1) */
   int32_t dkv_accum_zeroed;      /* 1: dk_accum/dv_accum must be zeroed by the caller (fused atomic kernel) */
-  int32_t dq_split;              /* atomic_dq = 1 with dS tiles: key ranges whose dQ partials are added */
+  int32_t dq_split;              /* atomic_dq = 1 with dS tiles: key ranges whose dQ partials are added
+                                    (2-8) when the 256-row query blocks are fewer than the CUs; 1: each
+                                    block writes its rows, no atomics (as atomic_dq = 0) */
 } FaBwdPlan;
 
 /* Size in bytes of the prepared-mask workspace for *p (no launch, no GPU access). */
@@ -178,8 +181,9 @@ int fa_bwd_preprocess(const FaBwdParams* p);
 int fa_bwd(const FaBwdParams* p);
 
 /* Backward finalisation.  dQ: from ds_tiles, dQ = scale dS K, written in dtype
- * (atomic_dq = 0) or added as fp32 partials over plan.dq_split key ranges into
- * dq_accum with atomics and converted (atomic_dq = 1); without ds_tiles,
+ * (atomic_dq = 0, or plan.dq_split = 1) or added as fp32 partials over
+ * plan.dq_split key ranges into dq_accum with atomics and converted (atomic_dq = 1,
+ * plan.dq_split > 1); without ds_tiles,
  * recomputed from S, P and dP (atomic_dq = 0) or converted from the dq_accum the
  * fused kernel filled (atomic_dq = 1).  dk, dv from dk_accum/dv_accum when
  * kv_split > 1.  Replaces the casts of python/fa2.py:535-536, the group sum of
