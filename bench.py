@@ -18,7 +18,8 @@ by ``fa_bwd`` on the deterministic path: 4 GEMMs (S, dP, dV, dK), i.e.
 8*B*Hq*Tq*Tk*D algorithmic FLOPs per launch, timed with HIP events on the
 launch stream inside the timed region.  ``traffic`` (HBM bytes per launch) is
 read from profiles/traffic_H_S.json, written from rocprofv3 FETCH_SIZE /
-WRITE_SIZE runs scaled by a copy-kernel calibration.  ``cpu_baseline`` times
+WRITE_SIZE runs of ``bench.py --traffic-pass`` scaled by a copy-kernel
+calibration.  ``cpu_baseline`` times
 this repository's eager fp32 oracle on the host cores on a bounded sample.
 
 The other BASELINE configs (P: packed-document mask, S: score + sparse mask,
@@ -180,6 +181,32 @@ def cpu_baseline(seconds: float) -> dict:
     }
 
 
+def traffic_pass(torch, api, dev) -> int:
+    """One untimed launch of each kernel whose HBM traffic is reported, after a
+    1 GiB copy whose counter reading calibrates the counters."""
+    x = torch.empty(2 ** 28, dtype=torch.float32, device=dev)
+    y = torch.empty_like(x)
+    y.copy_(x)
+    torch.cuda.synchronize()
+    del x, y
+    q0, k0, v0, do = make_inputs(torch, dev)
+    q, k, v = (t.detach().requires_grad_(True) for t in (q0, k0, v0))
+    with torch.no_grad():
+        api.tilelang_flash_attention(q0, k0, v0)
+    api.tilelang_flash_attention(q, k, v, use_atomic_backward=False).backward(do)
+    torch.cuda.synchronize()
+    del q, k, v, q0, k0, v0, do
+    for n, c in side_configs(torch, dev):
+        if n == "S":
+            with torch.no_grad():
+                api.tilelang_flash_attention(c["q"], c["k"], c["v"], mask=c["mask"], score=c["score"],
+                                             layout=c["layout"])
+            break
+    torch.cuda.synchronize()
+    log("traffic pass done")
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -189,6 +216,9 @@ def main() -> int:
     ap.add_argument("--no-side-configs", action="store_true",
                     help="skip the P / S / M config lines (mask, score+mask, MQA)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--traffic-pass", action="store_true",
+                    help="run once, untimed, what the rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes count: "
+                         "a 1 GiB fp32 copy (calibration), an H forward, an H deterministic fwd+bwd, an S forward")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}): this build has no multi-GPU "
@@ -204,6 +234,8 @@ def main() -> int:
         log("no GPU visible")
         return 1
     dev = torch.device("cuda:0")
+    if args.traffic_pass:
+        return traffic_pass(torch, api, dev)
     q0, k0, v0, do = make_inputs(torch, dev)
     q = q0.detach().requires_grad_(True)
     k = k0.detach().requires_grad_(True)
