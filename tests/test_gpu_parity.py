@@ -258,7 +258,7 @@ def test_bhsd_contiguous_inputs(cuda):
     check(ours, run_oracle_cpu(case, cfg), label="bhsd-contiguous")
 
 
-@pytest.mark.parametrize("mode", ["atomic", "det_ds"])
+@pytest.mark.parametrize("mode", ["atomic", "det_ds", "atomic_fused", "det_recompute"])
 def test_tiny_lengths(cuda, mode):
     # Boundary/indexing test (an indexing bug gives O(1) errors).  With a few
     # hundred entries per output the mean is dominated by single bf16 rounding
@@ -266,8 +266,11 @@ def test_tiny_lengths(cuda, mode):
     # dK entry sums 70 terms of bf16-rounded dS (rounded as in the reference
     # kernel, python/fa2.py:291-292) that are larger than the result, so the
     # per-entry bar is 4e-2 + 2^-5 |ref|.
-    for (tq, tk, causal) in [(1, 1, False), (1, 7, False), (5, 1, True), (3, 65, True), (70, 3, False)]:
-        cfg = C("tiny", 1, tq, tk, 2, 1, 64, is_causal=causal)
+    shapes = [(1, 1, False, 64, None), (1, 7, False, 64, None), (5, 1, True, 64, None), (3, 65, True, 64, None),
+              (70, 3, False, 64, None), (1, 40, False, 128, "bernoulli"), (33, 2, True, 128, "bernoulli"),
+              (2, 300, False, 128, None)]
+    for (tq, tk, causal, d, mask) in shapes:
+        cfg = C("tiny", 1, tq, tk, 2, 1, d, is_causal=causal, mask=mask, keep_prob=0.9)
         case = I.make_case(cfg, seed=6)
         atomic, ds_limit = MODES[mode]
         check(run_ours(case, cfg, atomic=atomic, ds_limit=ds_limit), run_oracle_cpu(case, cfg),
