@@ -18,18 +18,20 @@
 // that tile yields the B operand of dQ^T = K^T dS^T with lane l = position p
 // directly, so perm only matters when dQ rows are stored.
 //
-// Work decomposition: one workgroup of 4 waves per (256 query rows, head,
-// batch[, key split]); wave w owns query steps 8 qb + 2 w, + 1 (64 rows) and
-// walks the key steps of 32.  Deterministic: one workgroup covers every key
-// step and stores dQ.  Atomic (use_atomic_backward): the key steps are cut
-// into dq_split contiguous ranges and each workgroup adds its fp32 partial
-// dQ into the zeroed accumulator with fp32 atomics, one coalesced row segment
-// per instruction (the reference adds a partial per 64-key block,
-// python/fa2.py:295-297, which on this part is bound by atomic throughput).  Per step the workgroup stages one K tile (shared, XOR-swizzled
-// for the transpose reads) and each wave its two dS tiles (private) through
-// registers into LDS, kSets steps ahead of use; the kernel is bound by the
-// HBM reads of the dS tiles, so it keeps as many bytes in flight as registers
-// allow at two workgroups per CU.
+// Work decomposition: one workgroup of NW (4 or 8) waves per (64 NW query
+// rows, head, batch[, key split]); wave w owns query steps 2 NW qb + 2 w, + 1
+// (64 rows) and walks the key steps of 32.  Written dQ (deterministic mode,
+// and atomic mode when the row blocks give every CU a workgroup): one
+// workgroup covers every key step and stores dQ.  Atomic (use_atomic_backward
+// on smaller grids): the key steps are cut into dq_split contiguous ranges
+// and each workgroup adds its fp32 partial dQ into the zeroed accumulator
+// with fp32 atomics, one coalesced row segment per instruction (the reference
+// adds a partial per 64-key block, python/fa2.py:295-297, which on this part
+// is bound by atomic throughput).  Per step the workgroup stages one K tile
+// (shared, XOR-swizzled for the transpose reads) and each wave its two dS
+// tiles (private) through registers into LDS, kSets steps ahead of use; the
+// kernel is bound by the HBM reads of the dS tiles, so it keeps as many bytes
+// in flight as registers allow at two waves per SIMD.
 #include "fa_common.h"
 #include "fa_kernels.h"
 #include "fa_pipe.h"
