@@ -14,10 +14,12 @@ What differs on purpose:
 * Mask/Score may be broadcast views ([B|1, Hq|1, Tq, Tk] with stride 0);
 * dQ/dK/dV come back in the input dtype directly (the reference returns fp32
   dQ and lets autograd cast it, python/fa2.py:527,556);
-* dQ goes through dS tiles the dK/dV kernel stores: ``use_atomic_backward``
-  (default) adds fp32 partials over a few key ranges atomically, ``False``
-  writes dQ in one deterministic pass (the reference adds a partial per
-  64-key block atomically in both modes, python/fa2.py:295-297, 420-421);
+* dQ goes through dS tiles the dK/dV kernel stores: ``False`` writes dQ in
+  one deterministic pass; ``use_atomic_backward`` (default) does the same
+  when the 256-row query blocks give every CU a workgroup, and on smaller
+  grids adds fp32 partials over a few key ranges atomically (the reference
+  adds a partial per 64-key block atomically in both modes,
+  python/fa2.py:295-297, 420-421);
 * a mask is prepared once per call (``fa_mask_prepare``: bits, block states,
   live-tile lists) and the workspace is kept for the backward, so the kernels
   skip tiles without a kept entry (the reference streams every tile's mask
