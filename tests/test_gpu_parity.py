@@ -278,6 +278,30 @@ def test_tiny_lengths(cuda, mode):
               mean_rel=2.0 ** -7, abs_bar=4e-2, rel_bar=2.0 ** -5)
 
 
+def test_atomic_mode_on_a_full_grid_writes_dq_once(cuda):
+    """Atomic mode where the 256-row query blocks give every CU a workgroup:
+    dQ is written per block (no atomics), so it is bitwise repeatable and
+    equal to the deterministic mode's (the same kernel and row blocks)."""
+    import ctypes
+
+    from tilelang_fa2_4d_mask import _ext
+
+    cfg = WIDE_DQ[0]
+    lib = _ext.load_library()
+    p = _ext.FaBwdParams()
+    p.batch, p.seqlen_q, p.seqlen_k, p.heads_q, p.heads_k, p.head_dim = cfg.B, cfg.Tq, cfg.Tk, cfg.Hq, cfg.Hk, cfg.D
+    p.scale, p.atomic_dq = cfg.D ** -0.5, 1
+    plan = _ext.FaBwdPlan()
+    assert lib.fa_bwd_plan(ctypes.byref(p), ctypes.byref(plan)) == 0
+    assert plan.dq_split == 1 and plan.needs_dq_accum == 0
+    case = I.make_case(cfg, seed=8)
+    a = run_ours(case, cfg, atomic=True)
+    b = run_ours(case, cfg, atomic=True)
+    c = run_ours(case, cfg, atomic=False)
+    for n in a:
+        assert torch.equal(a[n], b[n]) and torch.equal(a[n], c[n]), n
+
+
 @pytest.mark.parametrize("ds_limit", [0, -1], ids=["det_ds", "det_recompute"])
 def test_deterministic_path_is_bitwise_repeatable(cuda, ds_limit):
     cfg = C("det", 1, 512, 512, 8, 2, 128, is_causal=True, mask="bernoulli")
