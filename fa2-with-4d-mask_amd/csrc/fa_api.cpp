@@ -189,6 +189,12 @@ int choose_split(const FaBwdParams* p) {
   return split;
 }
 
+// The delta workspace holds Delta [B, Hq, Tq], then the LSE the backward
+// kernels read (written by the preprocess).
+float* lse_b_of(const FaBwdParams* p) {
+  return p->delta + (int64_t)p->batch * p->heads_q * p->seqlen_q;
+}
+
 void fill_scales(float scale, float* scale_log2_fwd, float* qsign, int* zero, float* scale_log2_bwd) {
   *zero = scale == 0.f;
   *qsign = scale < 0.f ? -1.f : 1.f;
@@ -354,18 +360,25 @@ int fa_bwd_preprocess(const FaBwdParams* p) {
   int st = check_bwd(p, split);
   if (st) return st;
   fa::PreArgs a{};
-  a.o = p->o; a.dout = p->dout; a.lse = p->lse; a.delta = p->delta; a.dead = p->dead_flags;
+  a.o = p->o; a.dout = p->dout; a.lse = p->lse; a.dead = p->dead_flags;
+  a.delta = p->delta;
+  a.lse_b = lse_b_of(p);
   a.dq_accum = dq_atomics(p) ? p->dq_accum : nullptr;
   a.osb = p->o_stride_b; a.ost = p->o_stride_t; a.osh = p->o_stride_h;
   a.dsb = p->do_stride_b; a.dst = p->do_stride_t; a.dsh = p->do_stride_h;
   a.B = p->batch; a.Tq = p->seqlen_q; a.Hq = p->heads_q; a.Hk = p->heads_k; a.G = p->heads_q / p->heads_k;
+  a.is_causal = p->is_causal != 0;
+  if (p->mask) {
+    a.mws = (const char*)p->mask_ws;
+    a.ml = layout_of(p->batch, p->heads_q, p->seqlen_q, p->seqlen_k, p->mask_stride_b, p->mask_stride_h);
+  }
   return launch_status(fa::launch_preprocess(a, p->head_dim, p->dtype, (hipStream_t)p->stream), "fa_bwd_preprocess");
 }
 
 static fa::BwdArgs bwd_args(const FaBwdParams* p, int split) {
   fa::BwdArgs a{};
   a.q = p->q; a.k = p->k; a.v = p->v; a.dout = p->dout;
-  a.lse = p->lse; a.delta = p->delta; a.dead = p->dead_flags;
+  a.lse = lse_b_of(p); a.delta = p->delta; a.dead = p->dead_flags;
   a.mask = p->mask; a.score = p->score;
   a.dq_accum = p->dq_accum; a.dk_accum = p->dk_accum; a.dv_accum = p->dv_accum;
   a.dk = p->dk; a.dv = p->dv; a.dq = p->dq;

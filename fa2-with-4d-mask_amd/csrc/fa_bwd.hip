@@ -39,8 +39,25 @@ template <typename T>
 __device__ __forceinline__ float to_f(T x) { return (float)x; }
 
 // ---------------------------------------------------------------------------
-// preprocess: Delta, dead-row flags, zeroed dQ accumulator rows
+// preprocess: Delta, the backward's LSE, dead-row flags, zeroed dQ accumulator
+// rows
 // ---------------------------------------------------------------------------
+// Whether query row q of (b, h) keeps at least one key: j < Tk, j <= q when
+// causal, and the mask bit (the prepared bits are zero past Tk).  Only asked
+// for rows whose LSE is +inf, so a serial scan of the row's words is fine.
+__device__ bool row_keeps_a_key(const PreArgs& a, int b, int h, int q) {
+  if (!a.mws) return true;   // no mask: key 0 is kept (j <= q holds for j = 0)
+  const int pm = mask_plane(a.ml, b, h);
+  const uint32_t* w = (const uint32_t*)(a.mws + a.ml.bits + pm * a.ml.pbits) + (int64_t)q * a.ml.wk;
+  const int nw = a.is_causal ? min(q / 32 + 1, a.ml.nk32) : a.ml.nk32;
+  for (int i = 0; i < nw; ++i) {
+    uint32_t x = w[i];
+    if (a.is_causal && i == q / 32 && (q & 31) != 31) x &= (2u << (q & 31)) - 1u;
+    if (x) return true;
+  }
+  return false;
+}
+
 template <typename T, int D>
 __global__ __launch_bounds__(256) void preprocess_kernel(const PreArgs a) {
   constexpr int CH = D / 8;            // 16-byte chunks per row
@@ -71,8 +88,17 @@ __global__ __launch_bounds__(256) void preprocess_kernel(const PreArgs a) {
     }
     if (part == 0) {
       const int64_t ri = ((int64_t)b * a.Hq + h) * a.Tq + q;
-      const bool dead = a.lse[ri] == kPosInf;
+      // LSE = +inf: every kept logit of the row is -inf.  Either the row
+      // keeps no key (eager: dQ row 0, masked_fill's backward) or its kept
+      // keys all carry a -inf score (eager: the softmax row is NaN, and so
+      // are the dQ row and the dK rows of those keys).  The backward kernels
+      // take P = exp2(s c - LSE_b) and select dropped entries to 0: LSE_b =
+      // +inf gives P = 0 everywhere, LSE_b = -inf gives NaN on exactly the
+      // kept entries (s = -inf there).  dV of the kv-head is NaN either way.
+      const float lse = a.lse[ri];
+      const bool dead = lse == kPosInf;
       a.delta[ri] = dead ? 0.f : acc;
+      a.lse_b[ri] = dead ? (row_keeps_a_key(a, b, h, q) ? kNegInf : kPosInf) : lse;
       if (dead) a.dead[b * a.Hk + h / a.G] = 1;
     }
   }

@@ -97,9 +97,15 @@ struct FwdArgs {
 
 struct PreArgs {
   const void* o; const void* dout; const float* lse;
-  float* delta; int32_t* dead; float* dq_accum;
+  float* delta;         // Delta [B, Hq, Tq]
+  float* lse_b;         // LSE the backward kernels use [B, Hq, Tq]: the forward's, except
+                        // -inf for a row whose kept keys all have -inf logits
+  int32_t* dead; float* dq_accum;
   int64_t osb, ost, osh, dsb, dst, dsh;
   int B, Tq, Hq, Hk, G;
+  int is_causal;
+  const char* mws;      // prepared mask (with a mask): tells rows without a kept key
+  MaskLayout ml;
 };
 
 struct BwdArgs {

@@ -74,7 +74,10 @@ def _kernel_side(x: Optional[torch.Tensor], dtype: Optional[torch.dtype], B: int
     if x.device != device:
         raise ValueError(f"{name} must be on {device}, got {x.device}")
     if dtype is not None and x.dtype != dtype:
-        x = x.to(dtype)
+        # convert the stored entries only: broadcast (stride-0) dimensions stay
+        # broadcast, so the kernels and the workspaces see one plane for them
+        base = x[tuple(slice(0, 1) if (x.stride(d) == 0 and x.shape[d] > 1) else slice(None) for d in range(4))]
+        x = base.to(dtype).expand(x.shape)
     if tuple(x.shape[-2:]) != (Tq, Tk) or x.shape[0] not in (1, B) or x.shape[1] not in (1, Hq):
         raise ValueError(f"{name} has shape {tuple(x.shape)}, expected [{B} or 1, {Hq} or 1, {Tq}, {Tk}]")
     if x.stride(3) != 1 and Tk > 1:
@@ -231,7 +234,7 @@ def _backward_impl(do, q, k, v, O, LSE, mask, score, mask_ws, mst, sst, scale: f
     _ext.check(lib.fa_bwd_plan(ctypes.byref(p), ctypes.byref(plan)), "fa_bwd_plan", lib)
     p.kv_split = plan.kv_split
 
-    delta = torch.empty((B, Hq, Tq), dtype=torch.float32, device=dev)
+    delta = torch.empty((2, B, Hq, Tq), dtype=torch.float32, device=dev)   # Delta, backward LSE
     dead = torch.zeros((B * Hk,), dtype=torch.int32, device=dev)
     dq_acc = torch.empty((B, Tq, Hq, D), dtype=torch.float32, device=dev) if plan.needs_dq_accum else None
     dk_acc = dv_acc = None

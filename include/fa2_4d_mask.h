@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define FA_ABI_VERSION 3
+#define FA_ABI_VERSION 4
 
 enum FaDtype { FA_DTYPE_BF16 = 0, FA_DTYPE_FP16 = 1 };
 
@@ -81,7 +81,9 @@ typedef struct FaBwdParams {
   const void* o;                 /* forward output */
   const void* dout;              /* gradient of O, [B, Tq, Hq, D] by strides */
   const float* lse;              /* [B, Hq, Tq] from fa_fwd */
-  float* delta;                  /* workspace [B, Hq, Tq] fp32 (written by fa_bwd_preprocess) */
+  float* delta;                  /* workspace [2, B, Hq, Tq] fp32, written by fa_bwd_preprocess: Delta, then
+                                    the LSE the backward kernels read (the forward's, except -inf for a
+                                    row whose kept keys all have a -inf logit) */
   int32_t* dead_flags;           /* workspace [B * Hk] int32, zeroed by the caller */
   const uint8_t* mask; const float* score;
   float* dq_accum;               /* workspace [B, Hq, Tq, D] fp32 contiguous, head-major (atomic dQ) */
@@ -162,8 +164,12 @@ int fa_fwd(const FaFwdParams* p);
 
 /* Backward preprocess.  Replaces `bwd_preprocess` (python/fa2.py:142-179, launched at
  * python/fa2.py:509-513): delta[b,h,i] = sum_d O*dO in fp32; additionally zeroes the
- * dq_accum rows (when the plan uses it), zeroes delta and raises dead_flags[b*Hk+kvh]
- * for rows whose LSE is +inf (no kept key). */
+ * dq_accum rows (when the plan uses it), and for rows whose LSE is +inf (every kept
+ * logit -inf) zeroes delta and raises dead_flags[b*Hk+kvh].  Such a row gets the
+ * eager reference's gradients (benchmark/precision_check.py:158-174 under autograd):
+ * with no kept key (mask, causality) a zero dQ row; with kept keys whose logits are
+ * all -inf (a -inf score) a NaN dQ row and NaN dK rows at those keys; dV of the
+ * kv-head NaN in both cases. */
 int fa_bwd_preprocess(const FaBwdParams* p);
 
 /* Backward main pass.  Replaces `flash_attention_bwd_with_4d_mask_atomic`

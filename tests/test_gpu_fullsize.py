@@ -123,3 +123,70 @@ def test_fullsize_layouts_agree(cuda):
     b = run_ours(case2, cfg2, atomic=False)
     for n in a:
         assert torch.equal(a[n], b[n]), n
+
+
+# ---------------------------------------------------------------------------
+# The reference's scripted regression (precision_check.sh: B1 Tq=Tk=8191 Hq32
+# Hk8 D128 bf16, cases no_causal / causal / random_mask, --check-backward):
+# a length that is not a multiple of any tile, at the headline heads.  The
+# random_mask case is precision_check.py:110-117's per-head Bernoulli mask
+# (keep 0.75, key min(i, Tk-1) forced) -- [1, 32, 8191, 8191], drawn on the
+# device with a seeded generator (2 GiB; the same tensor goes to the oracle).
+# It runs the prepared-mask paths that small shapes never reach: per-head
+# lists of more than 128 steps (dK/dV list cursor across heads, dQ positions
+# past 128).
+# ---------------------------------------------------------------------------
+def _device_case(cfg, seed, dev, mask_heads=None):
+    """Seeded inputs drawn on the device (the CPU would need 8 GiB of floats
+    for a full-head mask of this size)."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+
+    def rnd(shape):
+        return torch.randn(shape, generator=g, device=dev, dtype=torch.float32).to(cfg.dtype)
+
+    q = rnd((cfg.B, cfg.Tq, cfg.Hq, cfg.D))
+    k = rnd((cfg.B, cfg.Tk, cfg.Hk, cfg.D))
+    v = rnd((cfg.B, cfg.Tk, cfg.Hk, cfg.D))
+    mask = None
+    if cfg.mask == "bernoulli":
+        mh = mask_heads or cfg.Hq
+        mask = torch.rand((cfg.B, mh, cfg.Tq, cfg.Tk), generator=g, device=dev) < cfg.keep_prob
+        qi = torch.arange(cfg.Tq, device=dev)
+        mask[:, :, qi, torch.clamp(qi, max=cfg.Tk - 1)] = True
+    grad = rnd((cfg.B, cfg.Tq, cfg.Hq, cfg.D))
+    case = {"q_bhsd": q.transpose(1, 2), "k_bhsd": k.transpose(1, 2), "v_bhsd": v.transpose(1, 2),
+            "grad_bhsd": grad.transpose(1, 2), "mask": mask, "score": None}
+    case.update(q=case["q_bhsd"], k=case["k_bhsd"], v=case["v_bhsd"], grad=case["grad_bhsd"])
+    return case
+
+
+REGRESSION = {
+    "no_causal": I.AttnConfig("R_no_causal", 1, 8191, 8191, 32, 8, 128),
+    "causal": I.AttnConfig("R_causal", 1, 8191, 8191, 32, 8, 128, is_causal=True),
+    "random_mask": I.AttnConfig("R_random_mask", 1, 8191, 8191, 32, 8, 128, mask="bernoulli", keep_prob=0.75),
+}
+REG_CASES = [(n, a) for n in REGRESSION for a in (True, False)]
+
+
+@pytest.mark.parametrize("name,atomic", REG_CASES, ids=[f"{n}-{'atomic' if a else 'det'}" for n, a in REG_CASES])
+def test_reference_regression_T8191(cuda, name, atomic):
+    cfg = REGRESSION[name]
+    print(f"case precision_check.sh {name} atomic={atomic} B1 T8191 Hq32 Hk8 D128", flush=True)
+    case = _device_case(cfg, seed=0, dev=cuda)
+    ours = run_ours(case, cfg, atomic=atomic)
+    ref = run_oracle(case, cfg)
+    check(ours, ref, f"T8191/{name}/{'atomic' if atomic else 'det'}")
+
+
+def test_long_keys_head_broadcast_mask(cuda):
+    """Tk 16384 with a head-broadcast mask: the forward's list of live 64-key
+    tiles runs to 256 positions (entries past 128 come from memory, not the
+    list registers); both backward modes."""
+    cfg = I.AttnConfig("long_keys_mask", 1, 2048, 16384, 8, 2, 128, mask="bernoulli", keep_prob=0.75)
+    case = _device_case(cfg, seed=3, dev=cuda, mask_heads=1)
+    for atomic in (True, False):
+        print(f"case long_keys_mask atomic={atomic} B1 Tq2048 Tk16384 Hq8 Hk2 D128, mask [1,1,T,T]", flush=True)
+        ours = run_ours(case, cfg, atomic=atomic)
+        ref = run_oracle(case, cfg)
+        check(ours, ref, f"long_keys_mask/{'atomic' if atomic else 'det'}")

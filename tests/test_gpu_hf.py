@@ -124,3 +124,57 @@ def test_llama_with_fa2_attention(cuda, style, padding):
     (h.float()[keep_tok.to(cuda)] ** 2).mean().backward()
     for n, p in ours.named_parameters():
         assert p.grad is not None and torch.isfinite(p.grad).all(), n
+
+
+@pytest.mark.parametrize("atomic", [True, False], ids=["atomic", "det"])
+def test_eager_style_padding_backward(cuda, atomic):
+    """One attention layer's forward and backward under transformers' eager-style
+    mask with left padding: causal + padding as an additive bf16 mask (0 or
+    finfo(bf16).min), [B, 1, T, T], through ``tilelang_attention_forward``.  The
+    adapter divides it by ``scaling`` (attention_mask_is_scaled), which overflows
+    to -inf in fp32 (python/modeling_attention.py:129-133), so the padding query
+    rows have every logit -inf: eager autograd gives them a NaN output row and a
+    NaN dQ row, NaN dK and dV for every key of their kv-heads (no key is dropped
+    by a bool mask or by causality here, the mask being additive).  Checked
+    against the oracle (autograd through the eager graph, fp32, CPU) with NaN
+    positions compared exactly."""
+    import tilelang_fa2_4d_mask as api
+    from oracle import eager as E
+
+    B, H, Hk, T, D = 2, 4, 2, 96, 64
+    pad = 7
+    g = torch.Generator().manual_seed(3)
+    q = torch.randn((B, H, T, D), generator=g).to(torch.bfloat16)
+    k = torch.randn((B, Hk, T, D), generator=g).to(torch.bfloat16)
+    v = torch.randn((B, Hk, T, D), generator=g).to(torch.bfloat16)
+    do = torch.randn((B, H, T, D), generator=g).to(torch.bfloat16)
+    keep = torch.ones((B, 1, T, T), dtype=torch.bool).tril()
+    keep[1, :, :, :pad] = False                    # left padding of sequence 1 (keys)
+    am = torch.zeros((B, 1, T, T), dtype=torch.bfloat16).masked_fill(~keep, torch.finfo(torch.bfloat16).min)
+    scaling = D ** -0.5
+    assert torch.isinf(am.float() / scaling).any()   # the overflow this case is about
+
+    class _Attn(torch.nn.Module):
+        is_causal = True
+
+    qd, kd, vd = (t.to(cuda).requires_grad_(True) for t in (q, k, v))
+    print(f"case eager-style padding backward atomic={atomic}", flush=True)
+    out, w = api.tilelang_attention_forward(_Attn(), qd, kd, vd, am.to(cuda), scaling, use_atomic_backward=atomic)
+    out.backward(do.to(cuda))
+    torch.cuda.synchronize()
+    ours = {"out": out.detach().float().cpu(), "dq": qd.grad.float().cpu(), "dk": kd.grad.float().cpu(),
+            "dv": vd.grad.float().cpu()}
+    o, dq, dk, dv = E.eager_fwd_bwd(q, k, v, None, am.float() / scaling, do, scale=scaling, is_causal=False)
+    ref = {"out": o.float(), "dq": dq.float(), "dk": dk.float(), "dv": dv.float()}
+    assert torch.isnan(ref["dq"][1, :, :pad]).all() and torch.isnan(ref["dk"][1]).all()
+    for name in ref:
+        st = E.finite_diff_stats(ours[name], ref[name])
+        r = ref[name]
+        fin = torch.isfinite(r)
+        print(f"  {name}: max_abs={st['max_abs']:.3e} mean_abs={st['mean_abs']:.3e} nan_match={st['nan_match']}",
+              flush=True)
+        assert st["nan_match"], name
+        if fin.any():
+            err = (ours[name][fin] - r[fin]).abs()
+            assert (err <= 2e-2 + 2.0 ** -6 * r[fin].abs()).all(), name
+            assert err.mean().item() <= max(1e-4, 2.0 ** -8 * r[fin].abs().mean().item()), name

@@ -138,6 +138,10 @@ SMALL = [
       extra={"packed": {"lo": 40, "hi": 160}}),
     C("alibi_sparse", 1, 256, 256, 4, 4, 128, mask="sparse_diag", mask_heads=4, score="alibi_noise"),
     C("fp16_mask_score_d64", 1, 200, 200, 4, 2, 64, torch.float16, mask="bernoulli", score="normal"),
+    # BASELINE configs[0] (C) at its shape, B1 Hq4 Hk2 T256 D64 causal, in the
+    # GPU dtypes (its fp32 form is the CPU oracle's own plumbing case)
+    C("C_shape_bf16", 1, 256, 256, 4, 2, 64, is_causal=True),
+    C("C_shape_fp16", 1, 256, 256, 4, 2, 64, torch.float16, is_causal=True),
 ]
 
 
@@ -214,6 +218,51 @@ def test_dead_rows_policy(cuda):
         assert torch.isnan(ours["dv"][0, 0]).all() and torch.isnan(ours["dv"][1, 1]).all()
         assert torch.isfinite(ours["dv"][0, 1]).all() and torch.isfinite(ours["dv"][1, 0]).all()
         assert torch.isfinite(ours["dk"]).all()
+
+
+SCORE_DEAD = [
+    C("score_dead_mask", 2, 256, 256, 4, 2, 64, mask="bernoulli", score="normal"),
+    C("score_dead_mask_causal", 1, 320, 320, 4, 2, 128, is_causal=True, mask="bernoulli", score="normal"),
+    C("score_dead_nomask", 2, 256, 200, 4, 2, 128, score="normal"),
+    C("score_dead_nomask_causal", 1, 300, 300, 4, 1, 64, is_causal=True, score="normal"),
+]
+
+
+@pytest.mark.parametrize("cfg", SCORE_DEAD, ids=[c.name for c in SCORE_DEAD])
+def test_dead_rows_from_scores(cuda, cfg):
+    """Rows whose kept logits are all -inf because of the score (HF's float
+    padding masks reach this: finfo.min / scale overflows to -inf) follow eager
+    autograd: O row NaN, dQ row NaN, dK NaN at exactly the keys the row keeps
+    (mask and causality), dV of the kv-head NaN; rows with no kept key at all
+    keep dQ = 0.  Every backward mode, against the CPU oracle (autograd through
+    the eager graph), NaN positions compared exactly."""
+    case = I.make_case(cfg, seed=11)
+    s = case["score"].clone()
+    s[0, 1, 17, :] = float("-inf")                # b0 h1 (kv-head 0): every key -inf
+    s[cfg.B - 1, 3, 100, : cfg.Tk // 3] = float("-inf")   # partly -inf: an ordinary row
+    if cfg.mask is not None:
+        m = case["mask"].clone()
+        m[0, 0, 30, :] = False
+        m[0, 0, 30, 3:12] = True                  # b0 h0 keeps keys 3..11 only ...
+        s[0, 0, 30, 3:12] = float("-inf")         # ... whose scores are -inf
+        m[cfg.B - 1, 2, 40, :] = False            # a row with no kept key: dQ row 0
+        case["mask"] = m
+    if cfg.is_causal:
+        s[0, 2, 5, :] = float("-inf")             # causal row 5 keeps keys 0..5
+    case["score"] = s
+    for mode, (atomic, ds_limit) in MODES.items():
+        print(f"case {cfg.name} mode={mode}", flush=True)
+        ours = run_ours(case, cfg, atomic=atomic, ds_limit=ds_limit)
+        ref = run_oracle_cpu(case, cfg)
+        assert torch.isnan(ref["dq"][0, 1, 17]).all() and torch.isnan(ref["out"][0, 1, 17]).all()
+        check(ours, ref, label=f"{cfg.name}/{mode}")
+        assert torch.isnan(ours["dq"][0, 1, 17]).all()
+        if cfg.mask is not None:
+            dk_nan = torch.isnan(ours["dk"][0, 0]).any(-1)
+            assert dk_nan[3:12].all() and torch.isnan(ours["dq"][0, 0, 30]).all()
+            assert (ours["dq"][cfg.B - 1, 2, 40] == 0).all()
+        elif not cfg.is_causal:
+            assert torch.isnan(ours["dk"][0, 0]).all()   # every key is kept by row 17
 
 
 def test_leading_masked_tiles_are_not_nan(cuda):
