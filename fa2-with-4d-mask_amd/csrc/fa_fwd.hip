@@ -43,6 +43,12 @@
 // m_run is still -inf does the slow path compute the tile maximum, rescale
 // O and l, and redo P.  That is exact (O and l always share one reference)
 // and removes the max reduction and the rescale from almost every tile.
+// m_run is the maximum of the row's first tile holding a kept key, m0, and
+// afterwards moves only in whole steps (m0 + k, the tile maximum rounded up
+// to that grid): the 16-bit P that enters the PV product is then
+// round(2^frac(s c - m0)) times a power of two whichever m0 + k was current
+// -- the same values as against the row's final maximum taken to that grid
+// (the rescale factors are powers of two, so they add no rounding either).
 #include "fa_common.h"
 #include "fa_kernels.h"
 
@@ -506,7 +512,13 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
 #pragma unroll
         for (int e = 0; e < 16; ++e) mx = fmaxf(mx, sacc[kb][e]);
       mx = half_max(mx);
-      const float m_new = fmaxf(m_run, mx * c2);
+      // the row's first tile with a kept key sets the reference maximum m0
+      // (its largest p is exactly 1); later tiles raise it in whole steps:
+      // p = exp2(s c - m0 - k) has the same mantissa for every integer k, so P
+      // rounds to the same 16-bit values whichever maximum was current (and
+      // alpha below is an exact power of two)
+      const float mc = mx * c2;
+      const float m_new = m_run == kNegInf ? mc : m_run + fmaxf(0.f, ceilf(mc - m_run));
       const float alpha = (m_run == kNegInf) ? 0.f : exp2_fast(m_run - m_new);
       l_run *= alpha;
 #pragma unroll

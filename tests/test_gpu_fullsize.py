@@ -1,25 +1,35 @@
-"""GPU parity at the BASELINE configs, full size (H, P, S, M).
+"""GPU parity at the BASELINE configs, full size (H, P, S, M), and at the
+reference's own scripted regression (T 8191 at the headline heads).
 
-The oracle is the closed-form, row-chunked restatement of the eager reference
-(oracle/eager.py ``eager_grads_chunked``, pinned against autograd through the
-eager graph in tests/test_oracle.py), run in fp32 on the device: the CPU would
-take minutes per config.  Inputs are the seeded BASELINE inputs
-(oracle/inputs.py CONFIGS).
+Two oracles, both run on the device (the CPU would take minutes per config):
 
-Bar, per output (O, dQ, dK, dV) over the entries where the oracle is finite,
-with NaN positions identical: |ours - oracle| <= 2e-2 + 2^-6 |oracle| per entry
-and mean_abs <= max(1e-4, 2^-8 mean|oracle|) -- the rule of the small-shape
-suite (tests/test_gpu_parity.py).  The strict north-star bar (max_abs <= 2e-2
-and mean_abs <= 1e-4) is printed beside it.  It holds at H and M; where
-outputs are large it is below bf16 resolution: one bf16 ulp is 2^-5 at |x| >= 4
-(the causal configs' first keys reach |dV| ~ 10), and at P (short documents,
-mean|dV| ~ 0.17, ulp 2^-10) P and dS rounded to bf16 inside the GEMMs -- as the
-reference kernel does, python/fa2.py:287, 291 -- move a fraction of the bf16
-outputs to the neighbouring value, a mean error of about 0.3 ulp of the typical
-entry.  Every config runs the atomic-dQ backward (the reference default) and
-the deterministic one (dQ from the stored dS tiles).
+* the eager oracle: the closed-form, row-chunked restatement of the reference's
+  eager fp32 attention (oracle/eager.py ``eager_grads_chunked``, pinned against
+  autograd through the eager graph in tests/test_oracle.py);
+* the rounding restatement (oracle/rounding.py): the same attention in float64
+  with the 16-bit roundings the reference kernel makes (P before PV and dV, dS
+  before dK and dQ, Delta from the output in dtype; python/fa2.py:128-129,
+  166-176, 287, 291), pinned in tests/test_oracle.py.
 
-Size-independent properties checked beside the oracle:
+Every (config, output) cell is asserted one of two ways:
+
+* "met": the north-star bar against the eager oracle, max_abs <= 2e-2 and
+  mean_abs <= 1e-4 (``STRICT``);
+* "floor": the bar is below what 16-bit P and dS allow -- the restatement
+  alone misses it against the eager oracle (the CPU suite shows that on
+  sampled heads: test_bf16_rounding_floor_exceeds_the_strict_bar).  Asserted:
+  the HIP result is within the north-star bar of the restatement, and its
+  error against the eager oracle is no larger than the restatement's own (mean
+  within 5 %, no more entries above 2e-2).
+
+Every cell additionally needs NaN positions identical to both oracles'.  (A
+floor cell's entries are within 2e-2 of the restatement, which is as far as a
+per-entry statement goes there: the restatement itself is off the eager
+oracle by up to a few bf16 steps at some entries.)
+Both backward modes run: use_atomic_backward=True (the reference default) and
+the deterministic one.
+
+Size-independent properties checked beside the oracles:
   * the deterministic backward is bitwise repeatable at full size;
   * bhsd and bshd inputs of the same data give identical outputs (config M).
 """
@@ -29,11 +39,20 @@ import torch
 
 from oracle import eager as E
 from oracle import inputs as I
+from oracle import rounding as R
 
 pytestmark = pytest.mark.gpu
 
 MAX_ABS = 2e-2
 MEAN_ABS = 1e-4
+OUTS = ("out", "dq", "dk", "dv")
+
+# cells that meet the north-star bar against the eager oracle; the others are
+# on the 16-bit rounding floor (see the module docstring)
+STRICT = {
+    "H": OUTS, "M": OUTS, "H_causal": ("out", "dq"), "P": (), "S": (),
+    "R_no_causal": OUTS, "R_causal": ("out", "dq"), "R_random_mask": OUTS, "long_keys_mask": OUTS,
+}
 
 
 def _api():
@@ -65,26 +84,46 @@ def run_oracle(case, cfg):
     return {"out": out, "dq": dq, "dk": dk, "dv": dv}
 
 
-def check(ours, ref, label):
+def run_rounded(case, cfg):
+    r = R.rounded_attention(case["q_bhsd"], case["k_bhsd"], case["v_bhsd"], case["mask"], case["score"],
+                            case["grad_bhsd"], scale=cfg.D ** -0.5, is_causal=cfg.is_causal, round_dtype=cfg.dtype,
+                            block=128)
+    torch.cuda.synchronize()
+    return {n: r[n].to(cfg.dtype) for n in OUTS}
+
+
+def _diff(a, r):
+    """|a - r| over the entries where r is finite, the larger magnitude of the
+    two there, and whether the NaN positions agree."""
+    a, r = a.float(), r.float()
+    fin = torch.isfinite(r)
+    return (a[fin] - r[fin]).abs(), torch.maximum(a[fin].abs(), r[fin].abs()), \
+        bool(torch.equal(torch.isnan(a), torch.isnan(r)))
+
+
+def check(ours, ref, rnd, label, strict):
     failures = []
     for name in ref:
-        st = E.finite_diff_stats(ours[name], ref[name])
-        r = ref[name].float()
-        fin = torch.isfinite(r)
-        err = (ours[name].float()[fin] - r[fin]).abs()
-        mag = r[fin].abs().mean().item() if err.numel() else 0.0
-        margin = (err - (MAX_ABS + 2.0 ** -6 * r[fin].abs())).max().item() if err.numel() else -1.0
-        mean_tol = max(MEAN_ABS, 2.0 ** -8 * mag)
-        strict = st["max_abs"] <= MAX_ABS and st["mean_abs"] <= MEAN_ABS
-        print(f"[{label}] {name}: max_abs={st['max_abs']:.3e} mean_abs={st['mean_abs']:.3e} (tol {mean_tol:.2e}) "
-              f"mean|ref|={mag:.3e} entries>2e-2: {int((err > MAX_ABS).sum().item())} of {err.numel()} "
-              f"nan_match={st['nan_match']} strict_north_star={strict}", flush=True)
-        if not st["nan_match"]:
+        err, r, nan_ok = _diff(ours[name], ref[name])
+        rerr, _, _ = _diff(rnd[name], ref[name])
+        derr, _, nan_rd = _diff(ours[name], rnd[name])
+        mean, rmean = err.mean().item(), rerr.mean().item()
+        over, rover = int((err > MAX_ABS).sum()), int((rerr > MAX_ABS).sum())
+        cell = "met" if name in strict else "floor"
+        print(f"[{label}] {name} ({cell}): vs eager max={err.max().item():.3e} mean={mean:.3e} >2e-2:{over} | "
+              f"restatement vs eager mean={rmean:.3e} >2e-2:{rover} | ours vs restatement "
+              f"max={derr.max().item():.3e} mean={derr.mean().item():.3e}", flush=True)
+        if not nan_ok or not nan_rd:
             failures.append(f"{name}: NaN positions differ")
-        if margin > 0:
-            failures.append(f"{name}: an entry exceeds 2e-2 + 2^-6 |ref| by {margin:.3e}")
-        if st["mean_abs"] > mean_tol:
-            failures.append(f"{name}: mean_abs {st['mean_abs']:.3e} > {mean_tol:.2e}")
+        if name in strict:
+            if err.max().item() > MAX_ABS or mean > MEAN_ABS:
+                failures.append(f"{name}: misses the north-star bar (max {err.max().item():.3e}, mean {mean:.3e})")
+        else:
+            if derr.max().item() > MAX_ABS or derr.mean().item() > MEAN_ABS:
+                failures.append(f"{name}: not within the north-star bar of the rounding restatement")
+            if mean > 1.05 * rmean + 1e-7 or over > rover:
+                failures.append(f"{name}: error above the restatement's floor ({mean:.3e} vs {rmean:.3e}, "
+                                f"{over} vs {rover} entries > 2e-2)")
     assert not failures, f"{label}: " + "; ".join(failures)
 
 
@@ -99,8 +138,8 @@ def test_fullsize_vs_oracle(cuda, name, atomic):
           f"{cfg.layout} causal={cfg.is_causal} mask={cfg.mask} score={cfg.score}", flush=True)
     case = I.make_case(cfg, seed=0, device=cuda)
     ours = run_ours(case, cfg, atomic=atomic)
-    ref = run_oracle(case, cfg)
-    check(ours, ref, f"{name}/{'atomic' if atomic else 'det'}")
+    check(ours, run_oracle(case, cfg), run_rounded(case, cfg), f"{name}/{'atomic' if atomic else 'det'}",
+          STRICT[name])
 
 
 def test_fullsize_deterministic_repeatable(cuda):
@@ -175,8 +214,8 @@ def test_reference_regression_T8191(cuda, name, atomic):
     print(f"case precision_check.sh {name} atomic={atomic} B1 T8191 Hq32 Hk8 D128", flush=True)
     case = _device_case(cfg, seed=0, dev=cuda)
     ours = run_ours(case, cfg, atomic=atomic)
-    ref = run_oracle(case, cfg)
-    check(ours, ref, f"T8191/{name}/{'atomic' if atomic else 'det'}")
+    check(ours, run_oracle(case, cfg), run_rounded(case, cfg), f"T8191/{name}/{'atomic' if atomic else 'det'}",
+          STRICT[cfg.name])
 
 
 def test_long_keys_head_broadcast_mask(cuda):
@@ -188,5 +227,5 @@ def test_long_keys_head_broadcast_mask(cuda):
     for atomic in (True, False):
         print(f"case long_keys_mask atomic={atomic} B1 Tq2048 Tk16384 Hq8 Hk2 D128, mask [1,1,T,T]", flush=True)
         ours = run_ours(case, cfg, atomic=atomic)
-        ref = run_oracle(case, cfg)
-        check(ours, ref, f"long_keys_mask/{'atomic' if atomic else 'det'}")
+        check(ours, run_oracle(case, cfg), run_rounded(case, cfg), f"long_keys_mask/{'atomic' if atomic else 'det'}",
+              STRICT[cfg.name])

@@ -22,6 +22,7 @@ import torch.nn.functional as F
 
 from oracle import bruteforce as BF
 from oracle import eager as E
+from oracle import rounding as R
 from oracle import inputs as I
 
 torch.set_num_threads(min(8, torch.get_num_threads()))
@@ -296,33 +297,120 @@ def test_make_case_layouts_are_bthd_backed():
     assert torch.equal(c2["q"].transpose(1, 2), c["q"])
 
 
-def test_dtype_probabilities_bound_the_mean_error_at_config_P():
-    """Why the strict north-star mean bar (mean_abs <= 1e-4) is out of reach at
-    config P for any kernel that feeds P to the PV product in the input dtype, as
-    the reference kernel does (python/fa2.py:128-129, acc_s cast to dtype before
-    the GEMM) and as this build does: with the maths otherwise exact (float64),
-    rounding only P to bf16 already gives mean_abs ~1.25e-4 against the bf16
-    cast of the exact output on the packed-document mask, where short documents
-    make |O| ~ 0.1.  At the headline shape the same rounding stays far below the
-    bar (long rows average the rounding out)."""
-    cfg = I.CONFIGS["P"].scaled(B=1, Hq=2, Hk=1)
-    case = I.make_case(cfg, seed=0, with_grad=False)
+# ---------------------------------------------------------------------------
+# The rounding-aware restatement (oracle/rounding.py) and the bf16 floor
+# ---------------------------------------------------------------------------
+ROUND_CASES = [
+    I.AttnConfig("r_gqa_mask_score", 1, 70, 90, 4, 2, 32, mask="bernoulli", score="normal"),
+    I.AttnConfig("r_causal_tq_gt_tk", 2, 50, 33, 2, 1, 16, is_causal=True),
+    I.AttnConfig("r_mha_causal_mask", 1, 64, 64, 3, 3, 16, is_causal=True, mask="bernoulli", keep_prob=0.5),
+]
 
-    def mean_err(case, groups):
-        q = case["q_bhsd"].double()
-        k = case["k_bhsd"].double().repeat_interleave(groups, 1)
-        v = case["v_bhsd"].double().repeat_interleave(groups, 1)
-        s = (q @ k.transpose(-1, -2)) * q.shape[-1] ** -0.5
-        if case["mask"] is not None:
-            s = s.masked_fill(~case["mask"], float("-inf"))
-        p = torch.exp(s - s.amax(-1, keepdim=True))
-        exact = ((p @ v) / p.sum(-1, keepdim=True)).float().to(torch.bfloat16).float()
-        pb = p.to(torch.bfloat16).double()
-        rounded = ((pb @ v) / pb.sum(-1, keepdim=True)).float().to(torch.bfloat16).float()
-        return (rounded - exact).abs().mean().item()
 
-    err_p = mean_err(case, 2)
-    assert 1.1e-4 < err_p < 1.5e-4, err_p
-    hcfg = I.CONFIGS["H"].scaled(Hq=1, Hk=1, Tq=512)     # headline rows (Tk 8192), a 512-row slice
-    err_h = mean_err(I.make_case(hcfg, seed=0, with_grad=False), 1)
-    assert err_h < 3e-5, err_h
+@pytest.mark.parametrize("c", ROUND_CASES, ids=[c.name for c in ROUND_CASES])
+def test_rounding_restatement_without_rounding_is_eager(c):
+    """With every rounding off, the restatement (first-tile maximum raised in
+    whole base-2 steps, LSE, Delta from the unrounded output, dS scaled after
+    the products) is the eager attention and its autograd gradients, in
+    float64, dead rows included."""
+    case = I.make_case(c, seed=5)
+    if case["mask"] is not None:
+        m = case["mask"].clone()
+        m[0, 0, 3, :] = False                     # a row with no kept key
+        case["mask"] = m
+    s = c.D ** -0.5
+    args = (case["q_bhsd"], case["k_bhsd"], case["v_bhsd"], case["mask"], case["score"], case["grad_bhsd"])
+    r = R.rounded_attention(*args, scale=s, is_causal=c.is_causal, round_dtype=None, block=16)
+    o, dq, dk, dv = E.eager_fwd_bwd(*[t.double() if torch.is_tensor(t) and t.is_floating_point() else t for t in args],
+                                    scale=s, is_causal=c.is_causal, compute_dtype=torch.float64)
+    for name, a, b in (("out", r["out"], o), ("dq", r["dq"], dq), ("dk", r["dk"], dk), ("dv", r["dv"], dv)):
+        assert torch.equal(torch.isnan(a), torch.isnan(b)), name
+        fin = torch.isfinite(b)
+        assert torch.allclose(a[fin], b[fin].double(), atol=1e-11, rtol=1e-9), name
+    lse = E.lse2_reference(case["q_bhsd"].double(), case["k_bhsd"].double(), case["mask"], case["score"], scale=s,
+                           is_causal=c.is_causal)
+    fin = torch.isfinite(lse)
+    assert torch.allclose(r["lse"][fin], lse[fin].double(), atol=1e-4)
+    # rounding points switched off one by one with a dtype given: still exact
+    r2 = R.rounded_attention(*args, scale=s, is_causal=c.is_causal, round_dtype=torch.bfloat16, round_p_fwd=False,
+                             round_p_bwd=False, round_ds=False, delta_from_output=False, block=16)
+    for n in ("out", "dq", "dk", "dv"):
+        fin = torch.isfinite(r[n])
+        assert torch.allclose(r2[n][fin], r[n][fin], atol=1e-11, rtol=1e-9), n
+
+
+def test_integer_maximum_makes_the_rounded_probabilities_independent_of_it():
+    """bf16(2^(y - m)) * 2^(m - m') == bf16(2^(y - m')) for integers m, m' (the
+    rounded mantissa is that of 2^frac(y)); a fractional shift of the maximum
+    changes the rounded values -- the property that lets an online softmax with
+    stale integer maxima round P exactly as a softmax against the final one."""
+    g = I.make_generator(0)
+    y = torch.rand(200000, generator=g, dtype=torch.float64) * 40 - 30
+    for m1, m2 in ((10.0, 3.0), (0.0, -7.0), (25.0, 24.0)):
+        a = torch.exp2(y - m1).to(torch.bfloat16).double() * 2.0 ** (m1 - m2)
+        b = torch.exp2(y - m2).to(torch.bfloat16).double()
+        assert torch.equal(a, b)
+    a = torch.exp2(y - 10.0).to(torch.bfloat16).double() * 2.0 ** (10.0 - 9.63)
+    b = torch.exp2(y - 9.63).to(torch.bfloat16).double()
+    assert (a != b).float().mean().item() > 0.5
+
+
+def _floor(cfg_name, heads_kv, mean_bar=1e-4):
+    """Mean |restatement - eager fp32| per output (both cast to bf16) on batch 0
+    and the first ``heads_kv`` kv-heads of a BASELINE config, for the
+    restatement with this build's rounding placements and with the
+    reference's own (fractional maximum, dS rounded after scaling)."""
+    cfg = I.CONFIGS[cfg_name]
+    case = I.make_case(cfg, seed=0)
+    G = cfg.Hq // cfg.Hk
+    hq = heads_kv * G
+    q, k, v, g = (case[n][:1, :h] for n, h in (("q_bhsd", hq), ("k_bhsd", heads_kv), ("v_bhsd", heads_kv),
+                                                ("grad_bhsd", hq)))
+    mask = case["mask"]
+    mask = None if mask is None else mask[:1, : (hq if mask.shape[1] > 1 else 1)]
+    score = None if case["score"] is None else case["score"][:1, :hq]
+    s = cfg.D ** -0.5
+    e32 = dict(zip(("out", "dq", "dk", "dv"), E.eager_grads_chunked(q, k, v, mask, score, g, scale=s,
+                                                                     is_causal=cfg.is_causal, block=256)))
+    res = {}
+    for label, kw in (("build", {}), ("reference", dict(max_mode="row", scale_ds_before_round=True))):
+        r = R.rounded_attention(q, k, v, mask, score, g, scale=s, is_causal=cfg.is_causal, round_dtype=cfg.dtype,
+                                block=256, **kw)
+        res[label] = {n: (r[n].to(cfg.dtype).float() - e32[n].float()).abs().mean().item() for n in e32}
+    return res
+
+
+@pytest.mark.parametrize("cfg_name,heads_kv", [("P", 1), ("S", 2)])
+def test_bf16_rounding_floor_exceeds_the_strict_bar(cfg_name, heads_kv):
+    """The floor that the reference kernel's rounding points (P before PV and
+    dV, dS before dK and dQ, Delta from the output in dtype; python/fa2.py:
+    128-129, 166-176, 287, 291) leave against the eager fp32 oracle: at config
+    P (short packed documents: few keys per row, |P| large) and at config S's
+    steepest ALiBi heads (local attention), every output's mean error exceeds
+    the strict bar 1e-4, with this build's rounding placements (integer
+    first-tile maximum raised in whole steps, dS rounded before the factor
+    scale) and with the reference's own
+    (fractional running maximum, dS rounded after scaling) alike.  The GPU
+    suite shows the HIP kernels equal the restatement within the strict bar,
+    so these cells sit on a floor every 16-bit kernel of this design shares."""
+    res = _floor(cfg_name, heads_kv)
+    print(cfg_name, res)
+    for label, errs in res.items():
+        for n, e in errs.items():
+            assert e > 1e-4, (label, n, e)
+    for n in res["build"]:
+        assert 0.6 < res["build"][n] / res["reference"][n] < 1.6, (n, res)
+
+
+def test_bf16_rounding_floor_is_far_below_the_bar_at_the_headline():
+    """At the headline's long rows the same roundings average out: a 256-row
+    slice of config H (Tk 8192, one kv-head group) stays well under 1e-4."""
+    cfg = I.CONFIGS["H"].scaled(Tq=256, Hq=4, Hk=1)
+    case = I.make_case(cfg, seed=0)
+    s = cfg.D ** -0.5
+    args = (case["q_bhsd"], case["k_bhsd"], case["v_bhsd"], None, None, case["grad_bhsd"])
+    e32 = dict(zip(("out", "dq", "dk", "dv"), E.eager_grads_chunked(*args, scale=s, is_causal=False, block=256)))
+    r = R.rounded_attention(*args, scale=s, is_causal=False, round_dtype=torch.bfloat16, block=256)
+    for n in e32:
+        err = (r[n].to(torch.bfloat16).float() - e32[n].float()).abs().mean().item()
+        assert err < 6e-5, (n, err)
