@@ -18,6 +18,10 @@ namespace fa {
 int fwd_block_rows();
 int dkdv_block_keys();
 int dq_block_rows();
+// fa_noalloc.hip: the allocation-free backward's device scratch
+int64_t noalloc_scratch_bytes();
+hipError_t scratch_device_ptr(void** out);
+hipError_t launch_fill_i32(int32_t* p, int64_t n, int32_t v, hipStream_t s);
 }  // namespace fa
 
 namespace {
@@ -493,6 +497,46 @@ int fa_bwd_finalize(const FaBwdParams* p) {
     if ((st = launch_status(fa::launch_convert(cv, p->dtype, s), "dv convert"))) return st;
   }
   return FA_OK;
+}
+
+// Allocation-free backward: the deterministic route with dQ recomputed and
+// dK/dV written directly (no dS tiles, no fp32 accumulators), with Delta, the
+// backward LSE and the dead-row flags in the library's device scratch
+// (fa_noalloc.hip) instead of caller workspaces.
+int fa_bwd_noalloc(const FaBwdParams* p) {
+  if (!p) return fail(FA_ERR_NULL, "params is NULL");
+  int st = check_dims(p->batch, p->seqlen_q, p->seqlen_k, p->heads_q, p->heads_k, p->head_dim, p->dtype, p->scale);
+  if (st) return st;
+  const int64_t rows = (int64_t)p->batch * p->heads_q * p->seqlen_q;
+  const int64_t flag_off = fa::align256(2 * rows * (int64_t)sizeof(float));
+  const int64_t need = flag_off + (int64_t)p->batch * p->heads_k * (int64_t)sizeof(int32_t);
+  const int64_t cap = fa::noalloc_scratch_bytes();
+  if (need > cap)
+    return fail(FA_ERR_WORKSPACE,
+                "fa_bwd_noalloc needs %lld bytes of device scratch (8 B per query row of every head, 4 B per "
+                "(batch, kv-head)); it holds %lld (B*Hq*Tq up to about %lld): use fa_bwd with workspaces",
+                (long long)need, (long long)cap, (long long)(cap / 8));
+  // validate everything with stand-in workspace addresses before any HIP call
+  FaBwdParams q = *p;
+  q.dq_accum = q.dk_accum = q.dv_accum = nullptr;
+  q.ds_tiles = nullptr;
+  q.ds_limit_bytes = -1;   // no dS tiles: dQ is recomputed
+  q.atomic_dq = 0;
+  q.kv_split = 1;          // dK/dV written by the kernel, no fp32 slabs
+  q.delta = (float*)(uintptr_t)256;
+  q.dead_flags = (int32_t*)(uintptr_t)256;
+  if ((st = check_bwd(&q, 1))) return st;
+  void* base = nullptr;
+  const hipError_t e = fa::scratch_device_ptr(&base);
+  if (e != hipSuccess) return fail(FA_ERR_LAUNCH, "fa_bwd_noalloc: device scratch lookup failed: %s", hipGetErrorString(e));
+  q.delta = (float*)base;
+  q.dead_flags = (int32_t*)((char*)base + flag_off);
+  if ((st = launch_status(fa::launch_fill_i32(q.dead_flags, (int64_t)p->batch * p->heads_k, 0, (hipStream_t)p->stream),
+                          "fa_bwd_noalloc flag clear")))
+    return st;
+  if ((st = fa_bwd_preprocess(&q))) return st;
+  if ((st = fa_bwd(&q))) return st;
+  return fa_bwd_finalize(&q);
 }
 
 }  // extern "C"

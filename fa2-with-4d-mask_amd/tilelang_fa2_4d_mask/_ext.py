@@ -88,7 +88,7 @@ class FaBwdPlan(ctypes.Structure):
 
 
 EXPORTED = ("fa_fwd", "fa_bwd_preprocess", "fa_bwd", "fa_bwd_finalize", "fa_bwd_plan", "fa_mask_plan",
-            "fa_mask_prepare", "fa_last_error", "fa_abi_version")
+            "fa_mask_prepare", "fa_last_error", "fa_abi_version", "fa_bwd_noalloc")
 
 _lib = None
 _lock = threading.Lock()
@@ -117,6 +117,8 @@ def load_library(path: os.PathLike | None = None) -> ctypes.CDLL:
         lib.fa_bwd.restype = ctypes.c_int
         lib.fa_bwd_finalize.argtypes = [ctypes.POINTER(FaBwdParams)]
         lib.fa_bwd_finalize.restype = ctypes.c_int
+        lib.fa_bwd_noalloc.argtypes = [ctypes.POINTER(FaBwdParams)]
+        lib.fa_bwd_noalloc.restype = ctypes.c_int
         lib.fa_bwd_plan.argtypes = [ctypes.POINTER(FaBwdParams), ctypes.POINTER(FaBwdPlan)]
         lib.fa_bwd_plan.restype = ctypes.c_int
         lib.fa_mask_plan.argtypes = [ctypes.POINTER(FaMaskParams), ctypes.POINTER(ctypes.c_int64)]

@@ -198,6 +198,23 @@ int fa_bwd(const FaBwdParams* p);
  * python/fa2.py:295-297, 420-421.  Must follow fa_bwd on the same stream. */
 int fa_bwd_finalize(const FaBwdParams* p);
 
+/* Backward without any workspace from the caller and without allocating.  No
+ * counterpart in the reference: for callers that cannot allocate device memory
+ * (code under HIP graph capture, serving loops, harnesses that forbid hipMalloc).
+ * Same problem, inputs, outputs and results as fa_bwd_preprocess + fa_bwd +
+ * fa_bwd_finalize with atomic_dq = 0 and no dS workspace (ds_limit_bytes < 0):
+ * dK/dV from the dK/dV kernel, dQ recomputed, deterministic.  Ignores delta,
+ * dead_flags, dq_accum, dk_accum, dv_accum, ds_tiles, ds_limit_bytes, atomic_dq
+ * and kv_split.  Delta, the backward LSE and the dead-row flags live in a 16 MiB
+ * device array of the library, one per GPU, held until the process ends: a
+ * problem needs 8 bytes per query row of every head plus 4 per (batch, kv-head),
+ * i.e. B*Hq*Tq up to about 2 million rows; larger ones return FA_ERR_WORKSPACE.
+ * Calls on one GPU share that array: calls that overlap on one GPU (other
+ * streams, unordered host threads) race.  A mask still needs its prepared
+ * workspace (mask_ws, the one the forward used).  The current device must be the
+ * stream's. */
+int fa_bwd_noalloc(const FaBwdParams* p);
+
 /* Fills *plan for the problem in *p (no launch, no GPU access). */
 int fa_bwd_plan(const FaBwdParams* p, FaBwdPlan* plan);
 

@@ -153,6 +153,25 @@ def test_null_params(lib):
     assert lib.fa_bwd_plan(None, None) == 1
     assert lib.fa_mask_plan(None, None) == 1
     assert lib.fa_mask_prepare(None) == 1
+    assert lib.fa_bwd_noalloc(None) == 1
+
+
+NOALLOC_ERRORS = [
+    (dict(seqlen_q=1 << 21), 8, "device scratch"),        # 2^26 rows: 512 MiB of Delta/LSE > 16 MiB
+    (dict(q=None), 1, "q is NULL"),
+    (dict(dq=None), 1, "dq is NULL"),
+    (dict(head_dim=32), 3, "head_dim 32"),
+    (dict(mask=FAKE), 8, "prepared workspace"),
+]
+
+
+@pytest.mark.parametrize("over,code,msg", NOALLOC_ERRORS, ids=[e[2] for e in NOALLOC_ERRORS])
+def test_noalloc_validation(lib, over, code, msg):
+    """The allocation-free backward rejects what it cannot run before any HIP
+    call; it needs none of the workspaces (they are NULL here)."""
+    over = dict(dict(delta=None, dead_flags=None, dq_accum=None, ds_tiles=None), **over)
+    assert lib.fa_bwd_noalloc(ctypes.byref(bwd_params(**over))) == code
+    assert msg in lib.fa_last_error().decode()
 
 
 BWD_ERRORS = [
