@@ -13,6 +13,17 @@ dQ = dS K); the reference's default atomic-dQ backward is timed in the same run
 FLOP convention (benchmark/throughput_check.py:85-92): fwd 4*B*Hq*Tq*Tk*D,
 fwd+bwd 14*..., x0.5 when causal.  Peak: MI355X dense bf16 MFMA 2.5 PFLOP/s.
 
+Timing (the reference's do_bench protocol, throughput_check.py:216, 248-256):
+after W untimed steps, each of K steps is timed with its own HIP event pair
+on the launch stream, with a 512 MiB write before it (outside the events) so
+that L2 and the 256 MB Infinity Cache hold none of its inputs; ``ms_per_step``
+is the median, with the 20/80 % quantiles beside it, and
+``ms_per_step_window`` the synchronised wall time of the whole loop per step
+(flushes included).  ``peak_mem_mib`` is the peak device memory one step
+allocates beyond what is live before it (throughput_check.py:218-243);
+``ds_limit_bytes`` the dS workspace limit in force (an eighth of free device
+memory, at most 8 GiB).
+
 ``roofline`` is for the dominant kernel of the step, the dK/dV kernel launched
 by ``fa_bwd`` on the deterministic path: 4 GEMMs (S, dP, dV, dK), i.e.
 8*B*Hq*Tq*Tk*D algorithmic FLOPs per launch, timed with HIP events on the
@@ -25,7 +36,10 @@ this repository's eager fp32 oracle on the host cores on a bounded sample.
 The other BASELINE configs (P: packed-document mask, S: score + sparse mask,
 M: MQA long KV, bshd) are timed after the headline and reported under
 ``configs`` with dense-convention TFLOPS and GB/s against their algorithmic
-bytes (each tensor once; mask at its passed head count).
+bytes (each tensor once; mask at its passed head count), the HBM fraction of
+8 TB/s, and for the masked ones the live TFLOPS (dense convention times the
+kept fraction of pairs) and its fraction of peak instead of a dense fraction.
+``cpu_baseline`` also times BASELINE configs[0] (C) on the host.
 
 Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline] [--no-side-configs]
 """
@@ -129,24 +143,97 @@ def side_bytes(x, mode: str) -> float:
     return float(fwd + 2 * d * (2 * b * tq * hq + 2 * b * tk * hk) + 4 * b * hq * tq + side)
 
 
-def time_steps(torch, fn, steps: int, warmup: int, record_events):
+FLUSH_BYTES = 512 << 20   # > the 256 MB Infinity Cache (MALL) and every XCD's L2
+
+
+class Flusher:
+    """Writes a 512 MiB buffer between timed steps (outside their events), so
+    that no step finds its inputs in L2 or the MALL, as the reference's
+    do_bench clears the cache before every repetition
+    (benchmark/throughput_check.py:248-256)."""
+
+    def __init__(self, torch, dev):
+        self.buf = torch.empty(FLUSH_BYTES // 4, dtype=torch.float32, device=dev)
+        self.n = 0
+
+    def __call__(self):
+        self.n += 1
+        self.buf.fill_(float(self.n))
+
+
+def time_steps(torch, fn, steps: int, warmup: int, record_events, flush):
+    """Times each of ``steps`` steps with a HIP event pair on the launch stream
+    (torch's current stream), after ``warmup`` untimed steps, with the cache
+    flushed before every step outside the events.  Returns the median and the
+    20/80 % quantiles of the per-step times (the reference's do_bench
+    statistics, throughput_check.py:216, 248-256), the synchronised wall time
+    of the whole timed loop per step (flushes included), and each library
+    call's mean time."""
     for _ in range(warmup):
+        flush()
         fn()
     torch.cuda.synchronize()
+    ev0 = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ev1 = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
     with record_events() as ev:
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        for _ in range(steps):
+        for i in range(steps):
+            flush()
+            ev0[i].record()
             fn()
+            ev1[i].record()
         torch.cuda.synchronize()
         t1 = time.perf_counter()
+    per = sorted(a.elapsed_time(b) for a, b in zip(ev0, ev1))
+    q = statistics.quantiles(per, n=10, method="inclusive") if len(per) > 1 else [per[0]] * 9
     per_kernel = {name: statistics.mean(v) for name, v in ev.elapsed_ms().items()}
-    return (t1 - t0) * 1e3 / steps, per_kernel
+    return {"ms": statistics.median(per), "ms_p20": q[1], "ms_p80": q[7],
+            "ms_window": (t1 - t0) * 1e3 / steps}, per_kernel
+
+
+def peak_extra_mib(torch, fn, dev) -> float:
+    """Peak device memory one step allocates beyond what is live before it
+    (benchmark/throughput_check.py:218-243)."""
+    torch.cuda.empty_cache()
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats(dev)
+    base = torch.cuda.memory_allocated(dev)
+    fn()
+    torch.cuda.synchronize()
+    return round((torch.cuda.max_memory_allocated(dev) - base) / 2 ** 20, 1)
+
+
+def cpu_config_c(seconds: float) -> dict:
+    """BASELINE configs[0] (C): the eager fp32 oracle's fwd+bwd at B1 Hq4 Hk2
+    T256 D64, causal, fp32 Q/K/V/dO ~ N(0,1), on the host cores."""
+    import torch
+
+    from oracle import eager as E
+
+    g = torch.Generator(device="cpu")
+    g.manual_seed(0)
+    q = torch.randn((1, 256, 4, 64), generator=g).transpose(1, 2)
+    k = torch.randn((1, 256, 2, 64), generator=g).transpose(1, 2)
+    v = torch.randn((1, 256, 2, 64), generator=g).transpose(1, 2)
+    do = torch.randn((1, 256, 4, 64), generator=g).transpose(1, 2)
+    E.eager_fwd_bwd(q, k, v, None, None, do, scale=64 ** -0.5, is_causal=True)   # warm-up
+    times = []
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end or len(times) < 3:
+        t0 = time.perf_counter()
+        E.eager_fwd_bwd(q, k, v, None, None, do, scale=64 ** -0.5, is_causal=True)
+        times.append(time.perf_counter() - t0)
+    ms = statistics.median(times) * 1e3
+    flops = 14.0 * 0.5 * 1 * 4 * 256 * 256 * 64
+    return {"workload": "C (BASELINE configs[0]): B1 Hq4 Hk2 T256 D64 fp32 causal, fwd+bwd", "ms": round(ms, 4),
+            "tflops": round(flops / (ms * 1e-3) * 1e-12, 5), "runs": len(times)}
 
 
 def cpu_baseline(seconds: float) -> dict:
     """Eager fp32 oracle (oracle/eager.py) on the host cores, fwd+bwd, on a bounded
-    sample of the headline workload: one kv-head group (Hq=4, Hk=1) at full T."""
+    sample of the headline workload: one kv-head group (Hq=4, Hk=1) at full T;
+    BASELINE configs[0] (C) beside it."""
     import torch
 
     from oracle import eager as E
@@ -178,6 +265,7 @@ def cpu_baseline(seconds: float) -> dict:
         "kind": "port",
         "sample": (f"oracle eager fp32 fwd+bwd (ref_block=128) at B1 T8192 Hq4 Hk1 D128 non-causal "
                    f"(1/8 of the headline heads), {runs} run(s) in {el:.1f} s; host affinity {cores} cores"),
+        "config_C": cpu_config_c(min(5.0, seconds / 3)),
     }
 
 
@@ -255,6 +343,9 @@ def main() -> int:
         return f
 
     log(f"device: {torch.cuda.get_device_name(dev)}; workload B{B} T{T} Hq{HQ} Hk{HK} D{D} bf16")
+    flush = Flusher(torch, dev)
+    from tilelang_fa2_4d_mask.fa2 import ds_limit_bytes
+    ds_limit = ds_limit_bytes(dev)
     results = {}
     for name, fn, mode, causal in (
         ("fwd_bwd", fwd_bwd(False, False), "fwd_bwd", False),
@@ -264,11 +355,19 @@ def main() -> int:
         ("fwd_bwd_atomic", fwd_bwd(False, True), "fwd_bwd", False),
         ("fwd_bwd_causal_atomic", fwd_bwd(True, True), "fwd_bwd", True),
     ):
-        ms, kern = time_steps(torch, fn, args.steps, args.warmup, record_kernel_events)
+        tm, kern = time_steps(torch, fn, args.steps, args.warmup, record_kernel_events, flush)
+        ms = tm["ms"]
         tf = conv_flops(mode, causal) / (ms * 1e-3) * 1e-12
-        results[name] = {"ms": round(ms, 4), "tflops": round(tf, 2), "frac_of_peak": round(tf / PEAK_TFLOPS, 4),
+        results[name] = {"ms": round(ms, 4), "ms_p20": round(tm["ms_p20"], 4), "ms_p80": round(tm["ms_p80"], 4),
+                         "ms_window": round(tm["ms_window"], 4), "tflops": round(tf, 2),
+                         "tflops_p20_p80": [round(conv_flops(mode, causal) / (tm[k] * 1e-3) * 1e-12, 2)
+                                            for k in ("ms_p80", "ms_p20")],
+                         "frac_of_peak": round(tf / PEAK_TFLOPS, 4),
+                         "peak_extra_mib": peak_extra_mib(torch, fn, dev),
                          "kernel_ms": {k2: round(v2, 4) for k2, v2 in kern.items()}}
-        log(f"{name:22s} {ms:8.3f} ms  {tf:8.1f} TFLOPS  ({100 * tf / PEAK_TFLOPS:5.1f}% of peak)  kernels {kern}")
+        q.grad = k.grad = v.grad = None
+        log(f"{name:22s} {ms:8.3f} ms (p20 {tm['ms_p20']:.3f}, p80 {tm['ms_p80']:.3f})  {tf:8.1f} TFLOPS  "
+            f"({100 * tf / PEAK_TFLOPS:5.1f}% of peak)  peak extra {results[name]['peak_extra_mib']} MiB  kernels {kern}")
 
     side = {}
     if not args.no_side_configs:
@@ -292,23 +391,34 @@ def main() -> int:
                 return f
 
             entry = {}
+            # kept fraction of (row, key) pairs: the work a kernel that skips
+            # dropped entries has to do (the dense convention overstates it)
+            keep = x["mask"].float().mean().item() if x["mask"] is not None else 1.0
             for mode, fn in (("fwd", sfwd), ("fwd_bwd", sfb(False)), ("fwd_bwd_atomic", sfb(True))):
-                ms, kern = time_steps(torch, fn, max(3, args.steps // 2), max(1, args.warmup // 2), record_kernel_events)
+                tm, kern = time_steps(torch, fn, max(3, args.steps // 2), max(1, args.warmup // 2),
+                                      record_kernel_events, flush)
+                ms = tm["ms"]
                 fl = flops_fwd * (1.0 if mode == "fwd" else 3.5)
                 nbytes = side_bytes(x, "fwd" if mode == "fwd" else "fwd_bwd")
-                entry[mode] = {"ms": round(ms, 4), "tflops_dense_conv": round(fl / (ms * 1e-3) * 1e-12, 2),
-                               "frac_of_peak": round(fl / (ms * 1e-3) * 1e-12 / PEAK_TFLOPS, 4),
-                               "alg_bytes": nbytes, "gbps": round(nbytes / (ms * 1e-3) * 1e-9, 1),
-                               "kernel_ms": {k2: round(v2, 4) for k2, v2 in kern.items()}}
-                log(f"{name} {mode:15s} {ms:8.3f} ms  {entry[mode]['tflops_dense_conv']:8.1f} TFLOPS (dense conv.)"
-                    f"  {entry[mode]['gbps']:8.1f} GB/s of {nbytes / 1e9:.3f} GB algorithmic  kernels {kern}")
+                gbps = nbytes / (ms * 1e-3) * 1e-9
+                e = {"ms": round(ms, 4), "ms_p20": round(tm["ms_p20"], 4), "ms_p80": round(tm["ms_p80"], 4),
+                     "ms_window": round(tm["ms_window"], 4),
+                     "tflops_dense_conv": round(fl / (ms * 1e-3) * 1e-12, 2),
+                     "alg_bytes": nbytes, "gbps": round(gbps, 1), "hbm_frac": round(gbps / 8000.0, 4),
+                     "peak_extra_mib": peak_extra_mib(torch, fn, dev),
+                     "kernel_ms": {k2: round(v2, 4) for k2, v2 in kern.items()}}
+                if x["mask"] is None:
+                    e["frac_of_peak"] = round(e["tflops_dense_conv"] / PEAK_TFLOPS, 4)
+                else:
+                    e["tflops_live"] = round(e["tflops_dense_conv"] * keep, 2)
+                    e["live_frac_of_peak"] = round(e["tflops_live"] / PEAK_TFLOPS, 4)
+                xq.grad = xk.grad = xv.grad = None
+                entry[mode] = e
+                log(f"{name} {mode:15s} {ms:8.3f} ms  {e['tflops_dense_conv']:8.1f} TFLOPS (dense conv.)"
+                    f"  {e['gbps']:8.1f} GB/s of {nbytes / 1e9:.3f} GB algorithmic  peak extra {e['peak_extra_mib']} MiB"
+                    f"  kernels {kern}")
             if x["mask"] is not None:
-                # useful work: the dense-convention FLOPs scaled by the kept fraction of
-                # (row, key) pairs (dead tiles are skipped, so the dense figure overstates)
-                keep = x["mask"].float().mean().item()
                 entry["mask_keep_fraction"] = round(keep, 4)
-                for mode in ("fwd", "fwd_bwd", "fwd_bwd_atomic"):
-                    entry[mode]["tflops_useful"] = round(entry[mode]["tflops_dense_conv"] * keep, 2)
             entry["config"] = {"B": bq, "Tq": tq, "Tk": tk, "Hq": hq, "Hk": hk, "D": d, "layout": x["layout"],
                                "mask": None if x["mask"] is None else list(x["mask"].shape),
                                "score": None if x["score"] is None else list(x["score"].shape)}
@@ -353,6 +463,10 @@ def main() -> int:
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": main_res["ms"],
+        "ms_per_step_p20_p80": [main_res["ms_p20"], main_res["ms_p80"]],
+        "ms_per_step_window": main_res["ms_window"],
+        "peak_mem_mib": main_res["peak_extra_mib"],
+        "ds_limit_bytes": ds_limit,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": round(main_res["tflops"] / PUBLISHED_FWD_BWD, 3),

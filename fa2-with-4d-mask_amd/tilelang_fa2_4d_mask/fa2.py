@@ -37,10 +37,27 @@ from torch.autograd.function import once_differentiable
 
 from . import _ext
 
-# Largest dS workspace (bytes) the deterministic backward may allocate to hand
-# dS from the dK/dV kernel to the dQ kernel; 0 = the library's default (8 GiB),
-# negative = never (dQ is then recomputed from Q, K, V, dO).
+# Largest dS workspace (bytes) the backward may allocate to hand dS from the
+# dK/dV kernel to the dQ kernel.  0 = automatic: an eighth of the device memory
+# that is free (to the driver or in torch's cache) at the call, at most 8 GiB
+# (the library's own default; also used under graph capture, where the query is
+# not made); negative = never (dQ is then recomputed from Q, K, V, dO: O(T)
+# extra memory, as the reference's backward).  Below the whole need the
+# backward runs in slices of (batch, kv-head) units.
 DS_LIMIT_BYTES = 0
+DS_LIMIT_CAP = 8 << 30
+DS_LIMIT_FREE_FRACTION = 8
+
+
+def ds_limit_bytes(device: torch.device) -> int:
+    """The dS workspace limit a backward on ``device`` uses now (see DS_LIMIT_BYTES)."""
+    if DS_LIMIT_BYTES != 0:
+        return int(DS_LIMIT_BYTES)
+    if torch.cuda.is_current_stream_capturing():
+        return DS_LIMIT_CAP
+    free, _ = torch.cuda.mem_get_info(device)
+    cached = torch.cuda.memory_reserved(device) - torch.cuda.memory_allocated(device)
+    return max(1, min(DS_LIMIT_CAP, (free + cached) // DS_LIMIT_FREE_FRACTION))
 
 
 def _norm_strides(x: torch.Tensor) -> tuple:
@@ -228,7 +245,7 @@ def _backward_impl(do, q, k, v, O, LSE, mask, score, mask_ws, mst, sst, scale: f
     p.atomic_dq = 1 if use_atomic_backward else 0
     p.kv_split = 0
     p.dtype = _ext.dtype_code(q.dtype)
-    p.ds_limit_bytes = DS_LIMIT_BYTES
+    p.ds_limit_bytes = ds_limit_bytes(dev)
     lib = _ext.load_library()
     plan = _ext.FaBwdPlan()
     _ext.check(lib.fa_bwd_plan(ctypes.byref(p), ctypes.byref(plan)), "fa_bwd_plan", lib)
