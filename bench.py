@@ -270,27 +270,35 @@ def cpu_baseline(seconds: float) -> dict:
 
 
 def traffic_pass(torch, api, dev) -> int:
-    """One untimed launch of each kernel whose HBM traffic is reported, after a
-    1 GiB copy whose counter reading calibrates the counters."""
+    """One untimed launch of each kernel whose counters are reported (what the
+    rocprofv3 --pmc passes count), after a 1 GiB copy whose FETCH_SIZE /
+    WRITE_SIZE reading calibrates those counters: the H forward and
+    deterministic fwd+bwd, non-causal and causal; the S and P fwd+bwd
+    (deterministic)."""
     x = torch.empty(2 ** 28, dtype=torch.float32, device=dev)
     y = torch.empty_like(x)
     y.copy_(x)
     torch.cuda.synchronize()
     del x, y
     q0, k0, v0, do = make_inputs(torch, dev)
-    q, k, v = (t.detach().requires_grad_(True) for t in (q0, k0, v0))
-    with torch.no_grad():
-        api.tilelang_flash_attention(q0, k0, v0)
-    api.tilelang_flash_attention(q, k, v, use_atomic_backward=False).backward(do)
-    torch.cuda.synchronize()
-    del q, k, v, q0, k0, v0, do
+    for causal in (False, True):
+        log(f"profile pass: H causal={causal}")
+        q, k, v = (t.detach().requires_grad_(True) for t in (q0, k0, v0))
+        with torch.no_grad():
+            api.tilelang_flash_attention(q0, k0, v0, is_causal=causal)
+        api.tilelang_flash_attention(q, k, v, is_causal=causal, use_atomic_backward=False).backward(do)
+        torch.cuda.synchronize()
+        del q, k, v
+    del q0, k0, v0, do
     for n, c in side_configs(torch, dev):
-        if n == "S":
-            with torch.no_grad():
-                api.tilelang_flash_attention(c["q"], c["k"], c["v"], mask=c["mask"], score=c["score"],
-                                             layout=c["layout"])
-            break
-    torch.cuda.synchronize()
+        if n not in ("S", "P"):
+            continue
+        log(f"profile pass: {n}")
+        q, k, v = (c[t].detach().requires_grad_(True) for t in ("q", "k", "v"))
+        api.tilelang_flash_attention(q, k, v, mask=c["mask"], score=c["score"], layout=c["layout"],
+                                     use_atomic_backward=False).backward(c["do"])
+        torch.cuda.synchronize()
+        del q, k, v, c
     log("traffic pass done")
     return 0
 
@@ -305,8 +313,9 @@ def main() -> int:
                     help="skip the P / S / M config lines (mask, score+mask, MQA)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--traffic-pass", action="store_true",
-                    help="run once, untimed, what the rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes count: "
-                         "a 1 GiB fp32 copy (calibration), an H forward, an H deterministic fwd+bwd, an S forward")
+                    help="run once, untimed, what the rocprofv3 --pmc passes count: a 1 GiB fp32 copy "
+                         "(calibration), the H forward and deterministic fwd+bwd (non-causal and causal), "
+                         "the S and P deterministic fwd+bwd")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}): this build has no multi-GPU "
