@@ -12,11 +12,15 @@
 //   perm(p) = 16 (p / 16) + 4 ((p / 8) % 2) + 8 ((p / 4) % 2) + p % 4
 // (the order in which the dK/dV kernel's lanes hold them).  In memory the
 // tile is chunk-major: 16-byte chunk c of key row k at byte c 512 + k 16 (the
-// dK/dV kernel then writes whole lines); the staging writes restore the
-// [key][64 bytes] rows in LDS, chunk c of row k at physical chunk
-// c ^ ((k / 4) % 4) (conflict-free 16-lane writes).  ds_read_b64_tr_b16 over
-// that tile yields the B operand of dQ^T = K^T dS^T with lane l = position p
-// directly, so perm only matters when dQ rows are stored.
+// dK/dV kernel then writes whole lines).  In LDS it stays chunk-major, with
+// the key index of chunk c XOR-ed with 4 c: chunk c of key k at byte
+// c 512 + (k ^ 4 c) 16.  A staging write (16 lanes: 16 keys of one chunk)
+// then covers one 256-byte span, and a transpose read (32 lanes: 4 keys x 4
+// chunks) 16 distinct 16-byte slots of one -- both free of bank conflicts
+// (with [key][64 bytes] rows the 64-byte stride of the writes cost 8 conflict
+// cycles per instruction).  ds_read_b64_tr_b16 over that tile yields the B
+// operand of dQ^T = K^T dS^T with lane l = position p directly, so perm only
+// matters when dQ rows are stored.
 //
 // Work decomposition: one workgroup of NW (4 or 8) waves per (64 NW query
 // rows, head, batch[, key split]); wave w owns query steps 2 NW qb + 2 w, + 1
@@ -148,12 +152,15 @@ __global__ __launch_bounds__(NW * 64, 2) void dq_ds_kernel(const BwdArgs a) {
       const int row = 4 * hf + rr + 8 * hi, col = nb * 32 + tr_col;
       at[hi][nb] = opaque(lds0 + row * ROWB + (((col >> 3) ^ swz_q<D>(row)) * 16) + (col & 7) * 2);
     }
-  // B = dS^T (transpose reads of the wave's [key][p] tiles, 64-byte rows, unswizzled)
+  // B = dS^T (transpose reads of the wave's chunk-major tiles): key rows
+  // 4 hf + rr + 8 hi (+16 for the second half, +256 bytes), positions tr_col..+3
+  // in chunk tr_col / 8
   uint32_t bd[2];
 #pragma unroll
-  for (int hi = 0; hi < 2; ++hi)   // rows 4 hf + rr + 8 hi (+16): chunk swizzle (row / 4) % 4 = (hf + 2 hi) % 4
-    bd[hi] = opaque(lds0 + KTILE + wv * DSW + (4 * hf + rr + 8 * hi) * 64 +
-                    ((((tr_col >> 3) ^ ((hf + 2 * hi) & 3))) * 16) + (tr_col & 7) * 2);
+  for (int hi = 0; hi < 2; ++hi) {
+    const int key = 4 * hf + rr + 8 * hi, ch = tr_col >> 3;
+    bd[hi] = opaque(lds0 + KTILE + wv * DSW + ch * 512 + ((key ^ (4 * ch)) & 31) * 16 + (tr_col & 7) * 2);
+  }
 
   // ---- staging -----------------------------------------------------------------------
   const T* __restrict__ kbase = (const T*)a.k + b * a.ksb + kvh * a.ksh;
@@ -168,8 +175,10 @@ __global__ __launch_bounds__(NW * 64, 2) void dq_ds_kernel(const BwdArgs a) {
   const int skey = lane & 31;
   uint32_t sd[2];
 #pragma unroll
-  for (int u = 0; u < 2; ++u)
-    sd[u] = opaque(lds0 + KTILE + wv * DSW + skey * 64 + ((((lane >> 5) + 2 * u) ^ ((skey >> 2) & 3)) * 16));
+  for (int u = 0; u < 2; ++u) {
+    const int ch = (lane >> 5) + 2 * u;
+    sd[u] = opaque(lds0 + KTILE + wv * DSW + ch * 512 + ((skey ^ (4 * ch)) & 31) * 16);
+  }
   const uint16_t* __restrict__ dsp = (const uint16_t*)a.ds;
   const int64_t plane = ((int64_t)b * a.Hq + h - (int64_t)a.bk0 * a.G) * a.ds_plane;
   int64_t row0[kDqSteps];
@@ -238,7 +247,7 @@ __global__ __launch_bounds__(NW * 64, 2) void dq_ds_kernel(const BwdArgs a) {
       V8 bf[kDqSteps];
 #pragma unroll
       for (int i = 0; i < kDqSteps; ++i) {
-        const uint32_t off = (uint32_t)(BUF * BUFB + i * 2048 + c * 1024);
+        const uint32_t off = (uint32_t)(BUF * BUFB + i * 2048 + c * 256);   // keys 16 c ..
         bf[i] = cat_tr<T>(lds_rdtr(bd[0] + off), lds_rdtr(bd[1] + off));
       }
 #pragma unroll
