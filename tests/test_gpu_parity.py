@@ -265,6 +265,44 @@ def test_dead_rows_from_scores(cuda, cfg):
             assert torch.isnan(ours["dk"][0, 0]).all()   # every key is kept by row 17
 
 
+RAMP = [
+    C("ramp_d128_ragged", 1, 320, 200, 4, 2, 128),
+    C("ramp_d64_causal", 1, 256, 256, 4, 4, 64, is_causal=True),
+]
+
+
+@pytest.mark.parametrize("cfg", RAMP, ids=[c.name for c in RAMP])
+def test_rising_row_maximum(cuda, cfg):
+    """Logits that rise along the keys by about 100 (D 128) or 140 (D 64) base-2
+    steps per 64-key tile: every row's running maximum is raised again and again,
+    each time far above the forward's fast-path allowance (O rescaled by powers
+    of two of up to 2^-140).  O against the oracle's forward, LSE (base 2)
+    against a float64 logsumexp of the same 16-bit inputs within 1e-3 (the fp32
+    row sum of up to 200 terms).  Gradients are left to the other tests: keys of
+    size ~300 make one 16-bit step of dS worth more than the gradient bar."""
+    case = I.make_case(cfg, seed=6, with_grad=False)
+    q, k = case["q_bhsd"], case["k_bhsd"]   # views of the tensors the API receives
+    q[..., 0] = 8.0
+    k[..., 0] = (1.5 * torch.arange(cfg.Tk, dtype=torch.float32)).to(k.dtype)
+    ours = run_ours(case, cfg, backward=False)
+    ref = run_oracle_cpu(case, cfg, backward=False)
+    check(ours, ref, label=f"rising-max {cfg.name}")
+    dev = torch.device("cuda:0")
+    scale = cfg.D ** -0.5
+    with torch.no_grad():
+        q_t, k_t, v_t = (case[n + "_bhsd"].transpose(1, 2).to(dev) for n in ("q", "k", "v"))   # [B, T, H, D]
+        _, lse, _ = torch.ops.tilelang_fa2_4d_mask.fwd(q_t, k_t, v_t, None, None, scale, cfg.is_causal, False)
+    kk = case["k_bhsd"].double().repeat_interleave(cfg.Hq // cfg.Hk, dim=1)
+    logits = (case["q_bhsd"].double() @ kk.transpose(-1, -2)) * scale
+    if cfg.is_causal:
+        keep = torch.arange(cfg.Tk)[None, :] <= torch.arange(cfg.Tq)[:, None]
+        logits = logits.masked_fill(~keep, float("-inf"))
+    want = torch.logsumexp(logits, dim=-1) / math.log(2.0)
+    err = (lse.cpu().double() - want).abs().max().item()
+    print(f"[rising-max {cfg.name}] lse max_abs={err:.3e} (|lse| up to {want.abs().max().item():.1f})", flush=True)
+    assert err <= 1e-3
+
+
 def test_leading_masked_tiles_are_not_nan(cuda):
     """A row whose first key tiles are all dropped but later keys are kept must be
     finite (the reference TileLang kernel turns such rows into NaN; eager does not)."""
