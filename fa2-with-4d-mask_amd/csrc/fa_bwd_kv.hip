@@ -492,6 +492,28 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
     }
 #pragma unroll
     for (int e = 0; e < EPS; ++e) elem_fin((NOP - 1) * EPS + e, pe[(NOP - 1) & 1][e]);
+    if constexpr (CAUSAL && !MASK) {
+      // Causal without a mask: P and dS leave the step only packed (dV, dK, the
+      // dS tile), so the entries above the diagonal are cleared there, with a
+      // 32-bit AND per pair of 16-bit entries, on the steps where some key of
+      // this wave lies above some row (bit pattern AND, so an overflowed p of a
+      // dropped entry goes too).  Entry i: row 8 (i/4) + 4 hf + i%4, kept iff
+      // dkq <= 8 (i/4) + i%4.
+      if (kw0 + 31 > it_qs) {
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          u32x4 mk;
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            const int i0 = 8 * c + 2 * k, i1 = i0 + 1;
+            mk[k] = (dkq <= 8 * (i0 >> 2) + (i0 & 3) ? 0x0000ffffu : 0u) |
+                    (dkq <= 8 * (i1 >> 2) + (i1 & 3) ? 0xffff0000u : 0u);
+          }
+          ppk[PJ][c] = __builtin_bit_cast(V8, __builtin_bit_cast(u32x4, ppk[PJ][c]) & mk);
+          dspk[PJ][c] = __builtin_bit_cast(V8, __builtin_bit_cast(u32x4, dspk[PJ][c]) & mk);
+        }
+      }
+    }
     // next step's dS descriptor and position, then its mask / score
     next_step(j);
     load_ms(j + 1 < n);
@@ -537,9 +559,10 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
     constexpr int BUF = decltype(BUFc)::value;
     store_tile((BUF + 2) % kNBuf, IC<BUF & 1>{});   // tile j+2 (staged two iterations ago)
     load_next(IC<BUF & 1>{});                       // tile j+4
-    // causal: the compare runs on every step (a second copy of the body for
-    // the steps off the diagonal would not fit the register budget)
-    iter(BUFc, IC<(MASK || CAUSAL) ? 1 : 0>{}, j);
+    // with a mask the keep test runs per entry on every step (a second copy of
+    // the body for steps without dropped entries would not fit the register
+    // budget); causal alone clears packed entries on the diagonal steps
+    iter(BUFc, IC<MASK ? 1 : 0>{}, j);
     lds_barrier();
   };
   int n4 = n > 0 ? (n + 4) & ~3 : 0;
