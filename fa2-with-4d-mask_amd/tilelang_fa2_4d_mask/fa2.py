@@ -23,7 +23,11 @@ What differs on purpose:
 * a mask is prepared once per call (``fa_mask_prepare``: bits, block states,
   live-tile lists) and the workspace is kept for the backward, so the kernels
   skip tiles without a kept entry (the reference streams every tile's mask
-  bytes, python/fa2.py:107-114, 261-280).
+  bytes, python/fa2.py:107-114, 261-280);
+* the kernels exist for head dims 64 and 128 (the reference compiles any D,
+  python/fa2.py:33); other D up to 128 run zero-padded to the next of those,
+  which is exact (see ``kernel_head_dim``), at the price of padded copies of
+  the operands.
 """
 
 from __future__ import annotations
@@ -47,6 +51,28 @@ from . import _ext
 DS_LIMIT_BYTES = 0
 DS_LIMIT_CAP = 8 << 30
 DS_LIMIT_FREE_FRACTION = 8
+
+
+# Head dims the kernels are built for.
+KERNEL_HEAD_DIMS = (64, 128)
+
+
+def kernel_head_dim(D: int) -> int:
+    """Head dim the kernels run a problem of head dim ``D`` at: the smallest of
+    KERNEL_HEAD_DIMS that is >= D (D itself when above them: the library then
+    rejects it).  Zero columns appended to Q, K, V (and O, dO) leave Q K^T, the
+    softmax and Delta = rowsum(O * dO) unchanged and give zero columns in O, dQ,
+    dK, dV, which are dropped: the padded problem is exact."""
+    for w in KERNEL_HEAD_DIMS:
+        if D <= w:
+            return w
+    return D
+
+
+def _pad_head_dim(x: torch.Tensor, Dp: int) -> torch.Tensor:
+    """[B, T, H, D] -> [B, T, H, Dp], zeros appended (x itself when D == Dp)."""
+    D = x.shape[3]
+    return x if D == Dp else torch.nn.functional.pad(x, (0, Dp - D))
 
 
 def ds_limit_bytes(device: torch.device) -> int:
@@ -184,9 +210,12 @@ def _check_qkv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> None:
 def _forward_impl(q, k, v, Mask, Score, scale: float, is_causal: bool):
     """Host side of the forward (python/fa2.py:438-488) on logical [B, T, H, D]
     operands: O [B, Tq, Hq, D], LSE [B, Hq, Tq] and the prepared mask (or None),
-    plus the operands as the kernels saw them."""
-    B, Tq, Hq, D = q.shape
+    plus the operands as the kernels saw them (zero-padded to the kernel head
+    dim, see ``kernel_head_dim``)."""
+    B, Tq, Hq, D_in = q.shape
     _, Tk, Hk, _ = k.shape
+    D = kernel_head_dim(D_in)
+    q, k, v = (_pad_head_dim(x, D) for x in (q, k, v))
     mask, mst = _kernel_side(Mask, torch.bool, B, Hq, Tq, Tk, "mask", q.device)
     score, sst = _kernel_side(Score, torch.float32, B, Hq, Tq, Tk, "score", q.device)
     O = torch.empty((B, Tq, Hq, D), dtype=q.dtype, device=q.device)
@@ -218,16 +247,21 @@ def _forward_impl(q, k, v, Mask, Score, scale: float, is_causal: bool):
             p.stream = _stream(q.device)
             p.mask_ws = _ext.ptr(mask_ws)
             _call(_ext.load_library(), "fa_fwd", p)
+    if D != D_in:
+        O = O[..., :D_in].contiguous()
     return O, LSE, mask_ws, (q, k, v, mask, score, mst, sst)
 
 
 def _backward_impl(do, q, k, v, O, LSE, mask, score, mask_ws, mst, sst, scale: float, is_causal: bool,
                    use_atomic_backward: bool):
     """Host side of the backward (python/fa2.py:490-556) on logical [B, T, H, D]
-    operands as the forward's kernels saw them; returns dQ, dK, dV in the
-    input dtype, [B, T, H, D] contiguous."""
-    B, Tq, Hq, D = q.shape
+    operands (Q, K, V as given or as the forward's kernels saw them); returns
+    dQ, dK, dV in the input dtype, [B, T, H, D] contiguous with D that of dO.
+    Head dims other than the kernels' run zero-padded (``kernel_head_dim``)."""
+    B, Tq, Hq, D_in = do.shape
     _, Tk, Hk, _ = k.shape
+    D = kernel_head_dim(D_in)
+    q, k, v, O, do = (_pad_head_dim(x, D) for x in (q, k, v, O, do))
     dev = q.device
     dQ = torch.empty((B, Tq, Hq, D), dtype=q.dtype, device=dev)
     dK = torch.empty((B, Tk, Hk, D), dtype=q.dtype, device=dev)
@@ -236,7 +270,7 @@ def _backward_impl(do, q, k, v, O, LSE, mask, score, mask_ws, mst, sst, scale: f
         dQ.zero_()
         dK.zero_()
         dV.zero_()
-        return dQ, dK, dV
+        return tuple(x[..., :D_in].contiguous() for x in (dQ, dK, dV))
     do = _kernel_operand(do.to(q.dtype))
     p = _ext.FaBwdParams()
     p.batch, p.seqlen_q, p.seqlen_k, p.heads_q, p.heads_k, p.head_dim = B, Tq, Tk, Hq, Hk, D
@@ -285,6 +319,8 @@ def _backward_impl(do, q, k, v, O, LSE, mask, score, mask_ws, mst, sst, scale: f
     _call(lib, "fa_bwd_preprocess", p)
     _call(lib, "fa_bwd", p)
     _call(lib, "fa_bwd_finalize", p)
+    if D != D_in:
+        dQ, dK, dV = (x[..., :D_in].contiguous() for x in (dQ, dK, dV))
     return dQ, dK, dV
 
 

@@ -265,6 +265,32 @@ def test_dead_rows_from_scores(cuda, cfg):
             assert torch.isnan(ours["dk"][0, 0]).all()   # every key is kept by row 17
 
 
+# head dims the kernels are not built for: zero-padded to 64 / 128 by the host
+PADDED_D = [
+    C("d32_gqa", 1, 192, 256, 4, 2, 32),
+    C("d80_causal", 1, 256, 256, 4, 4, 80, is_causal=True),
+    C("d96_mask", 2, 200, 200, 4, 2, 96, mask="bernoulli"),
+    C("d112_score_fp16", 1, 160, 224, 4, 2, 112, torch.float16, score="normal"),
+    C("d96_bshd_causal", 1, 257, 257, 8, 2, 96, layout="bshd", is_causal=True),
+]
+
+
+@pytest.mark.parametrize("mode", ["atomic", "det_ds"])
+@pytest.mark.parametrize("cfg", PADDED_D, ids=[c.name for c in PADDED_D])
+def test_padded_head_dims(cuda, cfg, mode):
+    """Head dims other than 64 and 128 (the reference compiles any D,
+    python/fa2.py:33) through the zero-padded kernels: output and gradients
+    against the CPU oracle at the small-shape bar, gradients shaped like the
+    inputs."""
+    atomic, ds_limit = MODES[mode]
+    case = I.make_case(cfg, seed=7)
+    ours = run_ours(case, cfg, atomic=atomic, ds_limit=ds_limit)
+    ref = run_oracle_cpu(case, cfg)
+    for name in ("dq", "dk", "dv", "out"):
+        assert ours[name].shape == ref[name].shape, name
+    check(ours, ref, label=f"padded-D {cfg.name}/{mode}")
+
+
 RAMP = [
     C("ramp_d128_ragged", 1, 320, 200, 4, 2, 128),
     C("ramp_d64_causal", 1, 256, 256, 4, 4, 64, is_causal=True),

@@ -148,3 +148,18 @@ def test_function_refuses_cpu_tensors():
         api.flash_attention_with_4d_mask(q, k, v, None, None, None, False, True, True)
     with pytest.raises(AssertionError):
         api.flash_attention_with_4d_mask(q[0], k, v, None, None, None, False, True, True)
+
+
+def test_kernel_head_dim_padding_rule():
+    """Head dims the kernels are built for run as they are; others up to 128 run
+    at the next built one (zero-padded, exact); larger ones are passed through for
+    the library to reject."""
+    from tilelang_fa2_4d_mask import fa2
+
+    assert fa2.KERNEL_HEAD_DIMS == (64, 128)
+    assert [fa2.kernel_head_dim(d) for d in (8, 32, 63, 64, 65, 96, 112, 128)] == [64, 64, 64, 64, 128, 128, 128, 128]
+    assert fa2.kernel_head_dim(160) == 160 and fa2.kernel_head_dim(256) == 256
+    x = torch.randn(2, 3, 4, 96)
+    y = fa2._pad_head_dim(x, 128)
+    assert y.shape == (2, 3, 4, 128) and torch.equal(y[..., :96], x) and not y[..., 96:].any()
+    assert fa2._pad_head_dim(x, 96) is x
