@@ -265,6 +265,40 @@ def test_dead_rows_from_scores(cuda, cfg):
             assert torch.isnan(ours["dk"][0, 0]).all()   # every key is kept by row 17
 
 
+SDPA_CASES = [
+    C("sdpa_mha_d128", 2, 256, 256, 4, 4, 128),
+    C("sdpa_gqa_causal_d64", 1, 384, 384, 8, 2, 64, is_causal=True),
+    C("sdpa_mask_d128", 1, 200, 300, 4, 2, 128, mask="bernoulli"),
+]
+
+
+@pytest.mark.parametrize("cfg", SDPA_CASES, ids=[c.name for c in SDPA_CASES])
+def test_sdpa_cross_check(cuda, cfg):
+    """The reference's SDPA comparison (precision_check.py:89-107, 247-263) on
+    the GPU: torch's scaled_dot_product_attention (math backend, float32 on the
+    device, K/V repeated over the query-head group, a bool mask as keep mask)
+    against ours through autograd, output and gradients at the small-shape bar.
+    A second, independent reference beside the eager oracle."""
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    dev = torch.device("cuda:0")
+    case = I.make_case(cfg, seed=11)
+    ours = run_ours(case, cfg, atomic=False)
+    G = cfg.Hq // cfg.Hk
+    q = case["q_bhsd"].to(dev).float().requires_grad_(True)
+    k = case["k_bhsd"].to(dev).float().requires_grad_(True)
+    v = case["v_bhsd"].to(dev).float().requires_grad_(True)
+    kk, vv = (x.repeat_interleave(G, dim=1) for x in (k, v))
+    mask = None if case["mask"] is None else case["mask"].to(dev)
+    assert not torch.backends.cuda.matmul.allow_tf32
+    with sdpa_kernel(SDPBackend.MATH):
+        o = torch.nn.functional.scaled_dot_product_attention(q, kk, vv, attn_mask=mask, is_causal=cfg.is_causal,
+                                                             scale=cfg.D ** -0.5)
+    o.backward(case["grad_bhsd"].to(dev).float())
+    ref = {"out": o.detach().cpu(), "dq": q.grad.cpu(), "dk": k.grad.cpu(), "dv": v.grad.cpu()}
+    check(ours, ref, label=f"sdpa {cfg.name}")
+
+
 # head dims the kernels are not built for: zero-padded to 64 / 128 by the host
 PADDED_D = [
     C("d32_gqa", 1, 192, 256, 4, 2, 32),
