@@ -25,6 +25,27 @@ __device__ __forceinline__ uint32_t nz4(uint32_t x) {
   return ((t * 0x01020408u) >> 24) & 0xfu;  // gathered into bits 0..3 (no carries)
 }
 
+// 32x32 bit transpose across each 32-lane half of a wave: lane r holds word r
+// of the matrix (bit c = column c); afterwards lane c holds column c (bit r =
+// row r).  Five block-swap stages (16, 8, 4, 2, 1): the lane with bit j clear
+// takes its partner's low j-bit groups into its high ones, the partner the
+// reverse; partner values come from ds_swizzle (xor j within 32 lanes).
+template <int J>
+__device__ __forceinline__ uint32_t transpose_stage(uint32_t a, bool hi, uint32_t m) {
+  const uint32_t p = (uint32_t)__builtin_amdgcn_ds_swizzle((int)a, (J << 10) | 0x1f);
+  const uint32_t sh = hi ? (p >> J) : (p << J);
+  const uint32_t keep = hi ? ~m : m;   // bits of a that stay
+  return (a & keep) | (sh & ~keep);
+}
+__device__ __forceinline__ uint32_t transpose32(uint32_t a, int l32) {
+  a = transpose_stage<16>(a, (l32 & 16) != 0, 0x0000ffffu);
+  a = transpose_stage<8>(a, (l32 & 8) != 0, 0x00ff00ffu);
+  a = transpose_stage<4>(a, (l32 & 4) != 0, 0x0f0f0f0fu);
+  a = transpose_stage<2>(a, (l32 & 2) != 0, 0x33333333u);
+  a = transpose_stage<1>(a, (l32 & 1) != 0, 0x55555555u);
+  return a;
+}
+
 // Grid (key chunk of 1024, row block of 32, plane).  Thread t reads rows
 // t/32 + 8 i (i = 0..3), keys 32 (t%32) .. +31 of the chunk: a wave reads two
 // whole 1 KB row segments per instruction pair, and every word written (bits
@@ -75,18 +96,17 @@ __global__ __launch_bounds__(256) void mask_bits_kernel(const MaskArgs a) {
   }
   __syncthreads();
 
-  // transposed: thread t -> keys kc0 + t + 256 j (j = 0..3), the row word of
-  // this block's 32 rows; the 32 keys of a key block fill one 128-byte line
+  // transposed: each half-wave turns the 32 row words of one key block into
+  // the 32 key words (bit r = row r0 + r), four passes of two blocks per wave;
+  // the 32 keys of a key block fill one 128-byte line
   const int s = r0 / 32;
+  const int wv = tid >> 6, l32 = tid & 31, hw = (tid >> 5) & 1;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int kl = tid + 256 * j, kk = kc0 + kl;
-    if (kk < Tk) {
-      uint32_t w = 0;
-#pragma unroll 8
-      for (int r = 0; r < 32; ++r) w |= ((words[r][kl >> 5] >> (kl & 31)) & 1u) << r;
-      bitsT[((int64_t)(kk >> 5) * ml.wq + s) * 32 + (kk & 31)] = w;
-    }
+  for (int q = 0; q < 4; ++q) {
+    const int cb = wv * 8 + 2 * q + hw;   // key block within the chunk
+    const uint32_t w = transpose32(words[l32][cb], l32);
+    const int kk = kc0 + 32 * cb + l32;
+    if (kk < Tk) bitsT[((int64_t)(kk >> 5) * ml.wq + s) * 32 + (kk & 31)] = w;
   }
 
   // block states of the 32 key blocks: thread t < 32 -> key block kc0/32 + t
