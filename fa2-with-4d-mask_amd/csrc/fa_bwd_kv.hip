@@ -102,6 +102,13 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
   const int h_first = kvh * a.G + g0, h_end = h_first + gsz;
   const int qstart = CAUSAL && !MASK ? (kt0 / kStep) * kStep : 0;   // rows above the block are masked
   const int nst = qstart < Tq ? (Tq - qstart + kStep - 1) / kStep : 0;
+  // Causal without a mask walks each head's steps downwards, from the last
+  // one (first row qfirst) to the one at the diagonal (qstart): the workgroups
+  // of a (batch, kv-head) that run together then read the same Q/dO rows at
+  // the same time (from L2), where upwards each would start at its own
+  // diagonal.  Otherwise steps go upwards from qfirst = qstart.
+  constexpr bool DESC = CAUSAL && !MASK;
+  const int qfirst = DESC && nst > 0 ? qstart + kStep * (nst - 1) : qstart;
   auto kv_list = [&](int h) __attribute__((always_inline)) -> const int32_t* {
     const int pm = mask_plane(a.ml, b, h);
     return (const int32_t*)(a.mws + a.ml.lkv + pm * a.ml.plkv) + (int64_t)kt * (1 + a.ml.nq32);
@@ -199,9 +206,9 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
   const uint32_t q_rec = (uint32_t)((int64_t)(Tq - 1) * a.qst * 2 + ROWB);
   const uint32_t d_rec = (uint32_t)((int64_t)(Tq - 1) * a.dst * 2 + ROWB);
   const uint32_t inc_q = (uint32_t)(kStep * a.qst * 2), inc_d = (uint32_t)(kStep * a.dst * 2);
-  const uint32_t so_q0 = (uint32_t)qstart * (uint32_t)a.qst * 2, so_d0 = (uint32_t)qstart * (uint32_t)a.dst * 2;
-  int ld_it = 0, ld_h = kvh * a.G + g0, ld_qs = qstart;
-  uint32_t so_q = so_q0, so_d = so_d0, so_l = (uint32_t)qstart * 4;
+  const uint32_t so_q0 = (uint32_t)qfirst * (uint32_t)a.qst * 2, so_d0 = (uint32_t)qfirst * (uint32_t)a.dst * 2;
+  int ld_it = 0, ld_h = kvh * a.G + g0, ld_qs = qfirst;
+  uint32_t so_q = so_q0, so_d = so_d0, so_l = (uint32_t)qfirst * 4;
   Cursor ldc = cursor0();
   const T* q_head = (const T*)a.q + b * a.qsb + (int64_t)ld_h * a.qsh;
   const T* d_head = (const T*)a.dout + b * a.dsb + (int64_t)ld_h * a.dsh;
@@ -257,16 +264,23 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
       }
       return;
     }
-    ld_qs += kStep;
-    so_q += inc_q;
-    so_d += inc_d;
-    so_l += kStep * 4;
-    if (ld_qs >= Tq) {
+    if constexpr (DESC) {
+      ld_qs -= kStep;
+      so_q -= inc_q;
+      so_d -= inc_d;
+      so_l -= kStep * 4;
+    } else {
+      ld_qs += kStep;
+      so_q += inc_q;
+      so_d += inc_d;
+      so_l += kStep * 4;
+    }
+    if (DESC ? ld_qs < qstart : ld_qs >= Tq) {
       ++ld_h;
-      ld_qs = qstart;
+      ld_qs = qfirst;
       so_q = so_q0;
       so_d = so_d0;
-      so_l = (uint32_t)qstart * 4;
+      so_l = (uint32_t)qfirst * 4;
       q_head += a.qsh;
       d_head += a.dsh;
       l_head += Tq;
@@ -294,7 +308,7 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
   };
 
   // ---- step being computed: head it_h, first row it_qs (advanced per step) -----------
-  int it_h = kvh * a.G + g0, it_qs = qstart;
+  int it_h = kvh * a.G + g0, it_qs = qfirst;
   Cursor itc = cursor0();
   if constexpr (MASK) {
     it_h = min(itc.h, h_end - 1);
@@ -339,7 +353,7 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
   // tile bytes are chunk-major (chunk c of key row k at c 512 + k 16): store t
   // writes chunks 2 t + hf, i.e. one contiguous kilobyte of whole lines
   const uint32_t ds_vo = (uint32_t)(hf * 512 + l32 * 16);
-  const int64_t ds_h0 = ((int64_t)b * a.Hq + it_h - ds_u0) * a.ds_plane + ds_row(qstart >> 5, a.nk32, CAUSAL) + kb32;
+  const int64_t ds_h0 = ((int64_t)b * a.Hq + it_h - ds_u0) * a.ds_plane + ds_row(qfirst >> 5, a.nk32, CAUSAL) + kb32;
   const uint16_t* it_ptr = (const uint16_t*)a.ds + ds_h0 * 1024;
   auto ds_rs = __builtin_amdgcn_make_buffer_rsrc((void*)a.ds, (short)0, 0, 0x00020000);
   // descriptor of step j's tile, then advance (it_h, it_qs, it_tile) to step j+1
@@ -365,11 +379,16 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
     }
     const bool ok = ds_on && j < n && (!CAUSAL || kb32 <= s);
     ds_rs = __builtin_amdgcn_make_buffer_rsrc((void*)it_ptr, (short)0, ok ? 2048 : 0, 0x00020000);
-    it_qs += kStep;
-    it_ptr += (int64_t)(CAUSAL ? min(s + 1, a.nk32) : a.nk32) * 1024;
-    if (it_qs >= Tq) {
+    if constexpr (DESC) {
+      it_qs -= kStep;
+      it_ptr -= (int64_t)min(s, a.nk32) * 1024;   // row s-1 holds min(s, nk32) tiles
+    } else {
+      it_qs += kStep;
+      it_ptr += (int64_t)(CAUSAL ? min(s + 1, a.nk32) : a.nk32) * 1024;
+    }
+    if (DESC ? it_qs < qstart : it_qs >= Tq) {
       ++it_h;
-      it_qs = qstart;
+      it_qs = qfirst;
       it_ptr = (const uint16_t*)a.ds + (ds_h0 + (int64_t)(it_h - (kvh * a.G + g0)) * a.ds_plane) * 1024;
     }
   };
