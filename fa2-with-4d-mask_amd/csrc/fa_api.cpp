@@ -274,6 +274,10 @@ int fa_fwd(const FaFwdParams* p) {
   if (p->k_stride_t < 0 || p->k_stride_t >= (1LL << 24) || p->v_stride_t < 0 || p->v_stride_t >= (1LL << 24))
     return fail(FA_ERR_STRIDE, "k/v time strides (%lld, %lld) must lie in [0, 2^24) elements",
                 (long long)p->k_stride_t, (long long)p->v_stride_t);
+  // ... and a wave's 32 score rows through one buffer with 32-bit offsets.
+  if (p->score && (31 * p->score_stride_q + (int64_t)p->seqlen_k + 64) * 4 >= (1LL << 32))
+    return fail(FA_ERR_STRIDE, "score query stride %lld: 32 score rows must span less than 4 GiB",
+                (long long)p->score_stride_q);
 
   fa::FwdArgs a{};
   a.q = p->q; a.k = p->k; a.v = p->v; a.o = p->o; a.lse = p->lse;

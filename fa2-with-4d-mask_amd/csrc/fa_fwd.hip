@@ -73,14 +73,6 @@ template <int D> __device__ __forceinline__ int swz_v(int r) {
   return D == 128 ? ((r & 3) << 2) : (((r >> 1) & 1) << 2);
 }
 
-__device__ __forceinline__ f32x4 load_score4(const float* row, int kk, int Tk, bool vec) {
-  if (vec && kk + 4 <= Tk) return *(const f32x4*)(row + kk);
-  f32x4 r;
-#pragma unroll
-  for (int t = 0; t < 4; ++t) r[t] = row[min(kk + t, Tk - 1)];
-  return r;
-}
-
 template <typename T>
 __device__ __forceinline__ u32x2 pack4(float x0, float x1, float x2, float x3) {
   typedef T T4 __attribute__((ext_vector_type(4)));
@@ -338,9 +330,16 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
     vaddr[nb] = opaque(lds0 + VOFF + tr_row * ROWB + ((((c >> 3) ^ swz_v<D>(tr_row))) * 16) + (c & 7) * 2);
   }
 
-  const float* srow = nullptr;
-  if constexpr (SCORE) srow = a.score + b * a.ssb + h * a.ssh + (int64_t)qrow_c * a.ssq;
-  const bool svec = a.score_vec != 0;
+  // Score of the wave's rows through one buffer descriptor from the wave's
+  // first (clamped) row, whose range ends with the wave's last row: lane
+  // offset = its row + 16 bytes per half-wave (+ the tile's keys); keys past
+  // Tk read the next row or, past the last row, zeros (never kept: they are
+  // masked below).  The host keeps the range below 2^32 bytes.
+  const int srow0 = min(q0 + 32 * __builtin_amdgcn_readfirstlane(wave), Tq - 1);   // wave-uniform
+  const __amdgpu_buffer_rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc(
+      SCORE ? (void*)(a.score + b * a.ssb + h * a.ssh + (int64_t)srow0 * a.ssq) : nullptr, (short)0,
+      SCORE ? (int)(((int64_t)min(Tq - 1 - srow0, 31) * a.ssq + Tk) * 4) : 0, 0x00020000);
+  const uint32_t soff_row = (uint32_t)((int64_t)(qrow_c - srow0) * a.ssq * 4) + hf * 16;
   const float c2 = a.scale_log2;
 
   f32x16 oacc[NB];
@@ -373,6 +372,29 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
     }
   };
   f32x4 sreg[SCORE ? 8 : 1];       // score of the tile in flight
+  // With a score: position p's list entry, mask bits and score, loaded at
+  // the start of M(p) and used in V(p).
+  auto fetch_cur = [&](int p) __attribute__((always_inline)) {     // position p < nt_w
+    int t = p;
+    if constexpr (MASK) {
+      const int e = ent_at(p);
+      t = e & 0x7fffffff;
+      mpart = e >= 0;
+      mreg[0] = mreg[1] = ~0u;
+      if (mpart) {
+        const u32x2 w = *(const u32x2*)(mbits + 2 * t);
+        mreg[0] = w[0] >> (4 * hf);
+        mreg[1] = w[1] >> (4 * hf);
+      }
+    }
+    tile_cur = t;
+    const uint32_t so = soff_row + (uint32_t)(t * BN * 4);   // range-checked: in the lane offset
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int gi = 0; gi < 4; ++gi)
+        sreg[kb * 4 + gi] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(srs, so + (kb * 32 + gi * 8) * 4, 0, 0));
+  };
   float m_run = kNegInf, l_run = 0.f;
 
   // ---- M(p): S(p) = K(p) Q^T and O += V(p-1)^T P(p-1) ---------------------------
@@ -390,29 +412,9 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
       mreg[0] = mreg_nx[0];
       mreg[1] = mreg_nx[1];
       if (p + 1 < nt_w) fetch_mask(p + 1);
-    } else if constexpr (MASK || SCORE) {
-      if (p < nt_w) {
-        int t = p;
-        if constexpr (MASK) {
-          const int e = ent_at(p);
-          t = e & 0x7fffffff;
-          mpart = e >= 0;
-          mreg[0] = mreg[1] = ~0u;
-          if (mpart) {
-            const u32x2 w = *(const u32x2*)(mbits + 2 * t);
-            mreg[0] = w[0] >> (4 * hf);
-            mreg[1] = w[1] >> (4 * hf);
-          }
-        }
-        tile_cur = t;
-        if constexpr (SCORE) {
-          const int k0 = t * BN;
-#pragma unroll
-          for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-            for (int gi = 0; gi < 4; ++gi) sreg[kb * 4 + gi] = load_score4(srow, k0 + kb * 32 + gi * 8 + hf * 4, Tk, svec);
-        }
-      }
+    }
+    if constexpr (SCORE) {
+      if (p < nt_w) fetch_cur(p);
     }
     __builtin_amdgcn_s_setprio(2);
     // The two independent chains interleaved, S op t = (kb = t%2, ds = t/2),
@@ -483,21 +485,34 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
     }
     const bool edge = (MASK && mpart) || a.zero_scale || (k0 + BN > Tk) || (CAUSAL && k0 + BN - 1 > q0w);
     if (edge) {
+      // Keep word of each 32-key half: bit 8 gi + t <-> key k0 + 32 kb +
+      // 8 gi + 4 hf + t; keys at or past Tk (causal: past the row) are a
+      // suffix of the bit positions.  Each entry then costs a sign-extended
+      // bit extract and one bitwise select against -inf (scale 0: against 0
+      // for the kept logits, in a copy of its own).
+      const int lim = CAUSAL ? min(Tk, qrow + 1) : Tk;
+      auto apply = [&](auto ZEROc) __attribute__((always_inline)) {
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+        for (int kb = 0; kb < 2; ++kb) {
+          const int n = lim - (k0 + 32 * kb + 4 * hf);
+          uint32_t keepw = n >= 32 ? ~0u : (n <= 0 ? 0u : (1u << n) - 1u);
+          if constexpr (MASK) keepw &= mreg[kb];
 #pragma unroll
-        for (int gi = 0; gi < 4; ++gi) {
-          const int kk = k0 + kb * 32 + gi * 8 + hf * 4;
+          for (int gi = 0; gi < 4; ++gi)
 #pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            const int key = kk + t;
-            bool keep = key < Tk;
-            if constexpr (CAUSAL) keep = keep && (key <= qrow);
-            if constexpr (MASK) keep = keep && ((mreg[kb] >> (8 * gi + t)) & 1u) != 0;
-            const float sv = sacc[kb][gi * 4 + t];
-            sacc[kb][gi * 4 + t] = keep ? (a.zero_scale ? 0.f : sv) : kNegInf;
-          }
+            for (int t = 0; t < 4; ++t) {
+              const uint32_t m = (uint32_t)((int32_t)(keepw << (31 - (8 * gi + t))) >> 31);
+              // (through a float copy: this compiler's bit_cast of a vector
+              // element operand reads element 0)
+              const float f = decltype(ZEROc)::value ? 0.f : sacc[kb][gi * 4 + t];
+              const uint32_t sv = __builtin_bit_cast(uint32_t, f);
+              sacc[kb][gi * 4 + t] = __builtin_bit_cast(float, (sv & m) | (0xff800000u & ~m));
+              asm volatile("" : "+v"(keepw));   // one entry at a time (no 32 live masks)
+            }
         }
+      };
+      if (a.zero_scale) apply(IC<1>{});
+      else apply(IC<0>{});
     }
     // The mask/score registers are consumed: loads issued from here on do not
     // delay this wave's next wait for them.

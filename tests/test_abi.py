@@ -134,6 +134,7 @@ FWD_ERRORS = [
     (dict(lse=None), 1, "lse is NULL"),
     (dict(mask=FAKE, mask_stride_q=-1), 5, "non-negative"),
     (dict(score=FAKE, score_stride_h=-4), 5, "non-negative"),
+    (dict(score=FAKE, score_stride_q=1 << 26), 5, "32 score rows"),
     (dict(mask=FAKE), 8, "prepared workspace"),
     (dict(mask=FAKE, mask_ws=FAKE + 16), 5, "mask_ws must be 256-byte aligned"),
 ]

@@ -138,6 +138,9 @@ SMALL = [
       extra={"packed": {"lo": 40, "hi": 160}}),
     C("alibi_sparse", 1, 256, 256, 4, 4, 128, mask="sparse_diag", mask_heads=4, score="alibi_noise"),
     C("fp16_mask_score_d64", 1, 200, 200, 4, 2, 64, torch.float16, mask="bernoulli", score="normal"),
+    # score rows of 203 floats (not 16-byte aligned), a partial last key tile
+    C("score_unaligned_ragged", 1, 200, 203, 4, 2, 128, mask="bernoulli", score="normal"),
+    C("score_causal_ragged", 1, 333, 203, 4, 2, 128, is_causal=True, score="normal"),
     # BASELINE configs[0] (C) at its shape, B1 Hq4 Hk2 T256 D64 causal, in the
     # GPU dtypes (its fp32 form is the CPU oracle's own plumbing case)
     C("C_shape_bf16", 1, 256, 256, 4, 2, 64, is_causal=True),
