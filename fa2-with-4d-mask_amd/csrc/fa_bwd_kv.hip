@@ -329,12 +329,21 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
       }
     }
     if constexpr (SCORE) {
-      // padding steps reread the last real step's rows (harmless)
+      // padding steps reread the last real step's rows (harmless).  Element
+      // (g, t) is row it_qs + 8 g + 4 hf + t: a lane pointer per step plus a
+      // uniform row offset per element; on a step that reaches past Tq the
+      // rows are clamped to Tq - 1 (their P is 0: LSE = +inf)
       const int h = live ? it_h : kvh * a.G + g0 + gsz - 1;
+      const float* pl = a.score + b * a.ssb + h * a.ssh + (int64_t)(it_qs + 4 * hf) * a.ssq + kc;
+      if (it_qs + 32 <= Tq) {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int q = min(it_qs + 8 * (i >> 2) + 4 * hf + (i & 3), Tq - 1);
-        sreg[i] = a.score[b * a.ssb + h * a.ssh + (int64_t)q * a.ssq + kc];
+        for (int i = 0; i < 16; ++i) sreg[i] = pl[(int64_t)(8 * (i >> 2) + (i & 3)) * a.ssq];
+      } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int q = min(it_qs + 8 * (i >> 2) + 4 * hf + (i & 3), Tq - 1);
+          sreg[i] = a.score[b * a.ssb + h * a.ssh + (int64_t)q * a.ssq + kc];
+        }
       }
     }
   };
@@ -454,13 +463,19 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
       asm volatile("" : "+v"(p));
       return p;
     };
+    // keep word of the step (EDGE): bit 8 gi + t <-> entry (gi, t); causal
+    // keeps the bit positions from dkq on.  An entry then costs a
+    // sign-extended bit extract and an AND (a dropped p becomes +0).
+    uint32_t keepw = ~0u;
+    if constexpr (EDGE) {
+      if constexpr (MASK) keepw = mreg;
+      if constexpr (CAUSAL) keepw &= dkq <= 0 ? ~0u : (dkq >= 32 ? 0u : ~0u << dkq);
+    }
     auto elem_fin = [&](int i, float p) __attribute__((always_inline)) {
       const int gi = i >> 2, t = i & 3;
       if constexpr (EDGE) {
-        bool keep = true;
-        if constexpr (CAUSAL) keep = dkq <= 8 * gi + t;
-        if constexpr (MASK) keep = keep && ((mreg >> (8 * gi + t)) & 1u) != 0;
-        p = keep ? p : 0.f;
+        const uint32_t m = (uint32_t)((int32_t)(keepw << (31 - (8 * gi + t))) >> 31);
+        p = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, p) & m);
       }
       sacc[PJ][i] = p;
       pacc[PJ][i] = p * pacc[PJ][i];   // P (dP - Delta); the factor scale goes into dK
