@@ -98,32 +98,25 @@ __global__ __launch_bounds__(256) void mask_bits_kernel(const MaskArgs a) {
 
   // transposed: each half-wave turns the 32 row words of one key block into
   // the 32 key words (bit r = row r0 + r), four passes of two blocks per wave;
-  // the 32 keys of a key block fill one 128-byte line
+  // the 32 keys of a key block fill one 128-byte line.  The block's state
+  // comes from the same words by two ballots over the half-wave: some valid
+  // key keeps some valid row (any), every valid key keeps every valid row
+  // (all).
   const int s = r0 / 32;
   const int wv = tid >> 6, l32 = tid & 31, hw = (tid >> 5) & 1;
+  const int nr = min(32, Tq - r0);
+  const uint32_t vrows = nr >= 32 ? 0xffffffffu : ((1u << nr) - 1u);
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const int cb = wv * 8 + 2 * q + hw;   // key block within the chunk
-    const uint32_t w = transpose32(words[l32][cb], l32);
+    const uint32_t w = transpose32(words[l32][cb], l32) & vrows;
     const int kk = kc0 + 32 * cb + l32;
-    if (kk < Tk) bitsT[((int64_t)(kk >> 5) * ml.wq + s) * 32 + (kk & 31)] = w;
-  }
-
-  // block states of the 32 key blocks: thread t < 32 -> key block kc0/32 + t
-  if (tid < 32) {
-    const int kb = kc0 / 32 + tid;
-    if (kb < ml.nk32) {
-      const int nk = min(32, Tk - 32 * kb);
-      const uint32_t vm = nk >= 32 ? 0xffffffffu : ((1u << nk) - 1u);
-      const int nr = min(32, Tq - r0);
-      uint32_t any = 0, all = vm;
-      for (int r = 0; r < nr; ++r) {
-        const uint32_t w = words[r][tid] & vm;
-        any |= w;
-        all &= w;
-      }
-      blk[(int64_t)s * ml.nk32 + kb] = any == 0 ? 0 : (all == vm ? 2 : 1);
-    }
+    const bool valid = kk < Tk;
+    if (valid) bitsT[((int64_t)(kk >> 5) * ml.wq + s) * 32 + (kk & 31)] = w;
+    const uint32_t any = (uint32_t)(__builtin_amdgcn_ballot_w64(valid && w != 0) >> (32 * hw));
+    const uint32_t notall = (uint32_t)(__builtin_amdgcn_ballot_w64(valid && w != vrows) >> (32 * hw));
+    const int kb = kc0 / 32 + cb;
+    if (l32 == 0 && kb < ml.nk32) blk[(int64_t)s * ml.nk32 + kb] = any == 0 ? 0 : (notall == 0 ? 2 : 1);
   }
 }
 
