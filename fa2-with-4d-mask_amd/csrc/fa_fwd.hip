@@ -511,8 +511,25 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
             }
         }
       };
-      if (a.zero_scale) apply(IC<1>{});
-      else apply(IC<0>{});
+      if constexpr (MASK || SCORE || CAUSAL) {
+        if (a.zero_scale) apply(IC<1>{});
+        else apply(IC<0>{});
+      } else {
+        // no mask, score or causality: only the last, partial key tile and
+        // scale 0 come here (per-entry selects: the plain kernel's register
+        // assignment stays as it is without the keep-word code)
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int gi = 0; gi < 4; ++gi) {
+            const int kk = k0 + kb * 32 + gi * 8 + hf * 4;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+              const float sv = sacc[kb][gi * 4 + t];
+              sacc[kb][gi * 4 + t] = kk + t < Tk ? (a.zero_scale ? 0.f : sv) : kNegInf;
+            }
+          }
+      }
     }
     // The mask/score registers are consumed: loads issued from here on do not
     // delay this wave's next wait for them.
