@@ -606,6 +606,10 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
       if (p >= 1 && p - 1 < nt_w) v_step(p - 1, stage);
       else stage();
     }
+    // D = 64 (one group: M then V in every wave): the phases are scheduled
+    // apart, which keeps the live registers of one phase at a time (150
+    // instead of 239 without a score; with a score 256 and spills before)
+    if constexpr (D == 64) __builtin_amdgcn_sched_barrier(0);
     if (grp == 0) {
       if (p < nt_w) v_step(p, stage);
       else stage();
