@@ -46,9 +46,11 @@ __device__ __forceinline__ uint32_t transpose32(uint32_t a, int l32) {
   return a;
 }
 
-// Grid (key chunk of 1024, row block of 32, plane).  Thread t reads rows
-// t/32 + 8 i (i = 0..3), keys 32 (t%32) .. +31 of the chunk: a wave reads two
-// whole 1 KB row segments per instruction pair, and every word written (bits
+// Grid (key chunk of 1024, row block of 32, plane).  Wave w reads rows
+// 8 w .. 8 w + 7 of the block, one instruction per row: lane l the 16 bytes
+// of keys 16 l .. 16 l + 15 of the chunk, so that each load instruction
+// covers one whole 1 KB row segment; lane pairs (2 c, 2 c + 1) join their 16
+// bits into the row word of key block c.  Every word written (bits
 // row-major, bitsT per key block) lands in full 128-byte lines.
 __global__ __launch_bounds__(256) void mask_bits_kernel(const MaskArgs a) {
   __shared__ uint32_t words[kRows][kKeys / 32 + 1];
@@ -62,39 +64,45 @@ __global__ __launch_bounds__(256) void mask_bits_kernel(const MaskArgs a) {
   uint32_t* bitsT = (uint32_t*)(a.ws + ml.bitsT + pm * ml.pbitsT);
   uint8_t* blk = (uint8_t*)(a.ws + ml.blk + pm * ml.pblk);
 
-  const int c = tid & 31, kbase = kc0 + 32 * c, wcol = kc0 / 32 + c;
-  // all rows' bytes are loaded before any word is stored (the stores could
-  // alias the mask as far as the compiler knows)
-  const bool vec = a.vec16 && kbase + 32 <= Tk;
-  u32x4 x[4][2];
+  {
+    const int wv = tid >> 6, l = tid & 63, k16 = kc0 + 16 * l;
+    // all rows' bytes are loaded before any word is stored (the stores could
+    // alias the mask as far as the compiler knows)
+    const bool vec = a.vec16 && k16 + 16 <= Tk;
+    u32x4 x[8];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int row = r0 + (tid >> 5) + 8 * i;
-    x[i][0] = x[i][1] = u32x4{0, 0, 0, 0};
-    if (vec && row < Tq) {
-      const uint8_t* p = src + row * a.msq + kbase;
-      x[i][0] = *(const u32x4*)p;
-      x[i][1] = *(const u32x4*)(p + 16);
+    for (int i = 0; i < 8; ++i) {
+      const int row = r0 + 8 * wv + i;
+      x[i] = u32x4{0, 0, 0, 0};
+      if (vec && row < Tq) x[i] = *(const u32x4*)(src + row * a.msq + k16);
     }
-  }
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int rl = (tid >> 5) + 8 * i, row = r0 + rl;
-    uint32_t w = 0;
-    if (vec) {
+    for (int i = 0; i < 8; ++i) {
+      const int rl = 8 * wv + i, row = r0 + rl;
+      uint32_t h = 0;
+      if (vec) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) w |= nz4(x[i][0][j]) << (4 * j);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) w |= nz4(x[i][1][j]) << (16 + 4 * j);
-    } else if (row < Tq && kbase < Tk) {
-      const uint8_t* p = src + row * a.msq + kbase;
-      const int n = min(32, Tk - kbase);
-      for (int j = 0; j < n; ++j) w |= (uint32_t)(p[j] != 0) << j;
+        for (int j = 0; j < 4; ++j) h |= nz4(x[i][j]) << (4 * j);
+      } else if (row < Tq && k16 < Tk) {
+        const uint8_t* p = src + row * a.msq + k16;
+        const int n = min(16, Tk - k16);
+        for (int j = 0; j < n; ++j) h |= (uint32_t)(p[j] != 0) << j;
+      }
+      // lane 2 c takes lane 2 c + 1's 16 bits (ds_swizzle xor 1 within 32 lanes)
+      const uint32_t hi = (uint32_t)__builtin_amdgcn_ds_swizzle((int)h, (1 << 10) | 0x1f);
+      if ((l & 1) == 0) words[rl][l >> 1] = h | (hi << 16);
     }
-    words[rl][c] = w;
-    if (row < Tq && wcol < ml.wk) bits[(int64_t)row * ml.wk + wcol] = w;   // padding words are written as 0
   }
   __syncthreads();
+  {
+    // row-major words: thread t stores rows t/32 + 8 i, key block t%32
+    const int c = tid & 31, wcol = kc0 / 32 + c;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int rl = (tid >> 5) + 8 * i, row = r0 + rl;
+      if (row < Tq && wcol < ml.wk) bits[(int64_t)row * ml.wk + wcol] = words[rl][c];   // padding words are 0
+    }
+  }
 
   // transposed: each half-wave turns the 32 row words of one key block into
   // the 32 key words (bit r = row r0 + r), four passes of two blocks per wave;
