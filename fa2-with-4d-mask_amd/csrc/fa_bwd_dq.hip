@@ -22,9 +22,9 @@
 // operand of dQ^T = K^T dS^T with lane l = position p directly, so perm only
 // matters when dQ rows are stored.
 //
-// Work decomposition: one workgroup of NW (4 or 8) waves per (64 NW query
-// rows, head, batch[, key split]); wave w owns query steps 2 NW qb + 2 w, + 1
-// (64 rows) and walks the key steps of 32.  Written dQ (deterministic mode,
+// Work decomposition: one workgroup of NW (4 or 8) waves per (32 NW ST query
+// rows, head, batch[, key split]); wave w owns the ST (1 or 2) query steps
+// NW ST qb + ST w, ... (32 ST rows) and walks the key steps of 32.  Written dQ (deterministic mode,
 // and atomic mode when the row blocks give every CU a workgroup): one
 // workgroup covers every key step and stores dQ.  Atomic (use_atomic_backward
 // on smaller grids): the key steps are cut into dq_split contiguous ranges
@@ -33,7 +33,7 @@
 // adds a partial per 64-key block, python/fa2.py:295-297, which on this part
 // is bound by atomic throughput).  Per step the workgroup stages one K tile
 // (shared, XOR-swizzled for the transpose reads) and each wave its two dS
-// tiles (private) through registers into LDS, kSets steps ahead of use; the
+// tile(s) (private) through registers into LDS, kSets steps ahead of use; the
 // kernel is bound by the HBM reads of the dS tiles, so it keeps as many bytes
 // in flight as registers allow at two waves per SIMD.
 #include "fa_common.h"
@@ -45,17 +45,20 @@ namespace {
 
 using namespace pipe;
 
-constexpr int kDqSteps = 2;                           // 32-row query steps per wave
 constexpr int kSets = 3;                              // register staging sets: tiles in flight
+constexpr unsigned kCuCount = 256;                    // compute units of the part
 
-// NW waves per workgroup, 64 query rows each.  NW = 8 (deterministic, head
-// dim 128, no mask, enough rows to give every CU a workgroup) shares each
-// step's K tile among 512 query rows, which halves its L2 reads (15 % faster
-// at T 8192); else NW = 4 (the prepared-mask lists are built per 256-row
-// block; with atomics 8 waves were 3-5 % slower).
-template <typename T, int D, bool CAUSAL, bool MASK, bool ATOMIC, int NW>
+// NW waves per workgroup, ST query steps (32 ST rows) each.  NW = 8, ST = 2
+// (deterministic, head dim 128, no mask, enough rows to give every CU a
+// workgroup) shares each step's K tile among 512 query rows, which halves its
+// L2 reads (15 % faster at T 8192).  With a mask the row blocks are the
+// prepared lists' 256 rows: NW = 8, ST = 1 (deterministic, head dim 128: twice
+// the waves, and dS bytes in flight, of NW = 4, ST = 2).  Else NW = 4, ST = 2
+// (with atomics 8 waves were 3-5 % slower).
+template <typename T, int D, bool CAUSAL, bool MASK, bool ATOMIC, int NW, int ST>
 __global__ __launch_bounds__(NW * 64, 2) void dq_ds_kernel(const BwdArgs a) {
   constexpr int kDqWaves = NW;
+  constexpr int kDqSteps = ST;                       // 32-row query steps per wave
   constexpr int kDqRows = kDqWaves * kDqSteps * 32;   // query rows per workgroup
   using V8 = typename Vec8<T>::type;
   constexpr int NB = D / 32, CH = D / 8, ROWB = 2 * D;
@@ -66,11 +69,11 @@ __global__ __launch_bounds__(NW * 64, 2) void dq_ds_kernel(const BwdArgs a) {
   constexpr int UD = DSW / (64 * 16);                // dS chunks per lane
   constexpr int OS = D + 8;                          // epilogue staging stride (elements)
   static_assert(UK >= 1 && UD >= 1, "tile split");
-  static_assert(kDqWaves * 32 * OS * 2 <= 2 * BUFB, "epilogue staging fits");
-  static_assert(kDqRows == (NW == 8 ? kDqDsRowsWide : kDqDsRows) && (!MASK || NW == 4),
+  static_assert(kDqRows == (NW == 8 && ST == 2 ? kDqDsRowsWide : kDqDsRows) && (!MASK || kDqRows == kDqDsRows),
                 "row blocks as the host and the prepared-mask lists assume");
   constexpr int OSF = D + 4;                         // atomic epilogue: fp32 staging stride
-  constexpr int SMEM = ATOMIC && kDqWaves * 32 * OSF * 4 > 2 * BUFB ? kDqWaves * 32 * OSF * 4 : 2 * BUFB;
+  constexpr int SMEM0 = kDqWaves * 32 * OS * 2 > 2 * BUFB ? kDqWaves * 32 * OS * 2 : 2 * BUFB;   // + epilogue staging
+  constexpr int SMEM = ATOMIC && kDqWaves * 32 * OSF * 4 > SMEM0 ? kDqWaves * 32 * OSF * 4 : SMEM0;
   __shared__ __attribute__((aligned(1024))) char smem[SMEM];
 
   // ---- which (batch, head, 256-row block) ----------------------------------------
@@ -349,12 +352,24 @@ template <typename T, int D, bool CAUSAL, bool ATOMIC>
 hipError_t launch_a(const BwdArgs& a, hipStream_t s) {
   const dim3 grid((unsigned)(a.nbk * a.G * a.nqt * (ATOMIC ? a.dq_split : 1)));
   if (a.mask) {
-    hipLaunchKernelGGL((dq_ds_kernel<T, D, CAUSAL, true, ATOMIC, 4>), grid, dim3(256), 0, s, a);
+    // With a mask the row blocks stay at 256 rows (the prepared lists are per
+    // 256-row block).  Deterministic at head dim 128 with fewer blocks than
+    // two per CU (the 4-wave kernel's residency): 8 waves of one 32-row step
+    // each, twice the waves and dS tiles in flight (S config: -13 %); with
+    // more blocks two 4-wave workgroups per CU already overlap (P: the 8-wave
+    // kernel, one workgroup per CU, was 10 % slower).
+    if constexpr (D == 128 && !ATOMIC) {
+      if (grid.x < 2 * kCuCount) {
+        hipLaunchKernelGGL((dq_ds_kernel<T, D, CAUSAL, true, ATOMIC, 8, 1>), grid, dim3(512), 0, s, a);
+        return hipGetLastError();
+      }
+    }
+    hipLaunchKernelGGL((dq_ds_kernel<T, D, CAUSAL, true, ATOMIC, 4, 2>), grid, dim3(256), 0, s, a);
   } else if constexpr (D == 128 && !ATOMIC) {
-    if (a.dq_rows == kDqDsRowsWide) hipLaunchKernelGGL((dq_ds_kernel<T, D, CAUSAL, false, ATOMIC, 8>), grid, dim3(512), 0, s, a);
-    else hipLaunchKernelGGL((dq_ds_kernel<T, D, CAUSAL, false, ATOMIC, 4>), grid, dim3(256), 0, s, a);
+    if (a.dq_rows == kDqDsRowsWide) hipLaunchKernelGGL((dq_ds_kernel<T, D, CAUSAL, false, ATOMIC, 8, 2>), grid, dim3(512), 0, s, a);
+    else hipLaunchKernelGGL((dq_ds_kernel<T, D, CAUSAL, false, ATOMIC, 4, 2>), grid, dim3(256), 0, s, a);
   } else {
-    hipLaunchKernelGGL((dq_ds_kernel<T, D, CAUSAL, false, ATOMIC, 4>), grid, dim3(256), 0, s, a);
+    hipLaunchKernelGGL((dq_ds_kernel<T, D, CAUSAL, false, ATOMIC, 4, 2>), grid, dim3(256), 0, s, a);
   }
   return hipGetLastError();
 }
