@@ -70,14 +70,6 @@ int check_mask_score(const uint8_t* mask, int64_t msb, int64_t msh, int64_t msq,
   return FA_OK;
 }
 
-// 32-bit (mask) / 128-bit (score) loads need every row start aligned.
-int mask_vec_ok(const uint8_t* m, int64_t sb, int64_t sh, int64_t sq) {
-  return m && ((uintptr_t)m % 4 == 0) && sb % 4 == 0 && sh % 4 == 0 && sq % 4 == 0;
-}
-int score_vec_ok(const float* s, int64_t sb, int64_t sh, int64_t sq) {
-  return s && ((uintptr_t)s % 16 == 0) && sb % 4 == 0 && sh % 4 == 0 && sq % 4 == 0;
-}
-
 fa::MaskLayout layout_of(int32_t B, int32_t Hq, int32_t Tq, int32_t Tk, int64_t msb, int64_t msh) {
   return fa::mask_layout(B, Hq, Tq, Tk, msb == 0, msh == 0);
 }
@@ -293,8 +285,6 @@ int fa_fwd(const FaFwdParams* p) {
   a.nqt = (p->seqlen_q + fa::fwd_block_rows() - 1) / fa::fwd_block_rows();
   float sl2b;
   fill_scales(p->scale, &a.scale_log2, &a.qsign, &a.zero_scale, &sl2b);
-  a.mask_vec = mask_vec_ok(p->mask, p->mask_stride_b, p->mask_stride_h, p->mask_stride_q);
-  a.score_vec = score_vec_ok(p->score, p->score_stride_b, p->score_stride_h, p->score_stride_q);
   if (p->mask) {
     a.mws = (const char*)p->mask_ws;
     a.ml = layout_of(p->batch, p->heads_q, p->seqlen_q, p->seqlen_k, p->mask_stride_b, p->mask_stride_h);
@@ -412,8 +402,6 @@ static fa::BwdArgs bwd_args(const FaBwdParams* p, int split) {
   a.scale = p->scale;
   float sl2f;
   fill_scales(p->scale, &sl2f, &a.qsign, &a.zero_scale, &a.scale_log2);
-  a.mask_vec = mask_vec_ok(p->mask, p->mask_stride_b, p->mask_stride_h, p->mask_stride_q);
-  a.score_vec = score_vec_ok(p->score, p->score_stride_b, p->score_stride_h, p->score_stride_q);
   // dS tiles of the deterministic path
   a.nq32 = (p->seqlen_q + 31) / 32;
   a.nk32 = (p->seqlen_k + 31) / 32;

@@ -89,8 +89,6 @@ struct FwdArgs {
   float scale_log2;     // |scale| * log2(e)  (1 when zero_scale)
   float qsign;          // -1 folds a negative scale into Q and Score
   int zero_scale;       // scale == 0: every kept logit is 0
-  int mask_vec;         // mask rows 4-byte aligned: 32-bit loads allowed
-  int score_vec;        // score rows 16-byte aligned: 128-bit loads allowed
   const char* mws;      // prepared mask (with a mask)
   MaskLayout ml;
 };
@@ -134,7 +132,6 @@ struct BwdArgs {
   float scale_log2;     // |scale| * log2(e)  (1 when zero_scale)
   float qsign;
   int zero_scale;
-  int mask_vec, score_vec;
   // dS tiles (written by the dK/dV kernel, read by the dQ kernel); null when
   // dQ is recomputed instead.  Tile (b, h, s, kb) holds dS / scale of query
   // rows 32 s.. and keys 32 kb.. as 32 key rows of 32 16-bit values stored
