@@ -298,15 +298,26 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
       lds_write16_at(soff_v[u] + vbuf * TILEB, stg[IPW + u]);
     }
   };
-  // Tile written straight through the staging registers (prologue).
-  // (positions 0 and 1: tiles from the scalar-loaded first entries)
-  auto put_tile = [&](bool is_k, int p, int buf) __attribute__((always_inline)) {
-    const int t = MASK ? (fl[1 + p] & 0x7fffffff) : p;
-    const auto rs = is_k ? rsrc_tile(kp, a.kst, t, p < nt) : rsrc_tile(vp, a.vst, t, p < nt);
+  // Prologue tiles K(0), K(1), V(0) of list positions 0 and 1 (from the
+  // scalar-loaded first entries), straight to LDS: the loads of all three
+  // first, then the LDS writes (the compiler does not move a buffer load
+  // above an LDS store, so interleaved they waited for each tile in turn).
+  auto put_tiles = [&]() __attribute__((always_inline)) {
+    const int t0 = MASK ? (fl[1] & 0x7fffffff) : 0, t1 = MASK ? (fl[2] & 0x7fffffff) : 1;
+    const auto rk0 = rsrc_tile(kp, a.kst, t0, 0 < nt), rk1 = rsrc_tile(kp, a.kst, t1, 1 < nt);
+    const auto rv0 = rsrc_tile(vp, a.vst, t0, 0 < nt);
+    u32x4 xk0[IPW], xk1[IPW], xv0[IPW];
 #pragma unroll
     for (int u = 0; u < IPW; ++u) {
-      const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(rs, is_k ? goff_k[u] : goff_v[u], 0, 0);
-      lds_write16_at((is_k ? soff_k[u] : soff_v[u]) + buf * TILEB, x);
+      xk0[u] = __builtin_amdgcn_raw_buffer_load_b128(rk0, goff_k[u], 0, 0);
+      xk1[u] = __builtin_amdgcn_raw_buffer_load_b128(rk1, goff_k[u], 0, 0);
+      xv0[u] = __builtin_amdgcn_raw_buffer_load_b128(rv0, goff_v[u], 0, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < IPW; ++u) {
+      lds_write16_at(soff_k[u], xk0[u]);
+      lds_write16_at(soff_k[u] + TILEB, xk1[u]);
+      lds_write16_at(soff_v[u], xv0[u]);
     }
   };
 
@@ -349,8 +360,11 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
   V8 pk[4];                        // P(p) packed, B operand of the next M step
 #pragma unroll
   for (int kk = 0; kk < 4; ++kk) pk[kk] = V8{};
-  // mask bits of the tile in flight: word kb holds keys 32 kb + 8 gi + t of
-  // this lane (shifted by 4 hf), all ones for a fully kept tile
+  // mask bits of the tile in flight as loaded: word kb holds keys 32 kb ..
+  // 32 kb + 31 of this lane's row (used, shifted by 4 hf, only when mpart).
+  // Loaded unconditionally (every listed tile's words exist) and used only
+  // in the softmax phase: a conditional load whose result is used at once
+  // made the compiler wait for all of the wave's loads right there.
   uint32_t mreg[2] = {~0u, ~0u};
   int tile_cur = 0;                // key tile of the tile in flight
   bool mpart = false;              // the tile in flight has dropped entries
@@ -364,12 +378,9 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
     const int e = p == 0 ? fl[1] : ent_at(p);
     tile_nx = e & 0x7fffffff;
     mpart_nx = e >= 0;
-    mreg_nx[0] = mreg_nx[1] = ~0u;
-    if (mpart_nx) {
-      const u32x2 w = *(const u32x2*)(mbits + 2 * tile_nx);
-      mreg_nx[0] = w[0] >> (4 * hf);
-      mreg_nx[1] = w[1] >> (4 * hf);
-    }
+    const u32x2 w = *(const u32x2*)(mbits + 2 * tile_nx);
+    mreg_nx[0] = w[0];
+    mreg_nx[1] = w[1];
   };
   f32x4 sreg[SCORE ? 8 : 1];       // score of the tile in flight
   // With a score: position p's list entry, mask bits and score, loaded at
@@ -380,12 +391,9 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
       const int e = ent_at(p);
       t = e & 0x7fffffff;
       mpart = e >= 0;
-      mreg[0] = mreg[1] = ~0u;
-      if (mpart) {
-        const u32x2 w = *(const u32x2*)(mbits + 2 * t);
-        mreg[0] = w[0] >> (4 * hf);
-        mreg[1] = w[1] >> (4 * hf);
-      }
+      const u32x2 w = *(const u32x2*)(mbits + 2 * t);
+      mreg[0] = w[0];
+      mreg[1] = w[1];
     }
     tile_cur = t;
     const uint32_t so = soff_row + (uint32_t)(t * BN * 4);   // range-checked: in the lane offset
@@ -496,7 +504,7 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
         for (int kb = 0; kb < 2; ++kb) {
           const int n = lim - (k0 + 32 * kb + 4 * hf);
           uint32_t keepw = n >= 32 ? ~0u : (n <= 0 ? 0u : (1u << n) - 1u);
-          if constexpr (MASK) keepw &= mreg[kb];
+          if constexpr (MASK) keepw &= mpart ? mreg[kb] >> (4 * hf) : ~0u;
 #pragma unroll
           for (int gi = 0; gi < 4; ++gi)
 #pragma unroll
@@ -574,9 +582,7 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
   if constexpr (MPRE) {
     if (nt_w > 0) fetch_mask(0);
   }
-  put_tile(true, 0, 0);
-  put_tile(true, 1, 1);
-  put_tile(false, 0, 0);
+  put_tiles();   // K(0), K(1), V(0)
   load_batch(batch_rsrc(0));
   lds_barrier();
 
