@@ -224,8 +224,17 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
   const bool live0 = n > 0;
   auto rq_c = rs_of(q_head, q_rec, live0), rd_c = rs_of(d_head, d_rec, live0);
   auto rl_c = rs_of(l_head, (uint32_t)Tq * 4, live0), re_c = rs_of(e_head, (uint32_t)Tq * 4, live0);
-  auto load_next = [&](auto Sc) __attribute__((always_inline)) {
+  // Mask words of the steps in flight (MASK): the transposed-bits word of
+  // step t at this lane's key as loaded, with the step's tile (four steps
+  // ahead), into slot t % 4; shifted by 4 hf (bit 8 gi + t' = row
+  // 8 gi + 4 hf + t' of the step) and zeroed past the last step when used.
+  // Loaded unconditionally (padding steps read the head's first words) and
+  // used only four steps later: a conditional load whose result is used at
+  // once made the compiler wait for all of the wave's loads right there.
+  uint32_t mq[MASK ? 4 : 1] = {};
+  auto load_next = [&](auto Sc, auto Qc) __attribute__((always_inline)) {
     constexpr int S = decltype(Sc)::value;
+    constexpr int Q = decltype(Qc)::value;
     const bool live = ld_it < n;
     if constexpr (MASK) {
       // position the loads at the cursor's step (rows past Tq read as zeros)
@@ -241,6 +250,8 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
         l_head = a.lse + ((int64_t)b * a.Hq + ld_h) * Tq;
         e_head = a.delta + ((int64_t)b * a.Hq + ld_h) * Tq;
       }
+      const uint32_t* bt = (const uint32_t*)(a.mws + a.ml.bitsT + mask_plane(a.ml, b, ld_h) * a.ml.pbitsT);
+      mq[Q] = bt[((int64_t)(kc >> 5) * a.ml.wq + (ld_qs >> 5)) * 32 + (kc & 31)];
     }
     const auto rq = MASK ? rs_of(q_head, q_rec, live) : rq_c;
     const auto rd = MASK ? rs_of(d_head, d_rec, live) : rd_c;
@@ -315,19 +326,9 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
     it_qs = n > 0 ? kStep * list_at(itc) : 0;
   }
 
-  // ---- mask / score of a step (lane's 16 query rows at its key) -----------------
-  // mask: the step's word of the transposed bits at this lane's key, shifted
-  // so that bit 8 gi + t is row 8 gi + 4 hf + t of the step.
-  uint32_t mreg = 0;
+  // ---- score of a step (lane's 16 query rows at its key) -----------------------
   float sreg[SCORE ? 16 : 1];
   auto load_ms = [&](bool live) __attribute__((always_inline)) {
-    if constexpr (MASK) {
-      mreg = 0;
-      if (live) {
-        const uint32_t* bt = (const uint32_t*)(a.mws + a.ml.bitsT + mask_plane(a.ml, b, it_h) * a.ml.pbitsT);
-        mreg = bt[((int64_t)(kc >> 5) * a.ml.wq + (it_qs >> 5)) * 32 + (kc & 31)] >> (4 * hf);
-      }
-    }
     if constexpr (SCORE) {
       // padding steps reread the last real step's rows (harmless).  Element
       // (g, t) is row it_qs + 8 g + 4 hf + t: a lane pointer per step plus a
@@ -366,13 +367,13 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
   const uint16_t* it_ptr = (const uint16_t*)a.ds + ds_h0 * 1024;
   auto ds_rs = __builtin_amdgcn_make_buffer_rsrc((void*)a.ds, (short)0, 0, 0x00020000);
   // descriptor of step j's tile, then advance (it_h, it_qs, it_tile) to step j+1
-  auto next_step = [&](int j) __attribute__((always_inline)) {
+  auto next_step = [&](int j, uint32_t mreg) __attribute__((always_inline)) {
     const int s = it_qs >> 5;
     if constexpr (MASK) {
       // tiles of blocks without a kept entry are neither stored nor read: the
-      // block holds one iff a lane's transposed mask word (loaded for this
-      // step; the lanes of half 0 hold the whole words of the 32 keys) is
-      // not 0 -- the block state the dQ kernel reads, without a scalar load
+      // block holds one iff a lane's transposed mask word (of this step; the
+      // lanes of half 0 hold the whole words of the 32 keys) is not 0 -- the
+      // block state the dQ kernel reads, without a scalar load
       const bool any = __builtin_amdgcn_ballot_w64(mreg != 0u) != 0;
       const bool ok = ds_on && j < n && (!CAUSAL || kb32 <= s) && any;
       const int64_t tile = ((int64_t)b * a.Hq + it_h - ds_u0) * a.ds_plane + ds_row(s, a.nk32, CAUSAL) + kb32;
@@ -419,7 +420,7 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
   // (buffer (BUF+2)%4, parity PAR) -- one interleaved MFMA stream, with the
   // P/dS VALU work of step it-1 (parity PAR^1) threaded through it.  EDGE:
   // some (row, key) of the step is masked (causal diagonal or a mask).
-  auto iter = [&](auto BUFc, auto EDGEc, int j) __attribute__((always_inline)) {
+  auto iter = [&](auto BUFc, auto EDGEc, int j, uint32_t mreg) __attribute__((always_inline)) {
     // j: step whose P/dS is computed now; S/dP of j+1; dV/dK of j-1
     constexpr int BUF = decltype(BUFc)::value;          // buffer of step j
     constexpr bool EDGE = decltype(EDGEc)::value != 0;
@@ -552,7 +553,7 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
       }
     }
     // next step's dS descriptor and position, then its mask / score
-    next_step(j);
+    next_step(j, mreg);
     load_ms(j + 1 < n);
   };
 
@@ -563,10 +564,10 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
     lds_wr16(sw[u] + 3 * QTILE, u32x4{0, 0, 0, 0});
     lds_wr16(sw[u] + DOFF + 3 * QTILE, u32x4{0, 0, 0, 0});
   }
-  load_next(IC<0>{}); store_tile(0, IC<0>{});   // tile 0
-  load_next(IC<1>{}); store_tile(1, IC<1>{});   // tile 1
-  load_next(IC<0>{});                           // tile 2 staged (set 0)
-  load_next(IC<1>{});                           // tile 3 staged (set 1)
+  load_next(IC<0>{}, IC<0>{}); store_tile(0, IC<0>{});   // tile 0
+  load_next(IC<1>{}, IC<1>{}); store_tile(1, IC<1>{});   // tile 1
+  load_next(IC<0>{}, IC<2>{});                           // tile 2 staged (set 0)
+  load_next(IC<1>{}, IC<3>{});                           // tile 3 staged (set 1)
   load_ms(n > 0);
   lds_barrier();
   // S / dP of step 0 (parity 0); the dP chain starts from -Delta
@@ -595,11 +596,13 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
   auto step = [&](auto BUFc, int j) __attribute__((always_inline)) {
     constexpr int BUF = decltype(BUFc)::value;
     store_tile((BUF + 2) % kNBuf, IC<BUF & 1>{});   // tile j+2 (staged two iterations ago)
-    load_next(IC<BUF & 1>{});                       // tile j+4
+    // mask word of step j (loaded with tile j), before slot BUF is refilled
+    const uint32_t mcur = MASK && j < n ? mq[MASK ? BUF : 0] >> (4 * hf) : 0u;
+    load_next(IC<BUF & 1>{}, IC<BUF>{});            // tile j+4 (its mask word into slot BUF)
     // with a mask the keep test runs per entry on every step (a second copy of
     // the body for steps without dropped entries would not fit the register
     // budget); causal alone clears packed entries on the diagonal steps
-    iter(BUFc, IC<MASK ? 1 : 0>{}, j);
+    iter(BUFc, IC<MASK ? 1 : 0>{}, j, mcur);
     lds_barrier();
   };
   int n4 = n > 0 ? (n + 4) & ~3 : 0;
