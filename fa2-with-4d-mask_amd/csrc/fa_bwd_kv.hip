@@ -119,23 +119,34 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
     if (a.ml.Hm == 1) n = gsz * kv_list(h_first)[0];
     else for (int h = h_first; h < h_end; ++h) n += kv_list(h)[0];
   }
-  // When the workgroup's heads share one list (a mask broadcast over the
-  // heads, or one head per workgroup) of at most 128 steps, it sits in two
-  // registers (lane i of lreg_v[w]: position 64 w + i), read with readlane
-  // instead of a scalar load per step.
-  const bool lreg = MASK && (a.ml.Hm == 1 || gsz == 1) && a.ml.nq32 <= 128;
+  // Step lists (MASK) are read through a window of 128 positions of one
+  // head's list held in two registers (lane i of lreg_v[w]: position
+  // win_base + 64 w + i), read with readlane.  The window moves (two vector
+  // loads and one wait) when the load cursor leaves it: once per 128 steps
+  // and per head, not at a head switch when the heads share one list (a mask
+  // broadcast over them).  A scalar load per step instead cost a wait for
+  // all of the wave's loads each step.
+  const bool shared_list = MASK && a.ml.Hm == 1;
   int32_t lreg_v[MASK ? 2 : 1] = {};
-  if constexpr (MASK) {
-    if (lreg) {
-      const int32_t* l0 = kv_list(h_first);
-      const int cnt0 = l0[0];
+  int win_h = -1, win_base = -128;
+  auto win_load = [&](int h, int base) __attribute__((always_inline)) {
+    const int32_t* l = kv_list(h);
+    const int cnt = l[0];
 #pragma unroll
-      for (int w = 0; w < 2; ++w) lreg_v[w] = 64 * w + lane < cnt0 ? l0[1 + 64 * w + lane] : 0;
+    for (int w = 0; w < 2; ++w) {
+      const int pos = base + 64 * w + lane;
+      lreg_v[w] = pos < cnt ? l[1 + pos] : 0;
     }
-  }
+    // consumed here, inside the (rarely taken) branch: otherwise the loads
+    // are still pending where the branch rejoins, and every step waits there
+    // for all of the wave's loads before reading the window
+    asm volatile("" : "+v"(lreg_v[0]), "+v"(lreg_v[1]));
+    win_h = h;
+    win_base = base;
+  };
   // List cursor (MASK): head h, position idx in that head's list of cnt
   // steps; seek() moves past exhausted and empty lists.  list_at(c): the
-  // query step at the cursor.
+  // query step at the cursor (c.h < h_end).
   struct Cursor { int h, idx, cnt; const int32_t* lst; };
   auto seek = [&](Cursor& c) __attribute__((always_inline)) {
     while (c.idx >= c.cnt && c.h < h_end) {
@@ -145,12 +156,12 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
     }
   };
   auto list_at = [&](const Cursor& c) __attribute__((always_inline)) -> int {
-    if (lreg) {
-      const int lo = __builtin_amdgcn_readlane(lreg_v[0], c.idx & 63);
-      const int hi = __builtin_amdgcn_readlane(lreg_v[1], c.idx & 63);
-      return c.idx < 64 ? lo : hi;
-    }
-    return c.lst[1 + c.idx];
+    const int base = c.idx & ~127;
+    if (base != win_base || (c.h != win_h && !shared_list)) win_load(c.h, base);
+    const int r = c.idx - win_base;
+    const int lo = __builtin_amdgcn_readlane(lreg_v[0], r & 63);
+    const int hi = __builtin_amdgcn_readlane(lreg_v[1], r & 63);
+    return r < 64 ? lo : hi;
   };
   auto cursor0 = [&]() __attribute__((always_inline)) -> Cursor {
     Cursor c{h_first, 0, 0, nullptr};
@@ -232,6 +243,9 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
   // used only four steps later: a conditional load whose result is used at
   // once made the compiler wait for all of the wave's loads right there.
   uint32_t mq[MASK ? 4 : 1] = {};
+  // ... and the step's position, (head << 16) | (first row / 32), read by
+  // the dS-store / score position four steps later (one list cursor only)
+  int pq[MASK ? 4 : 1] = {};
   auto load_next = [&](auto Sc, auto Qc) __attribute__((always_inline)) {
     constexpr int S = decltype(Sc)::value;
     constexpr int Q = decltype(Qc)::value;
@@ -252,6 +266,7 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
       }
       const uint32_t* bt = (const uint32_t*)(a.mws + a.ml.bitsT + mask_plane(a.ml, b, ld_h) * a.ml.pbitsT);
       mq[Q] = bt[((int64_t)(kc >> 5) * a.ml.wq + (ld_qs >> 5)) * 32 + (kc & 31)];
+      pq[Q] = (ld_h << 16) | (ld_qs >> 5);
     }
     const auto rq = MASK ? rs_of(q_head, q_rec, live) : rq_c;
     const auto rd = MASK ? rs_of(d_head, d_rec, live) : rd_c;
@@ -367,7 +382,7 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
   const uint16_t* it_ptr = (const uint16_t*)a.ds + ds_h0 * 1024;
   auto ds_rs = __builtin_amdgcn_make_buffer_rsrc((void*)a.ds, (short)0, 0, 0x00020000);
   // descriptor of step j's tile, then advance (it_h, it_qs, it_tile) to step j+1
-  auto next_step = [&](int j, uint32_t mreg) __attribute__((always_inline)) {
+  auto next_step = [&](int j, uint32_t mreg, int pos_next) __attribute__((always_inline)) {
     const int s = it_qs >> 5;
     if constexpr (MASK) {
       // tiles of blocks without a kept entry are neither stored nor read: the
@@ -379,12 +394,10 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
       const int64_t tile = ((int64_t)b * a.Hq + it_h - ds_u0) * a.ds_plane + ds_row(s, a.nk32, CAUSAL) + kb32;
       ds_rs = __builtin_amdgcn_make_buffer_rsrc((void*)((uint16_t*)a.ds + tile * 1024), (short)0, ok ? 2048 : 0,
                                                 0x00020000);
-      if (j < n) {
-        ++itc.idx;
-        seek(itc);
-      }
-      it_h = min(itc.h, h_end - 1);
-      it_qs = j + 1 < n ? kStep * list_at(itc) : 0;
+      // step j+1 as the load cursor queued it (padding steps: row 0 of the
+      // last head)
+      it_h = pos_next >> 16;
+      it_qs = kStep * (pos_next & 0xffff);
       return;
     }
     const bool ok = ds_on && j < n && (!CAUSAL || kb32 <= s);
@@ -420,7 +433,7 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
   // (buffer (BUF+2)%4, parity PAR) -- one interleaved MFMA stream, with the
   // P/dS VALU work of step it-1 (parity PAR^1) threaded through it.  EDGE:
   // some (row, key) of the step is masked (causal diagonal or a mask).
-  auto iter = [&](auto BUFc, auto EDGEc, int j, uint32_t mreg) __attribute__((always_inline)) {
+  auto iter = [&](auto BUFc, auto EDGEc, int j, uint32_t mreg, int pos_next) __attribute__((always_inline)) {
     // j: step whose P/dS is computed now; S/dP of j+1; dV/dK of j-1
     constexpr int BUF = decltype(BUFc)::value;          // buffer of step j
     constexpr bool EDGE = decltype(EDGEc)::value != 0;
@@ -553,7 +566,7 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
       }
     }
     // next step's dS descriptor and position, then its mask / score
-    next_step(j, mreg);
+    next_step(j, mreg, pos_next);
     load_ms(j + 1 < n);
   };
 
@@ -598,11 +611,12 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
     store_tile((BUF + 2) % kNBuf, IC<BUF & 1>{});   // tile j+2 (staged two iterations ago)
     // mask word of step j (loaded with tile j), before slot BUF is refilled
     const uint32_t mcur = MASK && j < n ? mq[MASK ? BUF : 0] >> (4 * hf) : 0u;
+    const int pnext = pq[MASK ? (BUF + 1) % 4 : 0];   // position of step j+1 (loaded with tile j+1)
     load_next(IC<BUF & 1>{}, IC<BUF>{});            // tile j+4 (its mask word into slot BUF)
     // with a mask the keep test runs per entry on every step (a second copy of
     // the body for steps without dropped entries would not fit the register
     // budget); causal alone clears packed entries on the diagonal steps
-    iter(BUFc, IC<MASK ? 1 : 0>{}, j, mcur);
+    iter(BUFc, IC<MASK ? 1 : 0>{}, j, mcur, pnext);
     lds_barrier();
   };
   int n4 = n > 0 ? (n + 4) & ~3 : 0;
