@@ -116,31 +116,39 @@ __global__ __launch_bounds__(NW * 64, 2) void dq_ds_kernel(const BwdArgs a) {
   const int chunk = (nstep + nsp - 1) / nsp;
   const int jb = min(nstep, ksp * chunk);
   const int nloc = min(nstep, jb + chunk) - jb;
-  // With a mask, positions jl < 128 of this workgroup's range sit in two
-  // registers (lane i of ents[w]: position 64 w + i), read with readlane:
-  // the key step, and in bits 30 and 31 whether the dK/dV kernel stored the
-  // tile of this wave's query step 0 and 1 (step below Tq, on or below the
-  // causal diagonal, block holding a kept entry).  Later positions use
-  // scalar loads.  (Per-step scalar loads of the list and block states cost
-  // a quarter of the kernel's time at the packed-document config.)
+  // With a mask, 128 positions jl of this workgroup's range at a time sit in
+  // two registers (lane i of ents[w]: position ebase + 64 w + i), read with
+  // readlane: the key step, and in bits 30 and 31 whether the dK/dV kernel
+  // stored the tile of this wave's query step 0 and 1 (step below Tq, on or
+  // below the causal diagonal, block holding a kept entry).  The window moves
+  // every 128 steps.  (Per-step scalar loads of the list and block states
+  // cost a quarter of the kernel's time at the packed-document config, and
+  // made each step wait for all of the wave's loads.)
   int32_t ents[MASK ? 2 : 1] = {};
-  if constexpr (MASK) {
+  int ebase = -128;
+  auto fill_ents = [&](int base) __attribute__((always_inline)) {
 #pragma unroll
     for (int w = 0; w < 2; ++w) {
-      const int jl = 64 * w + lane;
+      const int jl = base + 64 * w + lane;
+      int32_t e = 0;
       if (jl < nloc) {
         const int kb = dql[1 + jb + jl];
-        int32_t e = kb;
+        e = kb;
 #pragma unroll
         for (int i = 0; i < kDqSteps; ++i) {
           const int s = s0 + i;
           const bool ok = s < nq32 && (!CAUSAL || kb <= s) && blk[(int64_t)s * nk32 + kb] != 0;
           e |= ok ? (int32_t)(1u << (30 + i)) : 0;
         }
-        ents[w] = e;
       }
+      ents[w] = e;
     }
-  }
+    // consumed here, inside the branch that moves the window: loads still
+    // pending where it rejoins would make every step wait for all loads
+    asm volatile("" : "+v"(ents[0]), "+v"(ents[1]));
+    ebase = base;
+  };
+  if constexpr (MASK) fill_ents(0);
 
   // ---- LDS addresses ---------------------------------------------------------------
   const uint32_t lds0 = (uint32_t)(uintptr_t)(FA_LDS char*)smem;
@@ -200,18 +208,13 @@ __global__ __launch_bounds__(NW * 64, 2) void dq_ds_kernel(const BwdArgs a) {
     if constexpr (MASK) {
       kb = 0;
       if (inr) {
-        if (jl < 128) {
-          const int32_t e = __builtin_amdgcn_readlane(ents[jl >> 6], jl & 63);
-          kb = e & 0x3fffffff;
-          okb = (uint32_t)e >> 30;
-        } else {
-          kb = dql[1 + j];
-#pragma unroll
-          for (int i = 0; i < kDqSteps; ++i) {
-            const int s = s0 + i;
-            if (s < nq32 && (!CAUSAL || kb <= s) && blk[(int64_t)s * nk32 + kb] != 0) okb |= 1u << i;
-          }
-        }
+        if ((jl & ~127) != ebase) fill_ents(jl & ~127);
+        const int r = jl - ebase;
+        const int32_t lo = __builtin_amdgcn_readlane(ents[0], r & 63);
+        const int32_t hi = __builtin_amdgcn_readlane(ents[1], r & 63);
+        const int32_t e = r < 64 ? lo : hi;
+        kb = e & 0x3fffffff;
+        okb = (uint32_t)e >> 30;
       }
     }
     const int rows = inr ? min(32, Tk - kb * 32) : 0;

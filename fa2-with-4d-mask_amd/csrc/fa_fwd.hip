@@ -193,26 +193,39 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
   // every instantiation gets the same control flow and register assignment);
   // with a mask every wave walks the whole list (causality is applied per key)
   const int nt_w = (int)opaque((uint32_t)(CAUSAL && !MASK ? min(nt, (min(Tk, q0w + 32) + BN - 1) / BN) : nt));
-  // List entries: positions 0..127 sit in two registers (lane i of ents[w]
-  // holds position 64 w + i) and are read with readlane, so that walking the
-  // list costs no scalar-memory waits in the pipeline; later positions load
-  // them.
+  // List entries: a window of 128 positions sits in two registers (lane i
+  // of ents[w] holds position ebase + 64 w + i) and is read with readlane,
+  // so that walking the list costs no memory waits in the pipeline; it moves
+  // by 64 positions when a pair would read past it (a pair reads positions
+  // p .. p+3).
   constexpr bool ENTV = MASK;
   constexpr bool MPRE = MASK && !SCORE;   // mask bits fetched a pair ahead (no registers to spare with a score)
   int32_t ents[ENTV ? 2 : 1] = {};
-  if constexpr (ENTV) {
-    // range-checked loads (positions past the row read 0): no wait on the count
-    const auto rl = __builtin_amdgcn_make_buffer_rsrc((void*)flist, (short)0, (1 + a.ml.nft) * 4, 0x00020000);
+  int ebase = 0;
+  // range-checked loads (positions past the row read 0): no wait on the count
+  const auto rl = __builtin_amdgcn_make_buffer_rsrc((void*)flist, (short)0, MASK ? (1 + a.ml.nft) * 4 : 0, 0x00020000);
+  auto fill_ents = [&](int base) __attribute__((always_inline)) {
 #pragma unroll
     for (int w = 0; w < 2; ++w)
-      ents[w] = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(rl, (uint32_t)(1 + 64 * w + lane) * 4, 0, 0);
-  }
-  auto ent_at = [&](int p) __attribute__((always_inline)) -> int32_t {
+      ents[w] = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(rl, (uint32_t)(1 + base + 64 * w + lane) * 4, 0, 0);
+    ebase = base;
+  };
+  if constexpr (ENTV) fill_ents(0);
+  auto move_ents = [&](int p) __attribute__((always_inline)) {   // before pair p's reads
     if constexpr (ENTV) {
-      if (p < 64) return __builtin_amdgcn_readlane(ents[0], p);
-      if (p < 128) return __builtin_amdgcn_readlane(ents[1], p - 64);
+      if (p + 3 >= ebase + 128) {
+        fill_ents(ebase + 64);
+        // consumed inside the branch: loads still pending where it rejoins
+        // would make every pair wait for all of the wave's loads
+        asm volatile("" : "+v"(ents[0]), "+v"(ents[1]));
+      }
     }
-    return flist[1 + p];
+  };
+  auto ent_at = [&](int p) __attribute__((always_inline)) -> int32_t {
+    const int r = p - ebase;
+    const int32_t lo = __builtin_amdgcn_readlane(ents[0], r & 63);
+    const int32_t hi = __builtin_amdgcn_readlane(ents[1], r & 63);
+    return r < 64 ? lo : hi;
   };
   // key tile at list position p < nt
   auto tile_at = [&](int p) __attribute__((always_inline)) -> int {
@@ -601,6 +614,7 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
   auto pair = [&](auto KBc, int p) __attribute__((always_inline)) {
     constexpr int KB = decltype(KBc)::value;   // p % NBUF
     constexpr bool BAR = NBUF == 3 || (KB & 1) != 0;
+    move_ents(p);
     const Rs2 rs = batch_rsrc(p + 1);
     auto stage = [&]() __attribute__((always_inline)) {
       store_batch((KB + 2) % NBUF, (KB + 1) % NBUF);
