@@ -78,7 +78,8 @@ __global__ __launch_bounds__(NW * 64, 2) void dq_ds_kernel(const BwdArgs a) {
 
   // ---- which (batch, head, 256-row block) ----------------------------------------
   // Logical order: kv-head major (the heads of a group share K in L2), longest
-  // causal blocks first.
+  // blocks first: causal blocks from the last one, with a mask by the count of
+  // live key steps.
   const int nqb = a.nqt;
   const int nsp = ATOMIC ? a.dq_split : 1;
   const int nblk = a.nbk * a.G * nqb * nsp;
@@ -89,11 +90,11 @@ __global__ __launch_bounds__(NW * 64, 2) void dq_ds_kernel(const BwdArgs a) {
   const int bkl = W / per_kv;             // unit within this launch's slice
   const int bk = a.bk0 + bkl;
   const int rem = W - bkl * per_kv;
-  const int qb_rev = rem / a.G;
-  const int g = rem - qb_rev * a.G;
-  const int qb = nqb - 1 - qb_rev;
+  const int qb_rank = rem / a.G;
+  const int g = rem - qb_rank * a.G;
   const int b = bk / a.Hk, kvh = bk - b * a.Hk;
   const int h = kvh * a.G + g;
+  const int qb = MASK ? mask_order(a.ml, a.mws, mask_plane(a.ml, b, h), 2)[qb_rank] : nqb - 1 - qb_rank;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, hf = lane >> 5;

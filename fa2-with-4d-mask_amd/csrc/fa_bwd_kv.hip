@@ -67,8 +67,12 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
   const int bk = a.bk0 + bkl;
   const int rem = W - bkl * per_bk;
   const int sp = rem / a.nkt;
-  const int kt = rem - sp * a.nkt;        // ascending = most causal work first
   const int b = bk / a.Hk, kvh = bk - b * a.Hk;
+  // longest workgroups first: key blocks ascending (causal work shrinks with
+  // the block), with a mask by the count of live steps of the group's first head
+  const int kt_rank = rem - sp * a.nkt;
+  const int kt = MASK ? mask_order(a.ml, a.mws, mask_plane(a.ml, b, kvh * a.G + sp * (a.G / a.split)), 1)[kt_rank]
+                      : kt_rank;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, hf = lane >> 5;

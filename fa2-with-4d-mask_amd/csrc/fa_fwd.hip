@@ -129,19 +129,22 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
   __shared__ __attribute__((aligned(1024))) char smem[2 * NBUF * TILEB];
 
   // ---- which (batch, head, query tile) -------------------------------------
-  // Logical order (b, kv-head, [query tile descending, head in group]); with
-  // the XCD remap each XCD works on few kv-heads (K/V stay in its L2) and
-  // causal work is dispatched longest-first.
+  // Logical order (b, kv-head, [query tile rank, head in group]), with a
+  // mask (kv-head, b, ...) so that batches of different mask density mix
+  // on every XCD; with the XCD remap each XCD works on few kv-heads (K/V stay
+  // in its L2), and the longest workgroups are dispatched first: rank r is
+  // query tile nqt-1-r (causal work grows with the tile), with a mask the
+  // tile with the r-th most live key tiles.
   const int nblk = a.B * a.Hq * a.nqt;
   const int W = xcd_remap(blockIdx.x, nblk);
   const int per_kv = a.G * a.nqt;
   const int bk = W / per_kv;
   const int rem = W - bk * per_kv;
-  const int qt_rev = rem / a.G;
-  const int g = rem - qt_rev * a.G;
-  const int qt = a.nqt - 1 - qt_rev;
-  const int b = bk / a.Hk, kvh = bk - b * a.Hk;
+  const int qt_rank = rem / a.G;
+  const int g = rem - qt_rank * a.G;
+  const int b = MASK ? bk % a.B : bk / a.Hk, kvh = MASK ? bk / a.B : bk - b * a.Hk;
   const int h = kvh * a.G + g;
+  const int qt = MASK ? mask_order(a.ml, a.mws, mask_plane(a.ml, b, h), 0)[qt_rank] : a.nqt - 1 - qt_rank;
 
   const int tid = threadIdx.x, lane = tid & 63;
   // D = 64: the softmax phase is over twice the MFMA phase, and the two

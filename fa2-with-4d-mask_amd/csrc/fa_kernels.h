@@ -24,13 +24,16 @@ constexpr int kDqDsRowsWide = 512;   // the same with 8 waves (deterministic, D 
 //                               tiles ascending, bit 31 set when every block is 2
 //   lkv    int32  [nkb][1+nq32] per 128-key block: count, live 32-row steps
 //   ldq    int32  [ndq][1+nk32] per 256-row block: count, live 32-key steps
+//   ord    int32  [nfq + nkb + ndq] the units of lfwd, lkv, ldq (in that order)
+//                               by count, largest first, ties by unit: the
+//                               kernels run their longest workgroups first
 // "Live" folds in causality when the workspace was prepared with is_causal.
 struct MaskLayout {
   int Bm, Hm;
   int nq32, nk32, wk, wq;
   int nfq, nft, nkb, ndq;
-  int64_t bits, bitsT, blk, lfwd, lkv, ldq, total;   // byte offsets of the plane arrays, workspace size
-  int64_t pbits, pbitsT, pblk, plfwd, plkv, pldq;    // per-plane sizes (bytes)
+  int64_t bits, bitsT, blk, lfwd, lkv, ldq, ord, total;   // byte offsets of the plane arrays, workspace size
+  int64_t pbits, pbitsT, pblk, plfwd, plkv, pldq, pord;   // per-plane sizes (bytes)
 };
 
 __host__ __device__ inline int64_t align256(int64_t x) { return (x + 255) & ~(int64_t)255; }
@@ -53,6 +56,7 @@ __host__ __device__ inline MaskLayout mask_layout(int B, int Hq, int Tq, int Tk,
   m.plfwd = (int64_t)m.nfq * (1 + m.nft) * 4;
   m.plkv = (int64_t)m.nkb * (1 + m.nq32) * 4;
   m.pldq = (int64_t)m.ndq * (1 + m.nk32) * 4;
+  m.pord = (int64_t)(m.nfq + m.nkb + m.ndq) * 4;
   const int64_t np = (int64_t)m.Bm * m.Hm;
   m.bits = 0;
   m.bitsT = align256(m.bits + np * m.pbits);
@@ -60,8 +64,15 @@ __host__ __device__ inline MaskLayout mask_layout(int B, int Hq, int Tq, int Tk,
   m.lfwd = align256(m.blk + np * m.pblk);
   m.lkv = align256(m.lfwd + np * m.plfwd);
   m.ldq = align256(m.lkv + np * m.plkv);
-  m.total = align256(m.ldq + np * m.pldq);
+  m.ord = align256(m.ldq + np * m.pldq);
+  m.total = align256(m.ord + np * m.pord);
   return m;
+}
+
+// Count order of list kind `kind` (0 lfwd, 1 lkv, 2 ldq) of plane pm: entry
+// r is the unit with the r-th largest count.
+__host__ __device__ inline const int32_t* mask_order(const MaskLayout& m, const char* ws, int pm, int kind) {
+  return (const int32_t*)(ws + m.ord + pm * m.pord) + (kind == 0 ? 0 : (kind == 1 ? m.nfq : m.nfq + m.nkb));
 }
 
 // Plane of (batch b, query head h).

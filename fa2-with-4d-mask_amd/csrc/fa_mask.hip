@@ -214,6 +214,37 @@ __global__ __launch_bounds__(256) void mask_lists_kernel(const MaskArgs a) {
   if (lane == 0) lst[0] = count;
 }
 
+// One workgroup per (plane, list kind): the units of the lists in count
+// order, largest first, ties by unit (rank of unit i = #{j : c_j > c_i} +
+// #{j < i : c_j = c_i}); counts staged through LDS in chunks.
+constexpr int kOrdChunk = 4096;
+__global__ __launch_bounds__(256) void mask_order_kernel(const MaskArgs a) {
+  const MaskLayout& ml = a.ml;
+  const int pm = blockIdx.x, kind = blockIdx.y, tid = threadIdx.x;
+  const int n = kind == 0 ? ml.nfq : (kind == 1 ? ml.nkb : ml.ndq);
+  const int64_t stride = 1 + (kind == 0 ? ml.nft : (kind == 1 ? ml.nq32 : ml.nk32));
+  const int32_t* cnt = (const int32_t*)(a.ws + (kind == 0 ? ml.lfwd + pm * ml.plfwd
+                                                : (kind == 1 ? ml.lkv + pm * ml.plkv : ml.ldq + pm * ml.pldq)));
+  int32_t* ord = (int32_t*)mask_order(ml, a.ws, pm, kind);
+  __shared__ int32_t cs[kOrdChunk];
+  for (int i0 = 0; i0 < n; i0 += 256) {
+    const int i = i0 + tid;
+    const int ci = i < n ? cnt[i * stride] : 0;
+    int rank = 0;
+    for (int j0 = 0; j0 < n; j0 += kOrdChunk) {
+      const int m = min(kOrdChunk, n - j0);
+      __syncthreads();
+      for (int j = tid; j < m; j += 256) cs[j] = cnt[(j0 + j) * stride];
+      __syncthreads();
+      for (int j = 0; j < m; ++j) {
+        const int cj = cs[j];
+        rank += (cj > ci) | ((cj == ci) & (j0 + j < i));
+      }
+    }
+    if (i < n) ord[rank] = i;
+  }
+}
+
 }  // namespace
 
 hipError_t launch_mask_prepare(const MaskArgs& a, hipStream_t s) {
@@ -225,6 +256,9 @@ hipError_t launch_mask_prepare(const MaskArgs& a, hipStream_t s) {
   if (e != hipSuccess) return e;
   const int64_t nl = (int64_t)ml.Bm * ml.Hm * (ml.nfq + ml.nkb + ml.ndq);
   hipLaunchKernelGGL(mask_lists_kernel, dim3((unsigned)((nl + 3) / 4)), dim3(256), 0, s, a);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(mask_order_kernel, dim3((unsigned)(ml.Bm * ml.Hm), 3), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 

@@ -309,9 +309,9 @@ def test_mask_plan_sizes(lib):
     # config P: mask [2, 1, 4096, 4096] -> batch kept (stride != 0), heads broadcast: 2 planes
     T = 4096
     per = dict(bits=T * 128 * 4, bitsT=128 * 128 * 32 * 4, blk=128 * 128, lfwd=16 * 65 * 4, lkv=32 * 129 * 4,
-               ldq=16 * 129 * 4)
+               ldq=16 * 129 * 4, ord=(16 + 32 + 16) * 4)
     off = 0
-    for k in ("bits", "bitsT", "blk", "lfwd", "lkv", "ldq"):
+    for k in ("bits", "bitsT", "blk", "lfwd", "lkv", "ldq", "ord"):
         off = _a256(off + 2 * per[k])
     assert _mask_bytes(lib, mask_stride_b=T * T) == off
     # broadcast over batch too: one plane; full head extent: 64 planes

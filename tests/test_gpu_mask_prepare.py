@@ -32,6 +32,7 @@ def layout(B, Hq, Tq, Tk, bcast_b, bcast_h):
     m["plfwd"] = m["nfq"] * (1 + m["nft"]) * 4
     m["plkv"] = m["nkb"] * (1 + m["nq32"]) * 4
     m["pldq"] = m["ndq"] * (1 + m["nk32"]) * 4
+    m["pord"] = (m["nfq"] + m["nkb"] + m["ndq"]) * 4
     np_ = m["Bm"] * m["Hm"]
     m["bits"] = 0
     m["bitsT"] = a256(np_ * m["pbits"])
@@ -39,7 +40,8 @@ def layout(B, Hq, Tq, Tk, bcast_b, bcast_h):
     m["lfwd"] = a256(m["blk"] + np_ * m["pblk"])
     m["lkv"] = a256(m["lfwd"] + np_ * m["plfwd"])
     m["ldq"] = a256(m["lkv"] + np_ * m["plkv"])
-    m["total"] = a256(m["ldq"] + np_ * m["pldq"])
+    m["ord"] = a256(m["ldq"] + np_ * m["pldq"])
+    m["total"] = a256(m["ord"] + np_ * m["pord"])
     return m
 
 
@@ -174,3 +176,9 @@ def test_prepared_mask_matches_definition(cuda, B, Hq, Hm, Tq, Tk, causal, kind)
         assert read_lists(ws32, m["lfwd"] + pm * m["plfwd"], m["nfq"], 1 + m["nft"]) == lf, f"fwd lists plane {pm}"
         assert read_lists(ws32, m["lkv"] + pm * m["plkv"], m["nkb"], 1 + m["nq32"]) == lk, f"kv lists plane {pm}"
         assert read_lists(ws32, m["ldq"] + pm * m["pldq"], m["ndq"], 1 + m["nk32"]) == ld, f"dq lists plane {pm}"
+        # units of each list kind by count, largest first, ties by unit
+        got_ord = ws32[(m["ord"] + pm * m["pord"]) // 4:][: m["nfq"] + m["nkb"] + m["ndq"]].tolist()
+        want_ord = []
+        for lists in (lf, lk, ld):
+            want_ord += sorted(range(len(lists)), key=lambda i: (-len(lists[i]), i))
+        assert got_ord == want_ord, f"order plane {pm}"
