@@ -20,7 +20,8 @@ Every (config, output) cell is asserted one of two ways:
   sampled heads: test_bf16_rounding_floor_exceeds_the_strict_bar).  Asserted:
   the HIP result is within the north-star bar of the restatement, and its
   error against the eager oracle is no larger than the restatement's own (mean
-  within 5 %, no more entries above 2e-2).
+  within 5 %, no more entries above 2e-2).  A floor cell that meets the
+  north-star bar against the eager oracle passes on that alone.
 
 Every cell additionally needs NaN positions identical to both oracles'.  (A
 floor cell's entries are within 2e-2 of the restatement, which is as far as a
@@ -115,10 +116,14 @@ def check(ours, ref, rnd, label, strict):
               f"max={derr.max().item():.3e} mean={derr.mean().item():.3e}", flush=True)
         if not nan_ok or not nan_rd:
             failures.append(f"{name}: NaN positions differ")
+        met = err.max().item() <= MAX_ABS and mean <= MEAN_ABS
         if name in strict:
-            if err.max().item() > MAX_ABS or mean > MEAN_ABS:
+            if not met:
                 failures.append(f"{name}: misses the north-star bar (max {err.max().item():.3e}, mean {mean:.3e})")
-        else:
+        elif not met:
+            # a floor cell that meets the bar against eager needs no floor
+            # argument (the fused atomic route rounds dS at another point than
+            # the restatement and lands inside the bar at H causal)
             if derr.max().item() > MAX_ABS or derr.mean().item() > MEAN_ABS:
                 failures.append(f"{name}: not within the north-star bar of the rounding restatement")
             if mean > 1.05 * rmean + 1e-7 or over > rover:
@@ -140,6 +145,31 @@ def test_fullsize_vs_oracle(cuda, name, atomic):
     ours = run_ours(case, cfg, atomic=atomic)
     check(ours, run_oracle(case, cfg), run_rounded(case, cfg), f"{name}/{'atomic' if atomic else 'det'}",
           STRICT[name])
+
+
+NO_WS_CASES = [("H", True), ("H", False), ("H_causal", True), ("H_causal", False)]
+
+
+@pytest.mark.parametrize("name,atomic", NO_WS_CASES,
+                         ids=[f"{n}-{'fused_atomic' if a else 'recompute'}" for n, a in NO_WS_CASES])
+def test_fullsize_without_ds_workspace(cuda, name, atomic):
+    """The backward routes that keep memory O(T) (no dS workspace allowed):
+    atomic mode runs the fused dK/dV kernel that adds dQ with fp32 atomics,
+    the deterministic mode a dQ kernel that recomputes S, P and dP.  The
+    library falls back to them when the dS tiles do not fit the limit; here
+    they are forced at the headline shape and held to the same cells."""
+    import tilelang_fa2_4d_mask.fa2 as fa2mod
+
+    cfg = I.CONFIGS[name]
+    route = "fused atomic" if atomic else "recompute"
+    print(f"case {name} no dS workspace ({route}) B{cfg.B} T{cfg.Tq} Hq{cfg.Hq} Hk{cfg.Hk} D{cfg.D}", flush=True)
+    case = I.make_case(cfg, seed=4, device=cuda)
+    fa2mod.DS_LIMIT_BYTES = -1
+    try:
+        ours = run_ours(case, cfg, atomic=atomic)
+    finally:
+        fa2mod.DS_LIMIT_BYTES = 0
+    check(ours, run_oracle(case, cfg), run_rounded(case, cfg), f"{name}/no-ws/{route}", STRICT[name])
 
 
 def test_fullsize_deterministic_repeatable(cuda):
