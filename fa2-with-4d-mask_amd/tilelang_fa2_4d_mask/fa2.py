@@ -102,6 +102,21 @@ def _kernel_operand(x: torch.Tensor) -> torch.Tensor:
     return x
 
 
+# The backward kernels reach a Q / dO row with a 32-bit byte offset from its
+# head's first row (fa_api.cpp check_bwd: (Tq + 32) rows must span < 4 GiB).
+ROW_SPAN_LIMIT = 1 << 32
+
+
+def _rows_reachable(x: torch.Tensor, Tq: int) -> torch.Tensor:
+    """x itself when (Tq + 32) of its rows span less than ROW_SPAN_LIMIT bytes,
+    else a head-major copy (the rows of a head contiguous, D elements apart).
+    A token-major layout with many heads reaches the limit at ~2^32 / (2 H D)
+    tokens (524k at 32 heads of 128); head-major it moves to 2^31 / D rows."""
+    if (Tq + 32) * 2 * abs(x.stride(1)) < ROW_SPAN_LIMIT:
+        return x
+    return x.transpose(1, 2).contiguous().transpose(1, 2)
+
+
 def _bthd_strides(x: torch.Tensor) -> tuple:
     st = _norm_strides(x)
     return st[0], st[1], st[2]
@@ -271,7 +286,8 @@ def _backward_impl(do, q, k, v, O, LSE, mask, score, mask_ws, mst, sst, scale: f
         dK.zero_()
         dV.zero_()
         return tuple(x[..., :D_in].contiguous() for x in (dQ, dK, dV))
-    do = _kernel_operand(do.to(q.dtype))
+    do = _rows_reachable(_kernel_operand(do.to(q.dtype)), Tq)
+    q = _rows_reachable(q, Tq)
     p = _ext.FaBwdParams()
     p.batch, p.seqlen_q, p.seqlen_k, p.heads_q, p.heads_k, p.head_dim = B, Tq, Tk, Hq, Hk, D
     p.scale = scale

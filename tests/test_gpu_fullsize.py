@@ -259,3 +259,41 @@ def test_long_keys_head_broadcast_mask(cuda):
         ours = run_ours(case, cfg, atomic=atomic)
         check(ours, run_oracle(case, cfg), run_rounded(case, cfg), f"long_keys_mask/{'atomic' if atomic else 'det'}",
               STRICT[cfg.name])
+
+
+def test_long_rows_past_32bit_offsets(cuda):
+    """Tq 540000 at 32 query heads of 128 in token-major storage: a head's Q
+    and dO rows span 4.4 GB, past the 32-bit byte offsets with which the
+    backward kernels reach a row, so the host re-lays both head-major for the
+    backward.  Checked against the eager oracle (with the small-shape bar of
+    tests/test_gpu_parity.py: 64 keys per row make single entries large) and
+    bitwise against the same problem handed over head-major by the caller,
+    where no re-layout happens.  Tk 64 keeps the oracle cheap."""
+    cfg = I.AttnConfig("long_rows", 1, 540000, 64, 32, 8, 128)
+    print("case long_rows B1 Tq540000 Tk64 Hq32 Hk8 D128 token-major, deterministic", flush=True)
+    case = _device_case(cfg, seed=5, dev=cuda)
+    assert (cfg.Tq + 32) * 2 * case["q"].stride(2) >= 1 << 32   # the bhsd view's time stride (token-major)
+    ours = run_ours(case, cfg, atomic=False)
+    ref = E.eager_grads_chunked(case["q_bhsd"], case["k_bhsd"], case["v_bhsd"], None, None, case["grad_bhsd"],
+                                scale=cfg.D ** -0.5, is_causal=False, block=16384)
+    torch.cuda.synchronize()
+    for name, r in zip(OUTS, ref):
+        a, r = ours[name].float(), r.float()
+        err = (a - r).abs()
+        scale = r.abs().mean().item()
+        print(f"[long_rows] {name}: max={err.max().item():.3e} mean={err.mean().item():.3e} "
+              f"mean|ref|={scale:.3e} max|ref|={r.abs().max().item():.3e}", flush=True)
+        # O and dQ rows: the small-shape bar.  dK and dV entries each sum 2.2
+        # million products of 16-bit-rounded dS / P (python/fa2.py:287, 291):
+        # their error is that rounding's random walk, ~2^-9 of the entries'
+        # typical size whatever the entry's own value, so the absolute term
+        # scales with mean |ref| (here ~27) there
+        floor = 2e-2 if name in ("out", "dq") else 2.0 ** -6 * scale
+        assert bool((err <= floor + 2.0 ** -6 * r.abs()).all()), name
+        assert err.mean().item() <= max(1e-4, 2.0 ** -8 * scale), name
+    del ref
+    hm = {n: case[n + "_bhsd"].contiguous() for n in ("q", "k", "v", "grad")}
+    case_hm = dict(case, q=hm["q"], k=hm["k"], v=hm["v"], grad=hm["grad"])
+    again = run_ours(case_hm, cfg, atomic=False)
+    for n in OUTS:
+        assert torch.equal(ours[n], again[n]), n

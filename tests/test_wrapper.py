@@ -163,3 +163,23 @@ def test_kernel_head_dim_padding_rule():
     y = fa2._pad_head_dim(x, 128)
     assert y.shape == (2, 3, 4, 128) and torch.equal(y[..., :96], x) and not y[..., 96:].any()
     assert fa2._pad_head_dim(x, 96) is x
+
+
+def test_long_rows_are_relaid_head_major():
+    """The backward reaches a Q / dO row with a 32-bit byte offset from its
+    head's first row: (Tq + 32) rows spanning 4 GiB or more (token-major, 32
+    heads of 128 at 540k tokens) are re-laid head-major, shorter ones pass
+    through as the same tensor (meta tensors: no memory)."""
+    from tilelang_fa2_4d_mask import fa2
+
+    big = torch.empty((1, 540000, 32, 128), dtype=torch.bfloat16, device="meta")
+    assert (540000 + 32) * 2 * big.stride(1) >= fa2.ROW_SPAN_LIMIT
+    out = fa2._rows_reachable(big, 540000)
+    assert out.shape == big.shape
+    assert out.stride() == (32 * 540000 * 128, 128, 540000 * 128, 1)
+    assert (540000 + 32) * 2 * out.stride(1) < fa2.ROW_SPAN_LIMIT
+    small = torch.empty((1, 500000, 32, 128), dtype=torch.bfloat16, device="meta")
+    assert fa2._rows_reachable(small, 500000) is small
+    # a head-major view of token-major storage is left as it is
+    hm = big.transpose(1, 2).contiguous().transpose(1, 2)
+    assert fa2._rows_reachable(hm, 540000) is hm
