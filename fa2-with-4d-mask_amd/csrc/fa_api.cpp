@@ -215,9 +215,8 @@ static int check_mask_params(const FaMaskParams* p) {
     return fail(FA_ERR_STRIDE, "mask strides must be non-negative");
   const fa::MaskLayout ml = layout_of(p->batch, p->heads_q, p->seqlen_q, p->seqlen_k, p->mask_stride_b,
                                       p->mask_stride_h);
-  if ((int64_t)ml.Bm * ml.Hm > 65535 || (p->seqlen_q + 31) / 32 > 65535)
-    return fail(FA_ERR_SHAPE, "mask too large for the preparation grid (planes %d x %d, Tq %d)", ml.Bm, ml.Hm,
-                p->seqlen_q);
+  if ((int64_t)ml.Bm * ml.Hm >= (1LL << 31))
+    return fail(FA_ERR_SHAPE, "mask has too many planes (%d x %d) for 32-bit plane indices", ml.Bm, ml.Hm);
   return FA_OK;
 }
 

@@ -247,9 +247,12 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
   // used only four steps later: a conditional load whose result is used at
   // once made the compiler wait for all of the wave's loads right there.
   uint32_t mq[MASK ? 4 : 1] = {};
-  // ... and the step's position, (head << 16) | (first row / 32), read by
-  // the dS-store / score position four steps later (one list cursor only)
+  // ... and the step's position, ((head - h_first) << psh) | (first row / 32),
+  // read by the dS-store / score position four steps later (one list cursor
+  // only).  psh bits hold every step index; the host's B Hq Tq < 2^31 keeps
+  // the head part below 2^27.
   int pq[MASK ? 4 : 1] = {};
+  const int psh = 32 - __builtin_clz((uint32_t)max(a.nq32 - 1, 1));
   auto load_next = [&](auto Sc, auto Qc) __attribute__((always_inline)) {
     constexpr int S = decltype(Sc)::value;
     constexpr int Q = decltype(Qc)::value;
@@ -270,7 +273,7 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
       }
       const uint32_t* bt = (const uint32_t*)(a.mws + a.ml.bitsT + mask_plane(a.ml, b, ld_h) * a.ml.pbitsT);
       mq[Q] = bt[((int64_t)(kc >> 5) * a.ml.wq + (ld_qs >> 5)) * 32 + (kc & 31)];
-      pq[Q] = (ld_h << 16) | (ld_qs >> 5);
+      pq[Q] = ((ld_h - h_first) << psh) | (ld_qs >> 5);
     }
     const auto rq = MASK ? rs_of(q_head, q_rec, live) : rq_c;
     const auto rd = MASK ? rs_of(d_head, d_rec, live) : rd_c;
@@ -400,8 +403,8 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
                                                 0x00020000);
       // step j+1 as the load cursor queued it (padding steps: row 0 of the
       // last head)
-      it_h = pos_next >> 16;
-      it_qs = kStep * (pos_next & 0xffff);
+      it_h = h_first + (pos_next >> psh);
+      it_qs = kStep * (pos_next & ((1 << psh) - 1));
       return;
     }
     const bool ok = ds_on && j < n && (!CAUSAL || kb32 <= s);

@@ -52,11 +52,12 @@ __device__ __forceinline__ uint32_t transpose32(uint32_t a, int l32) {
 // covers one whole 1 KB row segment; lane pairs (2 c, 2 c + 1) join their 16
 // bits into the row word of key block c.  Every word written (bits
 // row-major, bitsT per key block) lands in full 128-byte lines.
-__global__ __launch_bounds__(256) void mask_bits_kernel(const MaskArgs a) {
-  __shared__ uint32_t words[kRows][kKeys / 32 + 1];
+// One (key chunk of 1024, row block of 32 rows from r0, plane pm) of the bits
+// kernel below.
+__device__ __forceinline__ void bits_block(const MaskArgs& a, uint32_t (&words)[kRows][kKeys / 32 + 1], int kc0,
+                                           int r0, int pm) {
   const MaskLayout& ml = a.ml;
   const int tid = threadIdx.x;
-  const int kc0 = blockIdx.x * kKeys, r0 = blockIdx.y * kRows, pm = blockIdx.z;
   const int bb = pm / ml.Hm, hh = pm - bb * ml.Hm;
   const uint8_t* src = a.mask + bb * a.msb + hh * a.msh;
   const int Tq = a.Tq, Tk = a.Tk;
@@ -125,6 +126,21 @@ __global__ __launch_bounds__(256) void mask_bits_kernel(const MaskArgs a) {
     const uint32_t notall = (uint32_t)(__builtin_amdgcn_ballot_w64(valid && w != vrows) >> (32 * hw));
     const int kb = kc0 / 32 + cb;
     if (l32 == 0 && kb < ml.nk32) blk[(int64_t)s * ml.nk32 + kb] = any == 0 ? 0 : (notall == 0 ? 2 : 1);
+  }
+}
+
+__global__ __launch_bounds__(256) void mask_bits_kernel(const MaskArgs a) {
+  __shared__ uint32_t words[kRows][kKeys / 32 + 1];
+  const MaskLayout& ml = a.ml;
+  const int kc0 = blockIdx.x * kKeys;
+  const int nrb = (a.Tq + kRows - 1) / kRows, np = ml.Bm * ml.Hm;
+  // row blocks and planes with grid strides: the grid's y and z hold at most
+  // 65535 (the loop bounds are uniform in the workgroup, and so its barriers)
+  for (int pm = blockIdx.z; pm < np; pm += gridDim.z) {
+    for (int rb = blockIdx.y; rb < nrb; rb += gridDim.y) {
+      bits_block(a, words, kc0, rb * kRows, pm);
+      __syncthreads();   // words is rewritten for the next (row block, plane)
+    }
   }
 }
 
@@ -249,8 +265,8 @@ __global__ __launch_bounds__(256) void mask_order_kernel(const MaskArgs a) {
 
 hipError_t launch_mask_prepare(const MaskArgs& a, hipStream_t s) {
   const MaskLayout& ml = a.ml;
-  const dim3 g1((unsigned)((a.Tk + kKeys - 1) / kKeys), (unsigned)((a.Tq + kRows - 1) / kRows),
-                (unsigned)(ml.Bm * ml.Hm));
+  const dim3 g1((unsigned)((a.Tk + kKeys - 1) / kKeys), (unsigned)min((a.Tq + kRows - 1) / kRows, 65535),
+                (unsigned)min(ml.Bm * ml.Hm, 65535));
   hipLaunchKernelGGL(mask_bits_kernel, g1, dim3(256), 0, s, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;

@@ -182,3 +182,106 @@ def test_prepared_mask_matches_definition(cuda, B, Hq, Hm, Tq, Tk, causal, kind)
         for lists in (lf, lk, ld):
             want_ord += sorted(range(len(lists)), key=lambda i: (-len(lists[i]), i))
         assert got_ord == want_ord, f"order plane {pm}"
+
+
+def _pack_words(keep):
+    """[..., C] bool -> [..., ceil(C/32)] int64 words (vectorised pack_bits)."""
+    C = keep.shape[-1]
+    n = cdiv(C, 32)
+    pad = torch.zeros(keep.shape[:-1] + (n * 32,), dtype=torch.int64, device=keep.device)
+    pad[..., :C] = keep.long()
+    return (pad.view(keep.shape[:-1] + (n, 32)) << torch.arange(32, dtype=torch.int64, device=keep.device)).sum(-1)
+
+
+def _check_bits_and_blocks(ws, mask, m, Tq, Tk):
+    """bits, bitsT and block states of every plane (Tq, Tk multiples of 32)."""
+    P = m["Bm"] * m["Hm"]
+    planes = mask.reshape(P, Tq, Tk)
+    ws32 = ws[: m["total"] // 4 * 4].view(torch.int32)
+    got = ws32[m["bits"] // 4:][: P * Tq * m["wk"]].view(P, Tq, m["wk"]).long() & 0xFFFFFFFF
+    assert torch.equal(got[:, :, : m["nk32"]], _pack_words(planes)), "bits"
+    got_t = ws32[m["bitsT"] // 4:][: P * m["nk32"] * m["wq"] * 32].view(P, m["nk32"], m["wq"], 32)
+    got_t = got_t.permute(0, 1, 3, 2).reshape(P, m["nk32"] * 32, m["wq"]).long() & 0xFFFFFFFF
+    assert torch.equal(got_t[:, :Tk, : m["nq32"]], _pack_words(planes.transpose(1, 2).contiguous())), "bitsT"
+    blocks = planes.view(P, m["nq32"], 32, m["nk32"], 32)
+    want = torch.where(blocks.any(4).any(2), torch.where(blocks.all(4).all(2), 2, 1), 0).to(torch.uint8)
+    got_b = ws[m["blk"]:][: P * m["pblk"]].view(P, m["nq32"], m["nk32"])
+    assert torch.equal(got_b, want), "blk"
+
+
+def _attention_vs_oracle(q, k, v, mask, do, label, long_sums=False):
+    """fwd+bwd in both modes against the eager oracle (small-shape bar).
+    long_sums: dK / dV entries sum millions of products of 16-bit-rounded dS
+    and P (python/fa2.py:287, 291), whose error is that rounding's random
+    walk, ~2^-9 of the entries' typical size whatever an entry's own value:
+    their absolute term scales with mean |ref| then."""
+    import tilelang_fa2_4d_mask as api
+    from oracle import eager as E
+
+    ref = E.eager_grads_chunked(q, k, v, mask, None, do, scale=q.shape[-1] ** -0.5, is_causal=False,
+                                block=65536)
+    for atomic in (True, False):
+        qq, kk, vv = (x.detach().requires_grad_(True) for x in (q, k, v))
+        out = api.tilelang_flash_attention(qq, kk, vv, mask=mask, use_atomic_backward=atomic)
+        out.backward(do)
+        torch.cuda.synchronize()
+        for name, a, r in zip(("out", "dq", "dk", "dv"), (out, qq.grad, kk.grad, vv.grad), ref):
+            a, r = a.float(), r.float()
+            assert torch.equal(torch.isnan(a), torch.isnan(r)), f"{label} {name}: NaN positions"
+            fin = torch.isfinite(r)
+            err = (a[fin] - r[fin]).abs()
+            print(f"[{label} atomic={atomic}] {name}: max={err.max().item():.3e} mean={err.mean().item():.3e}",
+                  flush=True)
+            floor = 2.0 ** -6 * r[fin].abs().mean().item() if long_sums and name in ("dk", "dv") else 2e-2
+            assert bool((err <= floor + 2.0 ** -6 * r[fin].abs()).all()), f"{label} {name}"
+            assert err.mean().item() <= max(1e-4, 2.0 ** -8 * r[fin].abs().mean().item()), f"{label} {name}"
+
+
+def test_more_planes_than_one_grid_dimension(cuda):
+    """A per-head mask of 2100 x 32 = 67200 planes: more than the 65535 a grid
+    dimension holds, so the preparation walks its planes with a grid stride
+    (large batches of short sequences reach this)."""
+    from tilelang_fa2_4d_mask import fa2
+
+    B, H, T, D = 2100, 32, 64, 64
+    print(f"case B{B} H{H} T{T} D{D} per-head mask: {B * H} planes", flush=True)
+    g = torch.Generator(device=cuda).manual_seed(11)
+    mask = torch.rand((B, H, T, T), generator=g, device=cuda) < 0.6
+    mask[:, :, torch.arange(T), torch.arange(T)] = True
+    mst = fa2._norm_strides(mask)[:3]
+    ws = fa2._prepare_mask(mask, mst, B, H, T, T, False, cuda)
+    torch.cuda.synchronize()
+    m = layout(B, H, T, T, False, False)
+    assert ws.numel() == m["total"]
+    _check_bits_and_blocks(ws, mask, m, T, T)
+    # lists and order of the first and last planes against the definition
+    ws_cpu = ws.cpu()
+    ws32 = ws_cpu[: m["total"] // 4 * 4].view(torch.int32)
+    for pm in (0, B * H - 1):
+        _, _, _, lf, lk, ld = expected(mask[pm // H, pm % H].cpu(), T, T, False, m)
+        assert read_lists(ws32, m["lfwd"] + pm * m["plfwd"], m["nfq"], 1 + m["nft"]) == lf, f"fwd lists {pm}"
+        assert read_lists(ws32, m["lkv"] + pm * m["plkv"], m["nkb"], 1 + m["nq32"]) == lk, f"kv lists {pm}"
+        assert read_lists(ws32, m["ldq"] + pm * m["pldq"], m["ndq"], 1 + m["nk32"]) == ld, f"dq lists {pm}"
+    rnd = lambda *s: torch.randn(s, generator=g, device=cuda).to(torch.bfloat16)  # noqa: E731
+    _attention_vs_oracle(rnd(B, H, T, D), rnd(B, H, T, D), rnd(B, H, T, D), mask, rnd(B, H, T, D), "planes")
+
+
+def test_more_row_blocks_than_one_grid_dimension(cuda):
+    """Tq 2^21 + 64: 65538 blocks of 32 rows, past the 65535 of a grid
+    dimension, so the preparation walks its row blocks with a grid stride."""
+    from tilelang_fa2_4d_mask import fa2
+
+    Tq, Tk, D = (1 << 21) + 64, 64, 64
+    print(f"case B1 H1 Tq{Tq} Tk{Tk} D{D}: {Tq // 32} row blocks", flush=True)
+    g = torch.Generator(device=cuda).manual_seed(12)
+    mask = torch.rand((1, 1, Tq, Tk), generator=g, device=cuda) < 0.5
+    mask[:, :, :, 0] = True
+    mst = fa2._norm_strides(mask)[:3]
+    ws = fa2._prepare_mask(mask, mst, 1, 1, Tq, Tk, False, cuda)
+    torch.cuda.synchronize()
+    m = layout(1, 1, Tq, Tk, True, True)
+    assert ws.numel() == m["total"]
+    _check_bits_and_blocks(ws, mask, m, Tq, Tk)
+    rnd = lambda *s: torch.randn(s, generator=g, device=cuda).to(torch.bfloat16)  # noqa: E731
+    _attention_vs_oracle(rnd(1, 1, Tq, D), rnd(1, 1, Tk, D), rnd(1, 1, Tk, D), mask, rnd(1, 1, Tq, D), "rows",
+                         long_sums=True)
