@@ -273,7 +273,7 @@ def traffic_pass(torch, api, dev) -> int:
     """One untimed launch of each kernel whose counters are reported (what the
     rocprofv3 --pmc passes count), after a 1 GiB copy whose FETCH_SIZE /
     WRITE_SIZE reading calibrates those counters: the H forward and
-    deterministic fwd+bwd, non-causal and causal; the S and P fwd+bwd
+    deterministic fwd+bwd, non-causal and causal; the P, S and M fwd+bwd
     (deterministic)."""
     x = torch.empty(2 ** 28, dtype=torch.float32, device=dev)
     y = torch.empty_like(x)
@@ -291,8 +291,6 @@ def traffic_pass(torch, api, dev) -> int:
         del q, k, v
     del q0, k0, v0, do
     for n, c in side_configs(torch, dev):
-        if n not in ("S", "P"):
-            continue
         log(f"profile pass: {n}")
         q, k, v = (c[t].detach().requires_grad_(True) for t in ("q", "k", "v"))
         api.tilelang_flash_attention(q, k, v, mask=c["mask"], score=c["score"], layout=c["layout"],
@@ -315,7 +313,7 @@ def main() -> int:
     ap.add_argument("--traffic-pass", action="store_true",
                     help="run once, untimed, what the rocprofv3 --pmc passes count: a 1 GiB fp32 copy "
                          "(calibration), the H forward and deterministic fwd+bwd (non-causal and causal), "
-                         "the S and P deterministic fwd+bwd")
+                         "the P, S and M deterministic fwd+bwd")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}): this build has no multi-GPU "
