@@ -345,3 +345,21 @@ def test_mask_prepare_needs_aligned_workspace(lib):
     assert "workspace is NULL" in lib.fa_last_error().decode()
     assert lib.fa_mask_prepare(ctypes.byref(mask_params(workspace=FAKE + 64))) == 5
     assert "256-byte aligned" in lib.fa_last_error().decode()
+
+
+def test_mask_plan_beyond_one_grid_dimension(lib):
+    """The preparation walks planes and 32-row blocks with grid strides: more
+    than 65535 of either plans (and prepares) like any other mask; planes
+    that overflow 32-bit plane indices are refused."""
+    # 70000 batches of a per-batch mask [70000, 1, 64, 64]: 70000 planes
+    n = _mask_bytes(lib, batch=70000, heads_q=1, seqlen_q=64, seqlen_k=64, mask_stride_b=64 * 64, mask_stride_q=64)
+    one = _mask_bytes(lib, batch=1, heads_q=1, seqlen_q=64, seqlen_k=64, mask_stride_b=64 * 64, mask_stride_q=64)
+    assert n > 60000 * one // 2
+    # 2^21 + 64 query rows: 65538 row blocks of 32
+    assert _mask_bytes(lib, batch=1, heads_q=1, seqlen_q=(1 << 21) + 64, seqlen_k=64, mask_stride_q=64) > 0
+    # 2^16 batches x 2^15 heads, per-head mask: 2^31 planes
+    nb = ctypes.c_int64(0)
+    p = mask_params(batch=1 << 16, heads_q=1 << 15, seqlen_q=32, seqlen_k=32, mask_stride_b=(1 << 15) * 1024,
+                    mask_stride_h=1024, mask_stride_q=32)
+    assert lib.fa_mask_plan(ctypes.byref(p), ctypes.byref(nb)) == 2
+    assert "32-bit plane indices" in lib.fa_last_error().decode()
