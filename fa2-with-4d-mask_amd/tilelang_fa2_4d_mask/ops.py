@@ -94,9 +94,14 @@ def _setup_context(ctx, inputs, output):
     O, LSE, mask_ws = output
     ctx.save_for_backward(q, k, v, O, LSE, mask, score, mask_ws)
     ctx.scale, ctx.is_causal, ctx.use_atomic_backward = scale, is_causal, use_atomic_backward
+    # LSE and the mask workspace never receive a gradient: without this,
+    # autograd launches a zero fill for each of them before every backward
+    ctx.set_materialize_grads(False)
 
 
 def _backward(ctx, dO, dLSE, dws):
+    if dO is None:  # O itself does not reach the loss
+        return None, None, None, None, None, None, None, None
     q, k, v, O, LSE, mask, score, mask_ws = ctx.saved_tensors
     dq, dk, dv = torch.ops.tilelang_fa2_4d_mask.bwd(dO, q, k, v, O, LSE, mask, score, mask_ws, ctx.scale,
                                                     ctx.is_causal, ctx.use_atomic_backward)
