@@ -53,3 +53,25 @@ def test_public_wrapper_routes_through_the_op():
     sig = inspect.signature(fa2.flash_attention_with_4d_mask)
     assert list(sig.parameters) == ["Q", "K", "V", "Mask", "Score", "scale", "is_causal", "use_atomic_backward",
                                     "bhsd_input"]
+
+
+def test_backward_without_an_output_gradient():
+    """LSE and the mask workspace get no materialised zero gradients (no fill
+    kernels before every backward); when O does not reach the loss either, the
+    backward returns no gradients and launches nothing."""
+    _, _, ops = _mods()
+
+    class Ctx:
+        materialize = True
+
+        def save_for_backward(self, *t):
+            self.saved_tensors = t
+
+        def set_materialize_grads(self, value):
+            self.materialize = value
+
+    ctx = Ctx()
+    q = torch.empty((1, 4, 2, 64), device="meta")
+    ops._setup_context(ctx, (q, q, q, None, None, 0.125, False, True), (q, q, q))
+    assert ctx.materialize is False
+    assert ops._backward(ctx, None, None, None) == (None,) * 8
