@@ -310,6 +310,9 @@ def main() -> int:
     ap.add_argument("--no-side-configs", action="store_true",
                     help="skip the P / S / M config lines (mask, score+mask, MQA)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--ds-limit", type=int, default=None,
+                    help="dS workspace limit in bytes for the backward (tilelang_fa2_4d_mask.fa2.DS_LIMIT_BYTES); "
+                         "default: the library's")
     ap.add_argument("--traffic-pass", action="store_true",
                     help="run once, untimed, what the rocprofv3 --pmc passes count: a 1 GiB fp32 copy "
                          "(calibration), the H forward and deterministic fwd+bwd (non-causal and causal), "
@@ -329,6 +332,9 @@ def main() -> int:
         log("no GPU visible")
         return 1
     dev = torch.device("cuda:0")
+    if args.ds_limit is not None:
+        import tilelang_fa2_4d_mask.fa2 as fa2mod
+        fa2mod.DS_LIMIT_BYTES = args.ds_limit
     if args.traffic_pass:
         return traffic_pass(torch, api, dev)
     q0, k0, v0, do = make_inputs(torch, dev)

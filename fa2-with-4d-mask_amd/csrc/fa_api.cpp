@@ -93,10 +93,13 @@ int launch_status(hipError_t e, const char* what) {
 // caller's limit (all of them when they fit), in as few slices of nearly
 // equal size as that allows: the backward then runs the two kernels once per
 // slice.  0 units: not even one unit fits.
+// With a mask or a score each tile is a pair: dS rounded, then its rounding
+// residual (the dQ kernel adds both products).
+int ds_tile_parts(const FaBwdParams* p) { return p->mask || p->score ? 2 : 1; }
 int64_t ds_unit_elems(const FaBwdParams* p) {
   const int64_t nq32 = (p->seqlen_q + 31) / 32, nk32 = (p->seqlen_k + 31) / 32;
   const int64_t plane = fa::ds_row(nq32, nk32, p->is_causal != 0);
-  return (int64_t)(p->heads_q / p->heads_k) * plane * 1024;   // one unit: the group's planes
+  return (int64_t)(p->heads_q / p->heads_k) * plane * 1024 * ds_tile_parts(p);   // one unit: the group's planes
 }
 int64_t ds_slice_units(const FaBwdParams* p) {
   const int64_t limit = p->ds_limit_bytes == 0 ? (int64_t)8 << 30 : p->ds_limit_bytes;
@@ -158,10 +161,11 @@ bool dq_atomics(const FaBwdParams* p) {
 }
 
 // query rows per workgroup of the dQ-from-dS kernel: 512 (8 waves sharing
-// each K tile) when dQ is written directly at head dim 128 without a mask and
-// that still gives every CU a workgroup, else 256
+// each K tile) when dQ is written directly at head dim 128 without a mask or
+// a score (whose tile pairs double the staging) and that still gives every CU
+// a workgroup, else 256
 int dq_rows(const FaBwdParams* p) {
-  if (p->head_dim != 128 || p->mask || dq_atomics(p)) return fa::kDqDsRows;
+  if (p->head_dim != 128 || p->mask || p->score || dq_atomics(p)) return fa::kDqDsRows;
   return dq_groups(p, fa::kDqDsRowsWide) >= kCus ? fa::kDqDsRowsWide : fa::kDqDsRows;
 }
 
@@ -255,6 +259,8 @@ int fa_fwd(const FaFwdParams* p) {
   if ((st = check_operand("k", p->k, p->k_stride_b, p->k_stride_t, p->k_stride_h))) return st;
   if ((st = check_operand("v", p->v, p->v_stride_b, p->v_stride_t, p->v_stride_h))) return st;
   if ((st = check_operand("o", p->o, p->o_stride_b, p->o_stride_t, p->o_stride_h))) return st;
+  if (p->o_lo && (st = check_operand("o_lo", p->o_lo, p->o_lo_stride_b, p->o_lo_stride_t, p->o_lo_stride_h)))
+    return st;
   if (!p->lse) return fail(FA_ERR_NULL, "lse is NULL");
   if ((st = check_mask_score(p->mask, p->mask_stride_b, p->mask_stride_h, p->mask_stride_q, p->score,
                              p->score_stride_b, p->score_stride_h, p->score_stride_q)))
@@ -288,6 +294,10 @@ int fa_fwd(const FaFwdParams* p) {
     a.mws = (const char*)p->mask_ws;
     a.ml = layout_of(p->batch, p->heads_q, p->seqlen_q, p->seqlen_k, p->mask_stride_b, p->mask_stride_h);
   }
+  if (p->o_lo && (p->mask || p->score)) {
+    a.olo = p->o_lo;
+    a.olsb = p->o_lo_stride_b; a.olst = p->o_lo_stride_t; a.olsh = p->o_lo_stride_h;
+  }
   return launch_status(fa::launch_fwd(a, p->head_dim, p->dtype, p->is_causal != 0, (hipStream_t)p->stream), "fa_fwd");
 }
 
@@ -302,6 +312,8 @@ static int check_bwd(const FaBwdParams* p, int split) {
   if ((st = check_operand("dq", p->dq, p->dq_stride_b, p->dq_stride_t, p->dq_stride_h))) return st;
   if ((st = check_operand("dk", p->dk, p->dk_stride_b, p->dk_stride_t, p->dk_stride_h))) return st;
   if ((st = check_operand("dv", p->dv, p->dv_stride_b, p->dv_stride_t, p->dv_stride_h))) return st;
+  if (p->o_lo && (st = check_operand("o_lo", p->o_lo, p->o_lo_stride_b, p->o_lo_stride_t, p->o_lo_stride_h)))
+    return st;
   // The dK/dV kernel stages Q/dO tiles with 32-bit buffer offsets (32 rows of a tile).
   // The dQ kernel stages K tiles the same way.
   if (p->q_stride_t < 0 || p->q_stride_t >= (1LL << 24) || p->do_stride_t < 0 || p->do_stride_t >= (1LL << 24) ||
@@ -324,6 +336,10 @@ static int check_bwd(const FaBwdParams* p, int split) {
   if (split > 1 && (!aligned16(p->dk_accum) || !aligned16(p->dv_accum)))
     return fail(FA_ERR_STRIDE, "dk_accum/dv_accum must be 16-byte aligned");
   if (ds_elems(p) > 0 && !p->ds_tiles) return fail(FA_ERR_WORKSPACE, "dQ from dS tiles needs ds_tiles (plan.ds_elems)");
+  if (ds_elems(p) > 0 && p->ds_tiles_elems < ds_elems(p))
+    return fail(FA_ERR_WORKSPACE, "ds_tiles holds %lld elements, the plan needs %lld (with a mask or a score each "
+                "block is a pair of tiles: plan with mask/score set)", (long long)p->ds_tiles_elems,
+                (long long)ds_elems(p));
   if (ds_elems(p) > 0 && !aligned16(p->ds_tiles)) return fail(FA_ERR_STRIDE, "ds_tiles must be 16-byte aligned");
   if ((st = check_mask_ws(p->mask, p->mask_ws))) return st;
   return check_mask_score(p->mask, p->mask_stride_b, p->mask_stride_h, p->mask_stride_q, p->score,
@@ -363,6 +379,8 @@ int fa_bwd_preprocess(const FaBwdParams* p) {
   a.dq_accum = dq_atomics(p) ? p->dq_accum : nullptr;
   a.osb = p->o_stride_b; a.ost = p->o_stride_t; a.osh = p->o_stride_h;
   a.dsb = p->do_stride_b; a.dst = p->do_stride_t; a.dsh = p->do_stride_h;
+  a.olo = p->o_lo;
+  a.olsb = p->o_lo_stride_b; a.olst = p->o_lo_stride_t; a.olsh = p->o_lo_stride_h;
   a.B = p->batch; a.Tq = p->seqlen_q; a.Hq = p->heads_q; a.Hk = p->heads_k; a.G = p->heads_q / p->heads_k;
   a.is_causal = p->is_causal != 0;
   if (p->mask) {

@@ -77,6 +77,19 @@ __global__ __launch_bounds__(256) void preprocess_kernel(const PreArgs a) {
 #pragma unroll
       for (int t = 0; t < 8; ++t) acc = fmaf(to_f<T>(ov[t]), to_f<T>(dv[t]), acc);
     }
+    if (a.olo) {
+      // O's rounding residual from the forward (mask or score): O to about
+      // 16 significant bits
+      const T* lp = (const T*)a.olo + b * a.olsb + (int64_t)q * a.olst + h * a.olsh;
+#pragma unroll
+      for (int u = 0; u < CPT; ++u) {
+        const int c = part + 4 * u;
+        const auto lv = as_vec8<T>(gload16(lp + c * 8));
+        const auto dv = as_vec8<T>(gload16(dp + c * 8));
+#pragma unroll
+        for (int t = 0; t < 8; ++t) acc = fmaf(to_f<T>(lv[t]), to_f<T>(dv[t]), acc);
+      }
+    }
   }
   acc += __shfl_xor(acc, 1);
   acc += __shfl_xor(acc, 2);

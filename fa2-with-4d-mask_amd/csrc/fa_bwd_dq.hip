@@ -55,15 +55,21 @@ constexpr unsigned kCuCount = 256;                    // compute units of the pa
 // prepared lists' 256 rows: NW = 8, ST = 1 (deterministic, head dim 128: twice
 // the waves, and dS bytes in flight, of NW = 4, ST = 2).  Else NW = 4, ST = 2
 // (with atomics 8 waves were 3-5 % slower).
-template <typename T, int D, bool CAUSAL, bool MASK, bool ATOMIC, int NW, int ST>
+// PREC (a mask or a score): each stored block is a pair of tiles, dS rounded
+// and its rounding residual, and dQ adds both products (dS to about 16
+// significant bits); two register staging sets then hold as many bytes as
+// three of single tiles.
+template <typename T, int D, bool CAUSAL, bool MASK, bool ATOMIC, int NW, int ST, bool PREC>
 __global__ __launch_bounds__(NW * 64, 2) void dq_ds_kernel(const BwdArgs a) {
   constexpr int kDqWaves = NW;
   constexpr int kDqSteps = ST;                       // 32-row query steps per wave
   constexpr int kDqRows = kDqWaves * kDqSteps * 32;   // query rows per workgroup
   using V8 = typename Vec8<T>::type;
+  constexpr int NPART = PREC ? 2 : 1;                // 2 KB tiles per stored block
+  constexpr int kS = PREC && ST == 2 ? 2 : kSets;    // register staging sets
   constexpr int NB = D / 32, CH = D / 8, ROWB = 2 * D;
   constexpr int KTILE = 32 * ROWB;                   // bytes of one K step tile
-  constexpr int DSW = kDqSteps * 2048;               // dS bytes of one wave and step
+  constexpr int DSW = kDqSteps * NPART * 2048;       // dS bytes of one wave and step
   constexpr int BUFB = KTILE + kDqWaves * DSW;       // one LDS buffer
   constexpr int UK = 32 * CH / (kDqWaves * 64);      // K chunks per thread
   constexpr int UD = DSW / (64 * 16);                // dS chunks per lane
@@ -197,7 +203,7 @@ __global__ __launch_bounds__(NW * 64, 2) void dq_ds_kernel(const BwdArgs a) {
 #pragma unroll
   for (int i = 0; i < kDqSteps; ++i) row0[i] = plane + ds_row(s0 + i, nk32, CAUSAL);
 
-  u32x4 stk[kSets][UK], std_[kSets][UD];
+  u32x4 stk[kS][UK], std_[kS][UD];
   // Key step at local position jl (position jb + jl) into staging set S (keys
   // past Tk and dS tiles outside the stored set load as zeros; jl >= nloc
   // loads nothing).
@@ -227,8 +233,8 @@ __global__ __launch_bounds__(NW * 64, 2) void dq_ds_kernel(const BwdArgs a) {
     for (int i = 0; i < kDqSteps; ++i) {
       const int s = s0 + i;
       const bool ok = MASK ? ((okb >> i) & 1u) != 0 : inr && s < nq32 && (!CAUSAL || kb <= s);
-      const auto rd = __builtin_amdgcn_make_buffer_rsrc((void*)(dsp + (row0[i] + kb) * 1024), (short)0, ok ? 2048 : 0,
-                                                        0x00020000);
+      const auto rd = __builtin_amdgcn_make_buffer_rsrc((void*)(dsp + (row0[i] + kb) * 1024 * NPART), (short)0,
+                                                        ok ? 2048 * NPART : 0, 0x00020000);
 #pragma unroll
       for (int u = 0; u < UD / kDqSteps; ++u)   // non-temporal: each dS tile is read once
         std_[S][i * (UD / kDqSteps) + u] = __builtin_amdgcn_raw_buffer_load_b128(rd, (uint32_t)(lane * 16 + u * 1024), 0, 2);
@@ -251,9 +257,9 @@ __global__ __launch_bounds__(NW * 64, 2) void dq_ds_kernel(const BwdArgs a) {
   auto compute = [&](int BUF) __attribute__((always_inline)) {
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
-      V8 bf[kDqSteps];
+      V8 bf[kDqSteps * NPART];   // tile (step i, part) at (i NPART + part) 2048
 #pragma unroll
-      for (int i = 0; i < kDqSteps; ++i) {
+      for (int i = 0; i < kDqSteps * NPART; ++i) {
         const uint32_t off = (uint32_t)(BUF * BUFB + i * 2048 + c * 256);   // keys 16 c ..
         bf[i] = cat_tr<T>(lds_rdtr(bd[0] + off), lds_rdtr(bd[1] + off));
       }
@@ -262,28 +268,31 @@ __global__ __launch_bounds__(NW * 64, 2) void dq_ds_kernel(const BwdArgs a) {
         const uint32_t off = (uint32_t)(BUF * BUFB + c * 16 * ROWB);
         const V8 af = cat_tr<T>(lds_rdtr(at[0][nb] + off), lds_rdtr(at[1][nb] + off));
 #pragma unroll
-        for (int i = 0; i < kDqSteps; ++i) acc[i][nb] = mfma32(af, bf[i], acc[i][nb]);
+        for (int i = 0; i < kDqSteps; ++i) {
+          acc[i][nb] = mfma32(af, bf[i * NPART], acc[i][nb]);
+          if constexpr (PREC) acc[i][nb] = mfma32(af, bf[i * NPART + 1], acc[i][nb]);
+        }
       }
     }
   };
 
   // ---- prologue: tiles 0 .. kSets-1 loading (tile t in set t % kSets), tile 0 in buffer 0 --
 #pragma unroll
-  for (int t = 0; t < kSets; ++t) load(t, t);
+  for (int t = 0; t < kS; ++t) load(t, t);
   store(0, 0);
-  load(0, kSets);
+  load(0, kS);
   lds_barrier();
 
   // ---- main loop: iteration j writes tile j+1 to LDS buffer (j+1)%2, loads tile
-  // j+1+kSets into the set it freed, computes tile j from buffer j%2 ------------------
-  constexpr int U = kSets == 2 ? 2 : 6;   // lcm(kSets, 2): sets and buffers static per copy
+  // j+1+kS into the set it freed, computes tile j from buffer j%2 ---------------------
+  constexpr int U = kS == 2 ? 2 : 6;   // lcm(kS, 2): sets and buffers static per copy
   int nu = (nloc + U - 1) / U * U;
   asm volatile("" : "+s"(nu));
   for (int j = 0; j < nu; j += U) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      store((u + 1) % kSets, (u + 1) & 1);
-      load((u + 1) % kSets, j + u + 1 + kSets);
+      store((u + 1) % kS, (u + 1) & 1);
+      load((u + 1) % kS, j + u + 1 + kS);
       compute(u & 1);
       lds_barrier();
     }
@@ -352,30 +361,33 @@ __global__ __launch_bounds__(NW * 64, 2) void dq_ds_kernel(const BwdArgs a) {
   }
 }
 
-template <typename T, int D, bool CAUSAL, bool ATOMIC>
-hipError_t launch_a(const BwdArgs& a, hipStream_t s) {
+template <typename T, int D, bool CAUSAL, bool ATOMIC, bool PREC>
+hipError_t launch_p(const BwdArgs& a, hipStream_t s) {
   const dim3 grid((unsigned)(a.nbk * a.G * a.nqt * (ATOMIC ? a.dq_split : 1)));
-  if (a.mask) {
+  if (PREC && a.mask) {
     // With a mask the row blocks stay at 256 rows (the prepared lists are per
-    // 256-row block).  Deterministic at head dim 128 with fewer blocks than
-    // two per CU (the 4-wave kernel's residency): 8 waves of one 32-row step
-    // each, twice the waves and dS tiles in flight (S config: -13 %); with
-    // more blocks two 4-wave workgroups per CU already overlap (P: the 8-wave
-    // kernel, one workgroup per CU, was 10 % slower).
-    if constexpr (D == 128 && !ATOMIC) {
-      if (grid.x < 2 * kCuCount) {
-        hipLaunchKernelGGL((dq_ds_kernel<T, D, CAUSAL, true, ATOMIC, 8, 1>), grid, dim3(512), 0, s, a);
-        return hipGetLastError();
-      }
+    // 256-row block).  At head dim 128: 8 waves of one 32-row step each (with
+    // the tile pairs, the 4-wave shape of two steps per wave needs more
+    // registers than two waves per SIMD hold); at 64: 4 waves of two steps.
+    if constexpr (PREC) {
+      if constexpr (D == 128) hipLaunchKernelGGL((dq_ds_kernel<T, D, CAUSAL, true, ATOMIC, 8, 1, PREC>), grid, dim3(512), 0, s, a);
+      else hipLaunchKernelGGL((dq_ds_kernel<T, D, CAUSAL, true, ATOMIC, 4, 2, PREC>), grid, dim3(256), 0, s, a);
     }
-    hipLaunchKernelGGL((dq_ds_kernel<T, D, CAUSAL, true, ATOMIC, 4, 2>), grid, dim3(256), 0, s, a);
-  } else if constexpr (D == 128 && !ATOMIC) {
-    if (a.dq_rows == kDqDsRowsWide) hipLaunchKernelGGL((dq_ds_kernel<T, D, CAUSAL, false, ATOMIC, 8, 2>), grid, dim3(512), 0, s, a);
-    else hipLaunchKernelGGL((dq_ds_kernel<T, D, CAUSAL, false, ATOMIC, 4, 2>), grid, dim3(256), 0, s, a);
+  } else if constexpr (D == 128 && !ATOMIC && !PREC) {
+    if (a.dq_rows == kDqDsRowsWide) hipLaunchKernelGGL((dq_ds_kernel<T, D, CAUSAL, false, ATOMIC, 8, 2, PREC>), grid, dim3(512), 0, s, a);
+    else hipLaunchKernelGGL((dq_ds_kernel<T, D, CAUSAL, false, ATOMIC, 4, 2, PREC>), grid, dim3(256), 0, s, a);
   } else {
-    hipLaunchKernelGGL((dq_ds_kernel<T, D, CAUSAL, false, ATOMIC, 4, 2>), grid, dim3(256), 0, s, a);
+    hipLaunchKernelGGL((dq_ds_kernel<T, D, CAUSAL, false, ATOMIC, 4, 2, PREC>), grid, dim3(256), 0, s, a);
   }
   return hipGetLastError();
+}
+
+// A mask (PREC with the prepared lists) always has PREC; a score without a
+// mask runs the unmasked kernel with PREC.
+template <typename T, int D, bool CAUSAL, bool ATOMIC>
+hipError_t launch_a(const BwdArgs& a, hipStream_t s) {
+  if (a.mask || a.score) return launch_p<T, D, CAUSAL, ATOMIC, true>(a, s);
+  return launch_p<T, D, CAUSAL, ATOMIC, false>(a, s);
 }
 
 template <typename T, int D, bool CAUSAL>

@@ -57,6 +57,15 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
   static_assert(DOFF + kNBuf * QTILE <= 65536, "buffer offsets fit the DS immediate");
   static_assert(kKvWaves * 32 * OS * 2 <= 2 * kNBuf * QTILE, "epilogue staging fits");
   static_assert(kKvKeys == kKv2Keys && kStep == 32, "prepared-mask lists are built for this shape");
+  // With a mask or a score, P and dS enter dV += P^T dO and dK += dS^T Q in
+  // several 16-bit parts each (the rounded value and its rounding residuals:
+  // more MFMAs on the same LDS operand): dS in two, P in three, which carries
+  // P to fp32 precision -- dV sums the few large P of rows that see few keys
+  // into entries whose 16-bit output step is coarse, and two parts left
+  // about one in a thousand of those entries a step off.  Each dS tile is
+  // followed by the tile of its residuals for the dQ kernel.
+  constexpr bool PREC = MASK || SCORE;
+  constexpr int NPART = PREC ? 2 : 1;   // 2 KB tiles per stored 32x32 block
   __shared__ __attribute__((aligned(1024))) char smem[LOFF + kNBuf * LBUF];
 
   // ---- which (batch, kv-head, split, key block) ------------------------------
@@ -386,7 +395,7 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
   // writes chunks 2 t + hf, i.e. one contiguous kilobyte of whole lines
   const uint32_t ds_vo = (uint32_t)(hf * 512 + l32 * 16);
   const int64_t ds_h0 = ((int64_t)b * a.Hq + it_h - ds_u0) * a.ds_plane + ds_row(qfirst >> 5, a.nk32, CAUSAL) + kb32;
-  const uint16_t* it_ptr = (const uint16_t*)a.ds + ds_h0 * 1024;
+  const uint16_t* it_ptr = (const uint16_t*)a.ds + ds_h0 * 1024 * NPART;
   auto ds_rs = __builtin_amdgcn_make_buffer_rsrc((void*)a.ds, (short)0, 0, 0x00020000);
   // descriptor of step j's tile, then advance (it_h, it_qs, it_tile) to step j+1
   auto next_step = [&](int j, uint32_t mreg, int pos_next) __attribute__((always_inline)) {
@@ -399,8 +408,8 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
       const bool any = __builtin_amdgcn_ballot_w64(mreg != 0u) != 0;
       const bool ok = ds_on && j < n && (!CAUSAL || kb32 <= s) && any;
       const int64_t tile = ((int64_t)b * a.Hq + it_h - ds_u0) * a.ds_plane + ds_row(s, a.nk32, CAUSAL) + kb32;
-      ds_rs = __builtin_amdgcn_make_buffer_rsrc((void*)((uint16_t*)a.ds + tile * 1024), (short)0, ok ? 2048 : 0,
-                                                0x00020000);
+      ds_rs = __builtin_amdgcn_make_buffer_rsrc((void*)((uint16_t*)a.ds + tile * 1024 * NPART), (short)0,
+                                                ok ? 2048 * NPART : 0, 0x00020000);
       // step j+1 as the load cursor queued it (padding steps: row 0 of the
       // last head)
       it_h = h_first + (pos_next >> psh);
@@ -408,18 +417,18 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
       return;
     }
     const bool ok = ds_on && j < n && (!CAUSAL || kb32 <= s);
-    ds_rs = __builtin_amdgcn_make_buffer_rsrc((void*)it_ptr, (short)0, ok ? 2048 : 0, 0x00020000);
+    ds_rs = __builtin_amdgcn_make_buffer_rsrc((void*)it_ptr, (short)0, ok ? 2048 * NPART : 0, 0x00020000);
     if constexpr (DESC) {
       it_qs -= kStep;
-      it_ptr -= (int64_t)min(s, a.nk32) * 1024;   // row s-1 holds min(s, nk32) tiles
+      it_ptr -= (int64_t)min(s, a.nk32) * 1024 * NPART;   // row s-1 holds min(s, nk32) tiles
     } else {
       it_qs += kStep;
-      it_ptr += (int64_t)(CAUSAL ? min(s + 1, a.nk32) : a.nk32) * 1024;
+      it_ptr += (int64_t)(CAUSAL ? min(s + 1, a.nk32) : a.nk32) * 1024 * NPART;
     }
     if (DESC ? it_qs < qstart : it_qs >= Tq) {
       ++it_h;
       it_qs = qfirst;
-      it_ptr = (const uint16_t*)a.ds + (ds_h0 + (int64_t)(it_h - (kvh * a.G + g0)) * a.ds_plane) * 1024;
+      it_ptr = (const uint16_t*)a.ds + (ds_h0 + (int64_t)(it_h - (kvh * a.G + g0)) * a.ds_plane) * 1024 * NPART;
     }
   };
 
@@ -429,12 +438,18 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
   for (int nb = 0; nb < NB; ++nb) { dkt[nb] = f32x16{}; dvt[nb] = f32x16{}; }
   f32x16 sacc[2], pacc[2];   // S / dP of steps j (parity) ; lane: [q = 8 (i/4) + 4 hf + i%4][key]
   V8 ppk[2][2], dspk[2][2];  // P / dS packed: [parity][c], k-slot (hf, t) <-> row 16 c + 4 hf + t%4 + 8 (t/4)
+  V8 ppl[PREC ? 2 : 1][2], dsl[PREC ? 2 : 1][2];   // their rounding residuals (PREC)
+  V8 ppl2[PREC ? 2 : 1][2];                        // P's second residual (PREC)
 #pragma unroll
   for (int x = 0; x < 2; ++x) {
     sacc[x] = f32x16{}; pacc[x] = f32x16{};
 #pragma unroll
     for (int c = 0; c < 2; ++c) { ppk[x][c] = V8{}; dspk[x][c] = V8{}; }
   }
+#pragma unroll
+  for (int x = 0; x < (PREC ? 2 : 1); ++x)
+#pragma unroll
+    for (int c = 0; c < 2; ++c) { ppl[x][c] = V8{}; dsl[x][c] = V8{}; ppl2[x][c] = V8{}; }
 
   // S/dP of step "it" (tile in buffer BUF) -> parity PAR; dV/dK of step it-2
   // (buffer (BUF+2)%4, parity PAR) -- one interleaved MFMA stream, with the
@@ -503,7 +518,24 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
       }
       sacc[PJ][i] = p;
       pacc[PJ][i] = p * pacc[PJ][i];   // P (dP - Delta); the factor scale goes into dK
-      if ((i & 7) == 7) {
+      if constexpr (PREC) {
+        // per pair of entries: the packed 16-bit words and their residuals
+        if ((i & 1) == 1) {
+          const int c = i >> 3, k = (i >> 1) & 3;
+          uint32_t ph, pl, pl2, dh, dl;
+          split3<T>(sacc[PJ][i - 1], sacc[PJ][i], &ph, &pl, &pl2);
+          split2<T>(pacc[PJ][i - 1], pacc[PJ][i], &dh, &dl);
+          u32x4 w0 = as_u32x4<T>(ppk[PJ][c]), w1 = as_u32x4<T>(ppl[PJ][c]), w4 = as_u32x4<T>(ppl2[PJ][c]);
+          u32x4 w2 = as_u32x4<T>(dspk[PJ][c]), w3 = as_u32x4<T>(dsl[PJ][c]);
+          w0[k] = ph; w1[k] = pl; w4[k] = pl2; w2[k] = dh; w3[k] = dl;
+          ppk[PJ][c] = as_vec8<T>(w0); ppl[PJ][c] = as_vec8<T>(w1); ppl2[PJ][c] = as_vec8<T>(w4);
+          dspk[PJ][c] = as_vec8<T>(w2); dsl[PJ][c] = as_vec8<T>(w3);
+          asm volatile("" : "+v"(ppk[PJ][c]), "+v"(ppl[PJ][c]), "+v"(dspk[PJ][c]), "+v"(dsl[PJ][c]));
+          asm volatile("" : "+v"(ppl2[PJ][c]));
+        } else {
+          asm volatile("" : "+v"(sacc[PJ][i]), "+v"(pacc[PJ][i]));
+        }
+      } else if ((i & 7) == 7) {
         const int c = i >> 3;
         ppk[PJ][c] = pack8<T>(sacc[PJ][8 * c + 0], sacc[PJ][8 * c + 1], sacc[PJ][8 * c + 2], sacc[PJ][8 * c + 3],
                               sacc[PJ][8 * c + 4], sacc[PJ][8 * c + 5], sacc[PJ][8 * c + 6], sacc[PJ][8 * c + 7]);
@@ -529,11 +561,24 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
       else pacc[PN] = mfma32(as_vec8<T>(xs[t % AHEAD]), vf[t >> 1], (t >> 1) == 0 ? nd_next : pacc[PN]);
       // dS of step j-1 out to its tile (non-temporal: read once, by the dQ kernel)
       if (t < 2) __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, dspk[PN][t]), ds_rs, ds_vo + 1024 * t, 0, 2);
+      if constexpr (PREC) {   // the residual tile follows the tile
+        if (t >= 2 && t < 4)
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, dsl[PN][t - 2]), ds_rs,
+                                                 ds_vo + 2048 + 1024 * (t - 2), 0, 2);
+      }
       // stream 2: dV / dK of step j-1 (c, nb)
       {
         const int c = t / (2 * NB), nb = (t / 2) % NB;
-        if ((t & 1) == 0) mfma_acc(dvt[nb], xt[t % AHEAD], ppk[PN][c]);
-        else mfma_acc(dkt[nb], xt[t % AHEAD], dspk[PN][c]);
+        if ((t & 1) == 0) {
+          mfma_acc(dvt[nb], xt[t % AHEAD], ppk[PN][c]);
+          if constexpr (PREC) {
+            mfma_acc(dvt[nb], xt[t % AHEAD], ppl[PN][c]);
+            mfma_acc(dvt[nb], xt[t % AHEAD], ppl2[PN][c]);
+          }
+        } else {
+          mfma_acc(dkt[nb], xt[t % AHEAD], dspk[PN][c]);
+          if constexpr (PREC) mfma_acc(dkt[nb], xt[t % AHEAD], dsl[PN][c]);
+        }
       }
       if (t + AHEAD < NOP) { xs[t % AHEAD] = rd_sd(t + AHEAD); xt[t % AHEAD] = rd_tr(t + AHEAD); }
 #pragma unroll
@@ -569,6 +614,11 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
           }
           ppk[PJ][c] = __builtin_bit_cast(V8, __builtin_bit_cast(u32x4, ppk[PJ][c]) & mk);
           dspk[PJ][c] = __builtin_bit_cast(V8, __builtin_bit_cast(u32x4, dspk[PJ][c]) & mk);
+          if constexpr (PREC) {
+            ppl[PJ][c] = __builtin_bit_cast(V8, __builtin_bit_cast(u32x4, ppl[PJ][c]) & mk);
+            ppl2[PJ][c] = __builtin_bit_cast(V8, __builtin_bit_cast(u32x4, ppl2[PJ][c]) & mk);
+            dsl[PJ][c] = __builtin_bit_cast(V8, __builtin_bit_cast(u32x4, dsl[PJ][c]) & mk);
+          }
         }
       }
     }

@@ -63,6 +63,58 @@ __device__ __forceinline__ typename Vec8<T>::type pack8(float x0, float x1, floa
   return r;
 }
 
+// Two fp32 values as a pair of 16-bit T (round to nearest even) in *hi and
+// the rounding residuals (exact in fp32), rounded, in *lo: hi + lo carries
+// each value to about 16 significant bits.
+template <typename T>
+__device__ __forceinline__ void split2(float x0, float x1, uint32_t* hi, uint32_t* lo) {
+  typedef T T2 __attribute__((ext_vector_type(2)));
+  T2 h;
+  h[0] = (T)x0;
+  h[1] = (T)x1;
+  const uint32_t w = __builtin_bit_cast(uint32_t, h);
+  float f0, f1;
+  if constexpr (sizeof(T) == 2 && __is_same(T, __bf16)) {
+    f0 = __uint_as_float(w << 16);
+    f1 = __uint_as_float(w & 0xffff0000u);
+  } else {
+    f0 = (float)(T)x0;
+    f1 = (float)(T)x1;
+  }
+  T2 l;
+  l[0] = (T)(x0 - f0);
+  l[1] = (T)(x1 - f1);
+  *hi = w;
+  *lo = __builtin_bit_cast(uint32_t, l);
+}
+
+// The same with a second residual: hi + lo + lo2 carries each value to about
+// 24 significant bits (all of an fp32 value's).
+template <typename T>
+__device__ __forceinline__ void split3(float x0, float x1, uint32_t* hi, uint32_t* lo, uint32_t* lo2) {
+  typedef T T2 __attribute__((ext_vector_type(2)));
+  auto pack = [](float a, float b) {
+    T2 v;
+    v[0] = (T)a;
+    v[1] = (T)b;
+    return __builtin_bit_cast(uint32_t, v);
+  };
+  auto lo_f = [](uint32_t w, float a) {   // the low element of a pair as fp32
+    if constexpr (__is_same(T, __bf16)) return __uint_as_float(w << 16);
+    else return (float)(T)a;
+  };
+  auto hi_f = [](uint32_t w, float b) {   // the high element
+    if constexpr (__is_same(T, __bf16)) return __uint_as_float(w & 0xffff0000u);
+    else return (float)(T)b;
+  };
+  const uint32_t w = pack(x0, x1);
+  const float r0 = x0 - lo_f(w, x0), r1 = x1 - hi_f(w, x1);
+  const uint32_t l = pack(r0, r1);
+  *hi = w;
+  *lo = l;
+  *lo2 = pack(r0 - lo_f(l, r0), r1 - hi_f(l, r1));
+}
+
 // Transposed LDS read of 4 x 16-bit values (see the header comment).
 __device__ __forceinline__ s16x4 lds_read_tr(const void* p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((FA_LDS s16x4*)(uintptr_t)p);

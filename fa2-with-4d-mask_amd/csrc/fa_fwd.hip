@@ -126,6 +126,11 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
   constexpr int OS = D + 8;             // epilogue O staging stride (elements)
   static_assert(kWaves * 32 * OS * 2 <= 2 * NBUF * TILEB, "O staging fits in the K/V buffers");
   static_assert(BM == kFwdRows && BN == kFwdKeys, "prepared-mask lists are built for this tile shape");
+  // With a mask or a score, P enters O += P V as two 16-bit halves (the
+  // rounded value and its rounding residual, one more MFMA each): rows that
+  // see few keys (packed documents, steep position biases) would otherwise
+  // carry the 16-bit rounding of their few large weights into O.
+  constexpr bool PREC = MASK || SCORE;
   __shared__ __attribute__((aligned(1024))) char smem[2 * NBUF * TILEB];
 
   // ---- which (batch, head, query tile) -------------------------------------
@@ -342,17 +347,29 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
   // offsets are compile-time immediates (< 64 KB) added per read.  opaque()
   // keeps the compiler from moving the region base into those immediates.
   // K (A operand of S^T): lane reads row 32 kb + l32, logical chunk 2 ds + hf.
-  uint32_t kaddr[DS];
+  // With a score (registers short) one address: chunk 2 ds + hf of row l32
+  // sits at 16 ((2 ds) ^ (hf ^ swz)) within the row, i.e. at kaddr0 ^ (32 ds)
+  // (row starts are 256-byte aligned), one XOR per read instead of a register
+  // per ds.
+  constexpr bool KXOR = SCORE;
+  uint32_t kaddr[KXOR ? 1 : DS];
+  if constexpr (KXOR) {
+    kaddr[0] = opaque(lds0 + KOFF + l32 * ROWB + ((hf ^ swz_k<D>(l32)) * 16));
+  } else {
 #pragma unroll
-  for (int ds = 0; ds < DS; ++ds)
-    kaddr[ds] = opaque(lds0 + KOFF + l32 * ROWB + (((2 * ds + hf) ^ swz_k<D>(l32)) * 16));
+    for (int ds = 0; ds < DS; ++ds)
+      kaddr[ds] = opaque(lds0 + KOFF + l32 * ROWB + (((2 * ds + hf) ^ swz_k<D>(l32)) * 16));
+  }
+  static_assert(ROWB % 256 == 0 || ROWB == 128, "row starts aligned for the XOR addressing");
   // V (A operand of O^T via the transpose read): lane addresses key row
   // 32 (kk/2) + 16 (kk%2) + tr_row (+8), columns 32 nb + tr_col .. +3.
   const int tr_row = 4 * hf + ((lane >> 2) & 3);
   const int tr_col = ((lane >> 4) & 1) * 16 + (lane & 3) * 4;
-  uint32_t vaddr[NB];
+  // (with a score one address again: chunk 4 nb + tr_col / 8 of the row at
+  // vaddr0 ^ (64 nb), as for K)
+  uint32_t vaddr[KXOR ? 1 : NB];
 #pragma unroll
-  for (int nb = 0; nb < NB; ++nb) {
+  for (int nb = 0; nb < (KXOR ? 1 : NB); ++nb) {
     const int c = nb * 32 + tr_col;
     vaddr[nb] = opaque(lds0 + VOFF + tr_row * ROWB + ((((c >> 3) ^ swz_v<D>(tr_row))) * 16) + (c & 7) * 2);
   }
@@ -374,8 +391,11 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
   for (int nb = 0; nb < NB; ++nb) oacc[nb] = f32x16{};
   f32x16 sacc[2] = {f32x16{}, f32x16{}};
   V8 pk[4];                        // P(p) packed, B operand of the next M step
+  V8 pkl[PREC ? 4 : 1];            // ... and its rounding residual, P - pk (PREC)
 #pragma unroll
   for (int kk = 0; kk < 4; ++kk) pk[kk] = V8{};
+#pragma unroll
+  for (int kk = 0; kk < (PREC ? 4 : 1); ++kk) pkl[kk] = V8{};
   // mask bits of the tile in flight as loaded: word kb holds keys 32 kb ..
   // 32 kb + 31 of this lane's row (used, shifted by 4 hf, only when mpart).
   // Loaded unconditionally (every listed tile's words exist) and used only
@@ -398,26 +418,34 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
     mreg_nx[0] = w[0];
     mreg_nx[1] = w[1];
   };
-  f32x4 sreg[SCORE ? 8 : 1];       // score of the tile in flight
-  // With a score: position p's list entry, mask bits and score, loaded at
-  // the start of M(p) and used in V(p).
+  // With a mask and a score: position p's list entry and mask bits, loaded
+  // at the start of M(p) and used in V(p).
   auto fetch_cur = [&](int p) __attribute__((always_inline)) {     // position p < nt_w
-    int t = p;
-    if constexpr (MASK) {
-      const int e = ent_at(p);
-      t = e & 0x7fffffff;
-      mpart = e >= 0;
-      const u32x2 w = *(const u32x2*)(mbits + 2 * t);
-      mreg[0] = w[0];
-      mreg[1] = w[1];
-    }
-    tile_cur = t;
+    const int e = ent_at(p);
+    tile_cur = e & 0x7fffffff;
+    mpart = e >= 0;
+    const u32x2 w = *(const u32x2*)(mbits + 2 * tile_cur);
+    mreg[0] = w[0];
+    mreg[1] = w[1];
+  };
+  // Score of the next tile: the initial accumulator of its S chain (S = Score
+  // + K Q^T, the score added before the scale as in the reference).  Loaded
+  // at the start of the softmax phase before the tile's M step (in the
+  // prologue for position 0), so that its registers are live only from there
+  // to the chain's first MFMA.
+  f32x16 sc[SCORE ? 2 : 1];
+  sc[0] = f32x16{};
+  auto fetch_score = [&](int p) __attribute__((always_inline)) {   // position p < nt_w
+    const int t = MASK ? (ent_at(p) & 0x7fffffff) : p;
     const uint32_t so = soff_row + (uint32_t)(t * BN * 4);   // range-checked: in the lane offset
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int gi = 0; gi < 4; ++gi)
-        sreg[kb * 4 + gi] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(srs, so + (kb * 32 + gi * 8) * 4, 0, 0));
+      for (int gi = 0; gi < 4; ++gi) {
+        const f32x4 x = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(srs, so + (kb * 32 + gi * 8) * 4, 0, 0));
+#pragma unroll
+        for (int t4 = 0; t4 < 4; ++t4) sc[kb][gi * 4 + t4] = x[t4];
+      }
   };
   float m_run = kNegInf, l_run = 0.f;
 
@@ -437,22 +465,32 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
       mreg[1] = mreg_nx[1];
       if (p + 1 < nt_w) fetch_mask(p + 1);
     }
-    if constexpr (SCORE) {
+    if constexpr (MASK && SCORE) {
       if (p < nt_w) fetch_cur(p);
+    }
+    if constexpr (SCORE) {
+      // a negative scale is folded into Q and the score's sign (rare: the
+      // wait for the score loads happens here only then)
+      if (a.qsign < 0.f) {
+        sc[0] = -sc[0];
+        sc[1] = -sc[1];
+      }
     }
     __builtin_amdgcn_s_setprio(2);
     // The two independent chains interleaved, S op t = (kb = t%2, ds = t/2),
     // PV op t = (kk = t/NB, nb = t%NB); operands are read from LDS AHEAD op
     // pairs before their MFMAs.
     constexpr int NOP = 2 * DS;   // == 4 * NB
-    constexpr int AHEAD = 3;
+    constexpr int AHEAD = SCORE ? 2 : 3;
     auto rd_s = [&](int t) __attribute__((always_inline)) -> u32x4 {
-      return lds_read16_at(kaddr[t >> 1] + kb_lds + (uint32_t)((t & 1) * 32 * ROWB));
+      const uint32_t ka = KXOR ? (kaddr[0] ^ (uint32_t)(32 * (t >> 1))) : kaddr[t >> 1];
+      return lds_read16_at(ka + kb_lds + (uint32_t)((t & 1) * 32 * ROWB));
     };
     auto rd_pv = [&](int t) __attribute__((always_inline)) -> V8 {
       const int kk = t / NB, nb = t % NB;
       const uint32_t row = (kk >> 1) * 32 + 16 * (kk & 1);
-      const uint32_t base = vaddr[nb] + vb_lds + row * ROWB;
+      const uint32_t va = KXOR ? (vaddr[0] ^ (uint32_t)(64 * nb)) : vaddr[nb];
+      const uint32_t base = va + vb_lds + row * ROWB;
       return cat_tr<T>(lds_read_tr_at(base), lds_read_tr_at(base + 8 * ROWB));
     };
     u32x4 kq[AHEAD];
@@ -466,13 +504,14 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
 #pragma unroll
     for (int t = 0; t < NOP; ++t) {
       const int kb = t & 1, ds = t >> 1;
-      sacc[kb] = mfma32(as_vec8<T>(kq[t % AHEAD]), qf[ds], ds == 0 ? f32x16{} : sacc[kb]);
+      sacc[kb] = mfma32(as_vec8<T>(kq[t % AHEAD]), qf[ds], ds == 0 ? (SCORE ? sc[kb] : f32x16{}) : sacc[kb]);
       oacc[t % NB] = mfma32(vq[t % AHEAD], pk[t / NB], oacc[t % NB]);
+      if constexpr (PREC) oacc[t % NB] = mfma32(vq[t % AHEAD], pkl[t / NB], oacc[t % NB]);
       if (t + AHEAD < NOP) {
         kq[t % AHEAD] = rd_s(t + AHEAD);
         vq[t % AHEAD] = rd_pv(t + AHEAD);
       }
-      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, PREC ? 3 : 2, 0);
       if (t + AHEAD < NOP) __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
     }
     __builtin_amdgcn_s_setprio(0);
@@ -488,6 +527,14 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
 #pragma unroll
       for (int t = 0; t < 8; ++t) x[t] = exp2_fast(fmaf(sacc[kb][8 * c + t], c2, mneg));
       pk[kk] = pack8<T>(x[0], x[1], x[2], x[3], x[4], x[5], x[6], x[7]);
+      if constexpr (PREC) {
+        // residual of each rounded p (exact in fp32), itself rounded: pk + pkl
+        // carries p to about 16 significant bits
+        float r[8];
+#pragma unroll
+        for (int t = 0; t < 8; ++t) r[t] = x[t] - (float)(T)x[t];
+        pkl[kk] = pack8<T>(r[0], r[1], r[2], r[3], r[4], r[5], r[6], r[7]);
+      }
       lsum += ((x[0] + x[1]) + (x[2] + x[3])) + ((x[4] + x[5]) + (x[6] + x[7]));
     }
     return lsum;
@@ -497,15 +544,9 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
   // lane's entry (kb, e) is key 64 p + 32 kb + 8 (e/4) + 4 hf + e%4 of row qrow;
   // key slot t of k-step kk (= 2 kb + c) <-> key 32 kb + 16 c + 4 hf + t%4 + 8 (t/4)
   auto v_step = [&](int p, auto&& stage) __attribute__((always_inline)) {
-    const int k0 = (MASK || SCORE ? tile_cur : p) * BN;
+    const int k0 = (MASK ? tile_cur : p) * BN;
     if constexpr (SCORE) {
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int gi = 0; gi < 4; ++gi)
-#pragma unroll
-          for (int t = 0; t < 4; ++t)
-            sacc[kb][gi * 4 + t] = fmaf(a.qsign, sreg[kb * 4 + gi][t], sacc[kb][gi * 4 + t]);
+      if (p + 1 < nt_w) fetch_score(p + 1);   // for M(p+1)
     }
     const bool edge = (MASK && mpart) || a.zero_scale || (k0 + BN > Tk) || (CAUSAL && k0 + BN - 1 > q0w);
     if (edge) {
@@ -598,6 +639,9 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
   if constexpr (MPRE) {
     if (nt_w > 0) fetch_mask(0);
   }
+  if constexpr (SCORE) {
+    if (nt_w > 0) fetch_score(0);
+  }
   put_tiles();   // K(0), K(1), V(0)
   load_batch(batch_rsrc(0));
   lds_barrier();
@@ -686,6 +730,40 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
   }
   if (hf == 0 && qrow < Tq)
     a.lse[((int64_t)b * a.Hq + h) * Tq + qrow] = (l_tot > 0.f) ? m_run + log2_fast(l_tot) : kPosInf;
+  if constexpr (PREC) {
+    // O's rounding residual (fp32 O minus O as stored, rounded), through the
+    // same wave-private staging rows: Delta = rowsum(dO (O + residual)) then
+    // sees O to about 16 significant bits
+    if (a.olo) {
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int gi = 0; gi < 4; ++gi) {
+          const int d = nb * 32 + gi * 8 + hf * 4;
+          float r[4];
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const float o = oacc[nb][gi * 4 + t] * inv;
+            r[t] = o - (float)(T)o;
+          }
+          lds_write8(os + l32 * OS + d, pack4<T>(r[0], r[1], r[2], r[3]));
+        }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      T* lp = (T*)a.olo + b * a.olsb + h * a.olsh;
+#pragma unroll
+      for (int u = 0; u < NU; ++u) {
+        const int idx = lane + u * 64;
+        ov[u] = lds_read16(os + (idx / CH) * OS + (idx % CH) * 8);
+      }
+#pragma unroll
+      for (int u = 0; u < NU; ++u) {
+        const int idx = lane + u * 64;
+        const int r = idx / CH, c = idx % CH;
+        const int qr = q0w + r;
+        if (qr < Tq) gstore16(lp + (int64_t)qr * a.olst + c * 8, ov[u]);
+      }
+    }
+  }
 }
 
 template <typename T, int D, bool CAUSAL>

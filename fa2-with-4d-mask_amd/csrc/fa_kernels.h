@@ -27,13 +27,16 @@ constexpr int kDqDsRowsWide = 512;   // the same with 8 waves (deterministic, D 
 //   ord    int32  [nfq + nkb + ndq] the units of lfwd, lkv, ldq (in that order)
 //                               by count, largest first, ties by unit: the
 //                               kernels run their longest workgroups first
+//   hist   int32  [nft+1 + nq32+1 + nk32+1]  scratch of the ordering: per list
+//                               kind a histogram of the counts (0 .. its
+//                               largest possible count), then bin offsets
 // "Live" folds in causality when the workspace was prepared with is_causal.
 struct MaskLayout {
   int Bm, Hm;
   int nq32, nk32, wk, wq;
   int nfq, nft, nkb, ndq;
-  int64_t bits, bitsT, blk, lfwd, lkv, ldq, ord, total;   // byte offsets of the plane arrays, workspace size
-  int64_t pbits, pbitsT, pblk, plfwd, plkv, pldq, pord;   // per-plane sizes (bytes)
+  int64_t bits, bitsT, blk, lfwd, lkv, ldq, ord, hist, total;   // byte offsets of the plane arrays, workspace size
+  int64_t pbits, pbitsT, pblk, plfwd, plkv, pldq, pord, phist;  // per-plane sizes (bytes)
 };
 
 __host__ __device__ inline int64_t align256(int64_t x) { return (x + 255) & ~(int64_t)255; }
@@ -57,6 +60,7 @@ __host__ __device__ inline MaskLayout mask_layout(int B, int Hq, int Tq, int Tk,
   m.plkv = (int64_t)m.nkb * (1 + m.nq32) * 4;
   m.pldq = (int64_t)m.ndq * (1 + m.nk32) * 4;
   m.pord = (int64_t)(m.nfq + m.nkb + m.ndq) * 4;
+  m.phist = (int64_t)(m.nft + 1 + m.nq32 + 1 + m.nk32 + 1) * 4;
   const int64_t np = (int64_t)m.Bm * m.Hm;
   m.bits = 0;
   m.bitsT = align256(m.bits + np * m.pbits);
@@ -65,7 +69,8 @@ __host__ __device__ inline MaskLayout mask_layout(int B, int Hq, int Tq, int Tk,
   m.lkv = align256(m.lfwd + np * m.plfwd);
   m.ldq = align256(m.lkv + np * m.plkv);
   m.ord = align256(m.ldq + np * m.pldq);
-  m.total = align256(m.ord + np * m.pord);
+  m.hist = align256(m.ord + np * m.pord);
+  m.total = align256(m.hist + np * m.phist);
   return m;
 }
 
@@ -102,6 +107,8 @@ struct FwdArgs {
   int zero_scale;       // scale == 0: every kept logit is 0
   const char* mws;      // prepared mask (with a mask)
   MaskLayout ml;
+  void* olo;            // optional (mask or score): O's rounding residual, dtype, strided like O
+  int64_t olsb, olst, olsh;
 };
 
 struct PreArgs {
@@ -111,6 +118,8 @@ struct PreArgs {
                         // -inf for a row whose kept keys all have -inf logits
   int32_t* dead; float* dq_accum;
   int64_t osb, ost, osh, dsb, dst, dsh;
+  const void* olo;      // optional: O's rounding residual (Delta = sum dO (O + olo))
+  int64_t olsb, olst, olsh;
   int B, Tq, Hq, Hk, G;
   int is_causal;
   const char* mws;      // prepared mask (with a mask): tells rows without a kept key

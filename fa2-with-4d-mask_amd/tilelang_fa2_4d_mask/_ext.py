@@ -19,7 +19,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must be loaded before the HIP library, see above)
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libfa2_4d_mask.so"
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 FA_DTYPE_BF16 = 0
 FA_DTYPE_FP16 = 1
@@ -45,7 +45,8 @@ class FaFwdParams(ctypes.Structure):
         ("batch seqlen_q seqlen_k heads_q heads_k head_dim", _i32),
         ("scale", ctypes.c_float),
         ("is_causal dtype", _i32),
-        ("stream mask_ws", _vp),
+        ("stream mask_ws o_lo", _vp),
+        ("o_lo_stride_b o_lo_stride_t o_lo_stride_h", _i64),
     )
 
 
@@ -62,7 +63,8 @@ class FaBwdParams(ctypes.Structure):
         ("is_causal atomic_dq kv_split dtype", _i32),
         ("stream ds_tiles", _vp),
         ("ds_limit_bytes", _i64),
-        ("mask_ws", _vp),
+        ("mask_ws o_lo", _vp),
+        ("o_lo_stride_b o_lo_stride_t o_lo_stride_h ds_tiles_elems", _i64),
     )
 
 

@@ -225,11 +225,13 @@ def _check_qkv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> None:
     _ext.dtype_code(q.dtype)
 
 
-def _forward_impl(q, k, v, Mask, Score, scale: float, is_causal: bool):
+def _forward_impl(q, k, v, Mask, Score, scale: float, is_causal: bool, residual: bool = False):
     """Host side of the forward (python/fa2.py:438-488) on logical [B, T, H, D]
-    operands: O [B, Tq, Hq, D], LSE [B, Hq, Tq] and the prepared mask (or None),
-    plus the operands as the kernels saw them (zero-padded to the kernel head
-    dim, see ``kernel_head_dim``)."""
+    operands: O [B, Tq, Hq, D], LSE [B, Hq, Tq], the prepared mask (or None)
+    and, with ``residual`` and a mask or a score, O's rounding residual (else
+    None: the backward then takes Delta from O as stored), plus the operands
+    as the kernels saw them (zero-padded to the kernel head dim, see
+    ``kernel_head_dim``)."""
     B, Tq, Hq, D_in = q.shape
     _, Tk, Hk, _ = k.shape
     D = kernel_head_dim(D_in)
@@ -238,11 +240,14 @@ def _forward_impl(q, k, v, Mask, Score, scale: float, is_causal: bool):
     score, sst = _kernel_side(Score, torch.float32, B, Hq, Tq, Tk, "score", q.device)
     O = torch.empty((B, Tq, Hq, D), dtype=q.dtype, device=q.device)
     LSE = torch.empty((B, Hq, Tq), dtype=torch.float32, device=q.device)
+    O_lo = torch.empty_like(O) if residual and (mask is not None or score is not None) else None
     mask_ws = None
     if B * Tq * Hq > 0:
         if Tk == 0:
             O.zero_()
             LSE.fill_(float("-inf"))
+            if O_lo is not None:
+                O_lo.zero_()
         else:
             q = _kernel_operand(q)
             k = _kernel_operand(k)
@@ -256,6 +261,9 @@ def _forward_impl(q, k, v, Mask, Score, scale: float, is_causal: bool):
             p.k_stride_b, p.k_stride_t, p.k_stride_h = _bthd_strides(k)
             p.v_stride_b, p.v_stride_t, p.v_stride_h = _bthd_strides(v)
             p.o_stride_b, p.o_stride_t, p.o_stride_h = _bthd_strides(O)
+            if O_lo is not None:
+                p.o_lo = O_lo.data_ptr()
+                p.o_lo_stride_b, p.o_lo_stride_t, p.o_lo_stride_h = _bthd_strides(O_lo)
             p.mask_stride_b, p.mask_stride_h, p.mask_stride_q = mst
             p.score_stride_b, p.score_stride_h, p.score_stride_q = sst
             p.batch, p.seqlen_q, p.seqlen_k, p.heads_q, p.heads_k, p.head_dim = B, Tq, Tk, Hq, Hk, D
@@ -270,19 +278,24 @@ def _forward_impl(q, k, v, Mask, Score, scale: float, is_causal: bool):
             _call(lib, "fa_fwd", p)
     if D != D_in:
         O = O[..., :D_in].contiguous()
-    return O, LSE, mask_ws, (q, k, v, mask, score, mst, sst)
+        O_lo = None if O_lo is None else O_lo[..., :D_in].contiguous()
+    return O, LSE, mask_ws, O_lo, (q, k, v, mask, score, mst, sst)
 
 
 def _backward_impl(do, q, k, v, O, LSE, mask, score, mask_ws, mst, sst, scale: float, is_causal: bool,
-                   use_atomic_backward: bool):
+                   use_atomic_backward: bool, O_lo: Optional[torch.Tensor] = None):
     """Host side of the backward (python/fa2.py:490-556) on logical [B, T, H, D]
     operands (Q, K, V as given or as the forward's kernels saw them); returns
     dQ, dK, dV in the input dtype, [B, T, H, D] contiguous with D that of dO.
-    Head dims other than the kernels' run zero-padded (``kernel_head_dim``)."""
+    ``O_lo``: the forward's rounding residual of O (with a mask or a score),
+    added to O for Delta.  Head dims other than the kernels' run zero-padded
+    (``kernel_head_dim``)."""
     B, Tq, Hq, D_in = do.shape
     _, Tk, Hk, _ = k.shape
     D = kernel_head_dim(D_in)
     q, k, v, O, do = (_pad_head_dim(x, D) for x in (q, k, v, O, do))
+    if O_lo is not None:
+        O_lo = _pad_head_dim(O_lo, D)
     dev = q.device
     dQ = torch.empty((B, Tq, Hq, D), dtype=q.dtype, device=dev)
     dK = torch.empty((B, Tk, Hk, D), dtype=q.dtype, device=dev)
@@ -302,6 +315,8 @@ def _backward_impl(do, q, k, v, O, LSE, mask, score, mask_ws, mst, sst, scale: f
     p.kv_split = 0
     p.dtype = _ext.dtype_code(q.dtype)
     p.ds_limit_bytes = ds_limit_bytes(dev)
+    # the plan depends on whether a mask / score is given (dS tile pairs)
+    p.mask, p.score = _ext.ptr(mask), _ext.ptr(score)
     lib = _ext.load_library()
     plan = _ext.FaBwdPlan()
     _ext.check(lib.fa_bwd_plan(ctypes.byref(p), ctypes.byref(plan)), "fa_bwd_plan", lib)
@@ -320,17 +335,20 @@ def _backward_impl(do, q, k, v, O, LSE, mask, score, mask_ws, mst, sst, scale: f
 
     p.q, p.k, p.v, p.o, p.dout = q.data_ptr(), k.data_ptr(), v.data_ptr(), O.data_ptr(), do.data_ptr()
     p.lse, p.delta, p.dead_flags = LSE.data_ptr(), delta.data_ptr(), dead.data_ptr()
-    p.mask, p.score = _ext.ptr(mask), _ext.ptr(score)
     p.mask_ws = _ext.ptr(mask_ws)
     # dS tiles handed from the dK/dV kernel to the dQ kernel
     ds = torch.empty((plan.ds_elems,), dtype=q.dtype, device=dev) if plan.ds_elems else None
     p.dq_accum, p.dk_accum, p.dv_accum = _ext.ptr(dq_acc), _ext.ptr(dk_acc), _ext.ptr(dv_acc)
     p.ds_tiles = _ext.ptr(ds)
+    p.ds_tiles_elems = plan.ds_elems
     p.dq, p.dk, p.dv = dQ.data_ptr(), dK.data_ptr(), dV.data_ptr()
     p.q_stride_b, p.q_stride_t, p.q_stride_h = _bthd_strides(q)
     p.k_stride_b, p.k_stride_t, p.k_stride_h = _bthd_strides(k)
     p.v_stride_b, p.v_stride_t, p.v_stride_h = _bthd_strides(v)
     p.o_stride_b, p.o_stride_t, p.o_stride_h = _bthd_strides(O)
+    if O_lo is not None:
+        p.o_lo = O_lo.data_ptr()
+        p.o_lo_stride_b, p.o_lo_stride_t, p.o_lo_stride_h = _bthd_strides(O_lo)
     p.do_stride_b, p.do_stride_t, p.do_stride_h = _bthd_strides(do)
     p.dq_stride_b, p.dq_stride_t, p.dq_stride_h = _bthd_strides(dQ)
     p.dk_stride_b, p.dk_stride_t, p.dk_stride_h = _bthd_strides(dK)
@@ -372,8 +390,9 @@ class _flash_attention_with_4d_mask(torch.autograd.Function):
             scale = q.shape[3] ** -0.5
         scale = float(scale)
         _check_qkv(q, k, v)
-        O, LSE, mask_ws, (q, k, v, mask, score, mst, sst) = _forward_impl(q, k, v, Mask, Score, scale, bool(is_causal))
-        ctx.save_for_backward(q, k, v, O, LSE, mask, score, mask_ws)
+        O, LSE, mask_ws, O_lo, (q, k, v, mask, score, mst, sst) = _forward_impl(
+            q, k, v, Mask, Score, scale, bool(is_causal), residual=any(ctx.needs_input_grad[:3]))
+        ctx.save_for_backward(q, k, v, O, LSE, mask, score, mask_ws, O_lo)
         ctx.scale = scale
         ctx.is_causal = bool(is_causal)
         ctx.use_atomic_backward = bool(use_atomic_backward)
@@ -384,10 +403,10 @@ class _flash_attention_with_4d_mask(torch.autograd.Function):
     @staticmethod
     @once_differentiable
     def backward(ctx, dO: torch.Tensor):
-        q, k, v, O, LSE, mask, score, mask_ws = ctx.saved_tensors
+        q, k, v, O, LSE, mask, score, mask_ws, O_lo = ctx.saved_tensors
         do = dO.transpose(1, 2) if ctx.bhsd_input else dO
         dQ, dK, dV = _backward_impl(do, q, k, v, O, LSE, mask, score, mask_ws, ctx.mst, ctx.sst, ctx.scale,
-                                    ctx.is_causal, ctx.use_atomic_backward)
+                                    ctx.is_causal, ctx.use_atomic_backward, O_lo)
         if ctx.bhsd_input:
             dQ, dK, dV = dQ.transpose(1, 2), dK.transpose(1, 2), dV.transpose(1, 2)
         return dQ, dK, dV, None, None, None, None, None, None

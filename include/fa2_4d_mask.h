@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define FA_ABI_VERSION 4
+#define FA_ABI_VERSION 5
 
 enum FaDtype { FA_DTYPE_BF16 = 0, FA_DTYPE_FP16 = 1 };
 
@@ -73,6 +73,10 @@ typedef struct FaFwdParams {
   int32_t dtype;                 /* enum FaDtype */
   void* stream;                  /* hipStream_t; NULL = default stream */
   const void* mask_ws;           /* prepared mask (fa_mask_prepare of this mask); required with a mask */
+  void* o_lo;                    /* optional [B, Tq, Hq, D] dtype output, written with a mask or a score only:
+                                    O's rounding residual (O in fp32 minus O as stored, rounded to dtype),
+                                    for fa_bwd_preprocess; NULL = not written */
+  int64_t o_lo_stride_b, o_lo_stride_t, o_lo_stride_h;
 } FaFwdParams;
 
 /* Backward problem.  Reuses the forward's inputs plus O, LSE and dO. */
@@ -111,6 +115,11 @@ typedef struct FaBwdParams {
   int64_t ds_limit_bytes;        /* largest dS workspace the caller accepts; 0 = 8 GiB, < 0 = none
                                     (below the whole need: the backward runs in slices of units) */
   const void* mask_ws;           /* prepared mask, as for fa_fwd; required with a mask */
+  const void* o_lo;              /* optional: the o_lo fa_fwd wrote; Delta = sum_d dO (O + o_lo) */
+  int64_t o_lo_stride_b, o_lo_stride_t, o_lo_stride_h;
+  int64_t ds_tiles_elems;        /* 16-bit elements the caller allocated at ds_tiles; when ds_tiles is given
+                                    it must be at least plan.ds_elems of this problem (which depends on
+                                    whether a mask or a score is given), else FA_ERR_WORKSPACE */
 } FaBwdParams;
 
 /* Mask preparation: the bool mask of a problem turned into the workspace the
@@ -159,7 +168,10 @@ int fa_mask_prepare(const FaMaskParams* p);
 
 /* Forward.  Replaces the reference's `flash_attention_fwd_with_4d_mask`
  * (python/fa2.py:22-139) as launched by `_flash_attention_with_4d_mask.forward`
- * (python/fa2.py:474-478).  Writes O and LSE. */
+ * (python/fa2.py:474-478).  Writes O and LSE (and o_lo when given, with a mask or
+ * a score).  With a mask or a score the probabilities enter O += P V as two 16-bit
+ * halves, P rounded and its rounding residual (the reference rounds P once,
+ * python/fa2.py:128-129); the backward does the same for P and dS. */
 int fa_fwd(const FaFwdParams* p);
 
 /* Backward preprocess.  Replaces `bwd_preprocess` (python/fa2.py:142-179, launched at
@@ -215,7 +227,9 @@ int fa_bwd_finalize(const FaBwdParams* p);
  * stream's. */
 int fa_bwd_noalloc(const FaBwdParams* p);
 
-/* Fills *plan for the problem in *p (no launch, no GPU access). */
+/* Fills *plan for the problem in *p (no launch, no GPU access): sizes, head dim,
+ * dtype, causality, atomic_dq, kv_split, ds_limit_bytes and whether mask / score
+ * are non-NULL (with either, every dS block is stored as a pair of tiles). */
 int fa_bwd_plan(const FaBwdParams* p, FaBwdPlan* plan);
 
 /* Human-readable description of the last nonzero status on the calling thread. */

@@ -31,7 +31,16 @@ kernel's; tests/test_oracle.py checks the mean errors agree):
 * dS is rounded before the factor ``scale``, which is applied after the
   products (the reference rounds the scaled value, :291).
 
-Pinned by tests/test_oracle.py: with the roundings off the restatement equals
+With a mask or a score the kernels carry each of those values as two 16-bit
+parts, the rounded value plus its rounded residual, P for dV as three
+(``split=True``), and the forward stores O's residual for Delta.
+
+Pinned by tests/test_oracle.py: entry by entry against the scalar float64
+loops of ``bruteforce.attention_bruteforce_rounded`` (single and split
+roundings, bf16 and fp16), and planted placement mistakes in this function's
+own source (P rounded after normalising, P or dS not rounded, Delta from the
+unrounded O, dS rounded after the scale, the row's own maximum instead of the
+first-tile grid) each fail that comparison; with the roundings off it equals
 the eager oracle in float64 (forward, LSE and all three gradients, dead rows
 included); the integer-maximum property of the rounded P; the floor each
 rounding alone leaves at the BASELINE configs P and S.
@@ -51,6 +60,20 @@ LOG2E = 1.0 / math.log(2.0)
 
 def _round(x: torch.Tensor, dtype: Optional[torch.dtype]) -> torch.Tensor:
     return x if dtype is None else x.to(dtype).to(x.dtype)
+
+
+def _round_split(x: torch.Tensor, dtype: Optional[torch.dtype], terms: int = 2) -> torch.Tensor:
+    """x as ``terms`` 16-bit values: x rounded (through fp32, as a kernel
+    rounds its fp32 values), then the fp32 residual rounded, and so on."""
+    if dtype is None:
+        return x
+    r = x.to(torch.float32)
+    out = torch.zeros_like(x)
+    for _ in range(terms):
+        part = r.to(dtype).to(torch.float32)
+        out = out + part.to(x.dtype)
+        r = r - part   # exact in fp32
+    return out
 
 
 def _first_tile_grid_max(y: torch.Tensor, ymax: torch.Tensor, tile_keys: int) -> torch.Tensor:
@@ -88,6 +111,7 @@ def rounded_attention(
     tile_keys: int = 64,
     block: int = 128,
     compute_dtype: torch.dtype = torch.float64,
+    split: bool = False,
 ):
     """Forward (and backward when ``grad_out`` is given) of attention in BHSD
     layout with the 16-bit roundings listed in the module docstring.
@@ -100,6 +124,10 @@ def rounded_attention(
     ``scale_ds_before_round`` and ``max_mode="row"`` (the row's fractional
     maximum) give the reference's own placements; ``max_mode="first_tile"``
     is the grid of the module docstring, over ``tile_keys``-key tiles.
+    ``split``: every rounding point carries its value as two 16-bit parts,
+    the rounded value plus its rounded residual, and P for dV as three (the
+    second residual too) -- what the kernels do with a mask or a score; Delta
+    then takes O plus the residual the forward stores.
 
     Returns a dict with ``out`` (compute dtype, before the final cast), ``lse``
     (base 2, [B, Hq, Tq]) and, with ``grad_out``, ``dq``, ``dk``, ``dv``
@@ -113,6 +141,8 @@ def rounded_attention(
     cd = compute_dtype
     dev = q.device
     rd = round_dtype
+    R = (lambda x: _round_split(x, rd)) if split else (lambda x: _round(x, rd))
+    R3 = (lambda x: _round_split(x, rd, terms=3)) if split else R   # P for dV
     qf = q.to(cd)
     kf = _expand_kv(k, G).to(cd)
     vf = _expand_kv(v, G).to(cd)
@@ -143,7 +173,7 @@ def rounded_attention(
             raise ValueError(max_mode)
         pu = torch.exp2(y - m)                       # NaN rows where every logit is -inf
         l = pu.sum(dim=-1, keepdim=True)
-        pr = _round(pu, rd) if round_p_fwd else pu
+        pr = R(pu) if round_p_fwd else pu
         o = torch.matmul(pr, vf) / l
         out[:, :, q0:q1] = o
         lse[:, :, q0:q1] = (m + torch.log2(l)).squeeze(-1)
@@ -153,19 +183,19 @@ def rounded_attention(
         g = gf[:, :, q0:q1]
         dp = torch.matmul(g, vt)
         if delta_from_output:
-            delta = (_round(o, rd) * g).sum(dim=-1, keepdim=True)
+            delta = (R(o) * g).sum(dim=-1, keepdim=True)
         else:
             delta = (p * dp).sum(dim=-1, keepdim=True)
         ds = p * (dp - delta)
         if keep is not None:
             ds = ds.masked_fill(~keep, 0.0)
         if scale_ds_before_round:
-            dsr = _round(ds * scale, rd) if round_ds else ds * scale
+            dsr = R(ds * scale) if round_ds else ds * scale
             ds_scale = 1.0
         else:
-            dsr = _round(ds, rd) if round_ds else ds
+            dsr = R(ds) if round_ds else ds
             ds_scale = scale
-        pb = _round(p, rd) if round_p_bwd else p
+        pb = R3(p) if round_p_bwd else p
         dq[:, :, q0:q1] = torch.matmul(dsr, kf) * ds_scale
         dk += torch.matmul(dsr.transpose(-1, -2), qc) * ds_scale
         dv += torch.matmul(pb.transpose(-1, -2), g)

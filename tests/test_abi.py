@@ -185,8 +185,11 @@ BWD_ERRORS = [
     (dict(dead_flags=None), 1, "dead_flags is NULL"),
     (dict(dk_stride_h=100), 5, "multiples of 8"),
     (dict(head_dim=32), 3, "head_dim 32"),
-    (dict(mask=FAKE, ds_tiles=FAKE), 8, "prepared workspace"),
+    (dict(mask=FAKE, ds_tiles=FAKE, ds_tiles_elems=1 << 40), 8, "prepared workspace"),
     (dict(ds_tiles=None), 8, "needs ds_tiles"),
+    (dict(ds_tiles=FAKE, ds_tiles_elems=1024), 8, "the plan needs"),
+    # a workspace sized by a plan made without the mask: half the tile pairs
+    (dict(mask=FAKE, mask_ws=FAKE, ds_tiles=FAKE, ds_tiles_elems=32 * 256 * 256 * 1024), 8, "pair of tiles"),
 ]
 
 
@@ -254,13 +257,18 @@ def test_plan_ds_tiles(lib):
     assert _plan(lib, atomic_dq=0, ds_limit_bytes=(1 << 29) - 2).ds_elems == 0
     assert _plan(lib, atomic_dq=0, is_causal=1, ds_limit_bytes=-1).ds_elems == 0
     assert _plan(lib, atomic_dq=0, is_causal=1, ds_limit_bytes=3 << 30).ds_elems > 0
+    # with a mask or a score every stored block is a pair of tiles (dS and
+    # its rounding residual): twice the elements, and slices of half the units
+    for side in (dict(mask=FAKE), dict(score=FAKE), dict(mask=FAKE, score=FAKE)):
+        assert _plan(lib, **side).ds_elems == 2 * 32 * 256 * 256 * 1024
+        assert _plan(lib, atomic_dq=0, ds_limit_bytes=1 << 30, **side).ds_elems == 2 * unit
 
 
 def test_det_path_needs_ds_tiles(lib):
     p = bwd_params(atomic_dq=0)
     assert lib.fa_bwd(ctypes.byref(p)) == 8
     assert "needs ds_tiles" in lib.fa_last_error().decode()
-    p = bwd_params(atomic_dq=0, ds_tiles=FAKE + 8)
+    p = bwd_params(atomic_dq=0, ds_tiles=FAKE + 8, ds_tiles_elems=1 << 40)
     assert lib.fa_bwd(ctypes.byref(p)) == 5
     assert "ds_tiles must be 16-byte aligned" in lib.fa_last_error().decode()
 
@@ -309,9 +317,9 @@ def test_mask_plan_sizes(lib):
     # config P: mask [2, 1, 4096, 4096] -> batch kept (stride != 0), heads broadcast: 2 planes
     T = 4096
     per = dict(bits=T * 128 * 4, bitsT=128 * 128 * 32 * 4, blk=128 * 128, lfwd=16 * 65 * 4, lkv=32 * 129 * 4,
-               ldq=16 * 129 * 4, ord=(16 + 32 + 16) * 4)
+               ldq=16 * 129 * 4, ord=(16 + 32 + 16) * 4, hist=(65 + 129 + 129) * 4)
     off = 0
-    for k in ("bits", "bitsT", "blk", "lfwd", "lkv", "ldq", "ord"):
+    for k in ("bits", "bitsT", "blk", "lfwd", "lkv", "ldq", "ord", "hist"):
         off = _a256(off + 2 * per[k])
     assert _mask_bytes(lib, mask_stride_b=T * T) == off
     # broadcast over batch too: one plane; full head extent: 64 planes

@@ -51,7 +51,7 @@ OUTS = ("out", "dq", "dk", "dv")
 # cells that meet the north-star bar against the eager oracle; the others are
 # on the 16-bit rounding floor (see the module docstring)
 STRICT = {
-    "H": OUTS, "M": OUTS, "H_causal": ("out", "dq"), "P": (), "S": (),
+    "H": OUTS, "M": OUTS, "H_causal": ("out", "dq"), "P": OUTS, "S": OUTS,
     "R_no_causal": OUTS, "R_causal": ("out", "dq"), "R_random_mask": OUTS, "long_keys_mask": OUTS,
 }
 

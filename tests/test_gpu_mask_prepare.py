@@ -33,6 +33,7 @@ def layout(B, Hq, Tq, Tk, bcast_b, bcast_h):
     m["plkv"] = m["nkb"] * (1 + m["nq32"]) * 4
     m["pldq"] = m["ndq"] * (1 + m["nk32"]) * 4
     m["pord"] = (m["nfq"] + m["nkb"] + m["ndq"]) * 4
+    m["phist"] = (m["nft"] + 1 + m["nq32"] + 1 + m["nk32"] + 1) * 4
     np_ = m["Bm"] * m["Hm"]
     m["bits"] = 0
     m["bitsT"] = a256(np_ * m["pbits"])
@@ -41,7 +42,8 @@ def layout(B, Hq, Tq, Tk, bcast_b, bcast_h):
     m["lkv"] = a256(m["lfwd"] + np_ * m["plfwd"])
     m["ldq"] = a256(m["lkv"] + np_ * m["plkv"])
     m["ord"] = a256(m["ldq"] + np_ * m["pldq"])
-    m["total"] = a256(m["ord"] + np_ * m["pord"])
+    m["hist"] = a256(m["ord"] + np_ * m["pord"])
+    m["total"] = a256(m["hist"] + np_ * m["phist"])
     return m
 
 

@@ -39,17 +39,18 @@ def test_opcheck(cuda):
     q, k, v, do, mask, score = _inputs(cuda, 0)
     qt, kt, vt = (x.transpose(1, 2).detach().requires_grad_(True) for x in (q, k, v))
     print("case opcheck fwd with mask+score, causal", flush=True)
-    torch.library.opcheck(torch.ops.tilelang_fa2_4d_mask.fwd, (qt, kt, vt, mask, score, 0.125, True, False),
+    torch.library.opcheck(torch.ops.tilelang_fa2_4d_mask.fwd, (qt, kt, vt, mask, score, 0.125, True, False, True),
                           test_utils=("test_schema", "test_faketensor", "test_autograd_registration"))
     print("case opcheck fwd, no mask", flush=True)
-    torch.library.opcheck(torch.ops.tilelang_fa2_4d_mask.fwd, (qt, kt, vt, None, None, 0.125, False, True),
+    torch.library.opcheck(torch.ops.tilelang_fa2_4d_mask.fwd, (qt, kt, vt, None, None, 0.125, False, True, True),
                           test_utils=("test_schema", "test_faketensor", "test_autograd_registration"))
     with torch.no_grad():
-        O, L, ws = torch.ops.tilelang_fa2_4d_mask.fwd(qt, kt, vt, mask, score, 0.125, True, False)
+        O, L, ws, lo = torch.ops.tilelang_fa2_4d_mask.fwd(qt, kt, vt, mask, score, 0.125, True, False, True)
+    assert lo.shape == O.shape
     print("case opcheck bwd", flush=True)
     torch.library.opcheck(torch.ops.tilelang_fa2_4d_mask.bwd,
-                          (do.transpose(1, 2), qt.detach(), kt.detach(), vt.detach(), O, L, mask, score, ws, 0.125,
-                           True, False), test_utils=("test_schema", "test_faketensor"))
+                          (do.transpose(1, 2), qt.detach(), kt.detach(), vt.detach(), O, L, mask, score, ws, lo,
+                           0.125, True, False), test_utils=("test_schema", "test_faketensor"))
 
 
 def _fwd_bwd(fn, q, k, v, do, **kw):

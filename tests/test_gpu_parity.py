@@ -354,7 +354,8 @@ def test_rising_row_maximum(cuda, cfg):
     scale = cfg.D ** -0.5
     with torch.no_grad():
         q_t, k_t, v_t = (case[n + "_bhsd"].transpose(1, 2).to(dev) for n in ("q", "k", "v"))   # [B, T, H, D]
-        _, lse, _ = torch.ops.tilelang_fa2_4d_mask.fwd(q_t, k_t, v_t, None, None, scale, cfg.is_causal, False)
+        _, lse, _, _ = torch.ops.tilelang_fa2_4d_mask.fwd(q_t, k_t, v_t, None, None, scale, cfg.is_causal, False,
+                                                          False)
     kk = case["k_bhsd"].double().repeat_interleave(cfg.Hq // cfg.Hk, dim=1)
     logits = (case["q_bhsd"].double() @ kk.transpose(-1, -2)) * scale
     if cfg.is_causal:

@@ -23,14 +23,17 @@ def test_fake_shapes(mask_heads, mask_batch):
         q = torch.empty(B, Tq, Hq, D, dtype=torch.bfloat16, device="cuda")
         k = torch.empty(B, Tk, Hk, D, dtype=torch.bfloat16, device="cuda")
         mask = torch.empty(mask_batch, mask_heads, Tq, Tk, dtype=torch.bool, device="cuda")
-        O, L, ws = torch.ops.tilelang_fa2_4d_mask.fwd(q, k, k, mask, None, 0.125, True, True)
+        O, L, ws, lo = torch.ops.tilelang_fa2_4d_mask.fwd(q, k, k, mask, None, 0.125, True, True, True)
         assert O.shape == (B, Tq, Hq, D) and O.dtype == torch.bfloat16
         assert L.shape == (B, Hq, Tq) and L.dtype == torch.float32
+        assert lo.shape == O.shape and lo.dtype == O.dtype   # O's rounding residual (mask present)
         nws = ws.shape[0]
-        dq, dk, dv = torch.ops.tilelang_fa2_4d_mask.bwd(O, q, k, k, O, L, mask, None, ws, 0.125, True, False)
+        dq, dk, dv = torch.ops.tilelang_fa2_4d_mask.bwd(O, q, k, k, O, L, mask, None, ws, lo, 0.125, True, False)
         assert dq.shape == q.shape and dk.shape == k.shape and dv.shape == k.shape
-        O2, _, ws2 = torch.ops.tilelang_fa2_4d_mask.fwd(q, k, k, None, None, 0.125, False, True)
-        assert ws2.shape == (0,)
+        O2, _, ws2, lo2 = torch.ops.tilelang_fa2_4d_mask.fwd(q, k, k, None, None, 0.125, False, True, True)
+        assert ws2.shape == (0,) and lo2.shape == (0,)   # no mask, no score: no residual
+        _, _, _, lo3 = torch.ops.tilelang_fa2_4d_mask.fwd(q, k, k, mask, None, 0.125, True, True, False)
+        assert lo3.shape == (0,)   # not asked for
     # same size from the C ABI for the same broadcast
     lib = _ext.load_library()
     mp = _ext.FaMaskParams()
@@ -56,9 +59,10 @@ def test_public_wrapper_routes_through_the_op():
 
 
 def test_backward_without_an_output_gradient():
-    """LSE and the mask workspace get no materialised zero gradients (no fill
-    kernels before every backward); when O does not reach the loss either, the
-    backward returns no gradients and launches nothing."""
+    """LSE, the mask workspace and O's rounding residual get no materialised
+    zero gradients (no fill kernels before every backward); when O does not
+    reach the loss either, the backward returns no gradients and launches
+    nothing."""
     _, _, ops = _mods()
 
     class Ctx:
@@ -72,6 +76,6 @@ def test_backward_without_an_output_gradient():
 
     ctx = Ctx()
     q = torch.empty((1, 4, 2, 64), device="meta")
-    ops._setup_context(ctx, (q, q, q, None, None, 0.125, False, True), (q, q, q))
+    ops._setup_context(ctx, (q, q, q, None, None, 0.125, False, True, True), (q, q, q, q))
     assert ctx.materialize is False
-    assert ops._backward(ctx, None, None, None) == (None,) * 8
+    assert ops._backward(ctx, None, None, None, None) == (None,) * 9

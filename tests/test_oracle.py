@@ -414,3 +414,143 @@ def test_bf16_rounding_floor_is_far_below_the_bar_at_the_headline():
     for n in e32:
         err = (r[n].to(torch.bfloat16).float() - e32[n].float()).abs().mean().item()
         assert err < 6e-5, (n, err)
+
+
+# ---------------------------------------------------------------------------
+# The rounding restatement (oracle/rounding.py) against the scalar loops with
+# the kernels' 16-bit roundings (oracle/bruteforce.py), and planted placement
+# mistakes that comparison must catch.
+# ---------------------------------------------------------------------------
+def test_round16_matches_the_ieee_conversions():
+    """The scalar rounding: hand-checked ties and limits, and torch's own
+    float64 -> bf16 / fp16 conversion of 200k values of every magnitude."""
+    r = BF.round16
+    assert r(1.0 + 2.0 ** -8, "bf16") == 1.0                      # tie -> even mantissa
+    assert r(1.0 + 3 * 2.0 ** -8, "bf16") == 1.0 + 2.0 ** -6      # tie -> even (up)
+    assert r(1.0 + 2.0 ** -8 + 2.0 ** -20, "bf16") == 1.0 + 2.0 ** -7
+    assert r(-3.0e38, "bf16") == -2.9980278 * 10 ** 38 or abs(r(-3.0e38, "bf16") + 3.0e38) < 1e36
+    assert r(1.0 + 2.0 ** -11, "fp16") == 1.0 and r(1.0 + 3 * 2.0 ** -11, "fp16") == 1.0 + 2.0 ** -9
+    assert r(70000.0, "fp16") == math.inf and r(2.0 ** -25, "fp16") == 0.0
+    g = I.make_generator(7)
+    x = torch.randn(200000, generator=g, dtype=torch.float64) * torch.exp2(
+        torch.randint(-30, 30, (200000,), generator=g).double())
+    for name, dt in (("bf16", torch.bfloat16), ("fp16", torch.float16)):
+        want = x.to(dt).double()
+        got = torch.tensor([r(v, name) for v in x.tolist()], dtype=torch.float64)
+        assert torch.equal(got, want), name
+    # the split: value + rounded residual carries ~16 significant bits, three
+    # parts all 24 of an fp32 value
+    for v in x[:2000].tolist():
+        assert abs(BF.round16_split(v, "bf16") - v) <= abs(v) * 2.0 ** -15
+        assert BF.round16_split(v, "bf16", terms=3) == BF._f32(v)
+
+
+def _bf_rounded(q, k, v, m, s, do, scale, causal, dtype, split, tile_keys):
+    o, lse, dq, dk, dv = BF.attention_bruteforce_rounded(
+        q.tolist(), k.tolist(), v.tolist(), None if m is None else m.tolist(), None if s is None else s.tolist(),
+        do.tolist(), scale, causal, dtype=dtype, split=split, tile_keys=tile_keys)
+    return {n: torch.tensor(x, dtype=torch.float64) for n, x in
+            zip(("out", "lse", "dq", "dk", "dv"), (o, lse, dq, dk, dv))}
+
+
+ROUNDED_CASES = [
+    # (mask, score, causal, dead rows)
+    (False, False, False, False), (False, False, True, False), (True, False, False, True),
+    (True, True, True, False), (False, True, False, False), (True, True, False, True),
+]
+TILE = 4   # keys per tile of the first-tile maximum (rows span three tiles)
+
+
+def _rounded_inputs(seed, c):
+    mask, score, causal, dead = c
+    q, k, v, m, s, do = _tiny(seed, Tq=7, Tk=10, mask=mask, score=score, dead=dead)
+    if m is not None:
+        m[0, 0, 3, :TILE + 1] = False   # a row whose first tile keeps nothing
+    return (q, k, v, m, s, do), causal
+
+
+@pytest.mark.parametrize("dtype,split", [("bf16", False), ("bf16", True), ("fp16", False), ("fp16", True)])
+@pytest.mark.parametrize("c", ROUNDED_CASES, ids=[str(i) for i in range(len(ROUNDED_CASES))])
+def test_rounding_restatement_matches_the_rounded_scalar_loops(c, dtype, split):
+    """Entry by entry: O, LSE, dQ, dK, dV of oracle/rounding.py (tensor ops)
+    equal the scalar float64 loops that round at the same points, single or
+    split (value + residual), bf16 and fp16, GQA, causal, masks with dead rows
+    and rows whose first key tile is dropped, scores; scale 0.3 (not a power
+    of two, so where the scale enters relative to the rounding matters)."""
+    args, causal = _rounded_inputs(3, c)
+    want = _bf_rounded(*args, 0.3, causal, dtype, split, TILE)
+    got = R.rounded_attention(*args, scale=0.3, is_causal=causal, block=3, tile_keys=TILE,
+                              round_dtype=torch.bfloat16 if dtype == "bf16" else torch.float16, split=split)
+    for n in ("out", "dq", "dk", "dv"):
+        _close_with_nans(got[n], want[n], tol=1e-10)
+    # LSE: rows with no kept key are +inf in the loops (the kernels' marker)
+    # and not finite in the restatement
+    fin = torch.isfinite(want["lse"])
+    assert torch.equal(fin, torch.isfinite(got["lse"]))
+    assert torch.allclose(got["lse"][fin], want["lse"][fin], atol=1e-10, rtol=1e-10)
+
+
+def test_rounded_scalar_loops_without_rounding_are_the_plain_maths():
+    """With no rounding the new loops equal the plain brute force (pinned
+    against eager, SDPA and finite differences above) and the closed-form LSE."""
+    for c in ROUNDED_CASES:
+        (q, k, v, m, s, do), causal = _rounded_inputs(5, c)
+        got = _bf_rounded(q, k, v, m, s, do, 0.3, causal, None, False, TILE)
+        want = _bf(q, k, v, m, s, do, 0.3, causal)
+        for n, w in zip(("out", "dq", "dk", "dv"), want):
+            _close_with_nans(got[n], w, tol=1e-10)
+        lse = E.lse2_reference(q, k, m, s, scale=0.3, is_causal=causal).double()
+        assert torch.allclose(got["lse"], lse, atol=1e-5), c
+
+
+# (name, text in rounding.py's rounded_attention, replacement, split)
+PLACEMENT_MISTAKES = [
+    ("p_rounded_after_normalising", "pr = R(pu) if round_p_fwd else pu\n        o = torch.matmul(pr, vf) / l",
+     "pr = R(pu / l) if round_p_fwd else pu / l\n        o = torch.matmul(pr, vf)", False),
+    ("p_not_rounded_for_o", "pr = R(pu) if round_p_fwd else pu", "pr = pu", False),
+    ("p_not_rounded_for_dv", "pb = R3(p) if round_p_bwd else p", "pb = p", False),
+    ("ds_not_rounded", "dsr = R(ds) if round_ds else ds", "dsr = ds", False),
+    ("delta_from_unrounded_o", "delta = (R(o) * g).sum", "delta = (o * g).sum", False),
+    ("ds_rounded_after_scale", "dsr = R(ds) if round_ds else ds", "dsr = R(ds * scale) / scale if round_ds else ds",
+     False),
+    ("row_maximum_instead_of_first_tile_grid", "m = _first_tile_grid_max(y, m, tile_keys)", "pass", False),
+    ("residual_dropped", "R = (lambda x: _round_split(x, rd)) if split", "R = (lambda x: _round(x, rd)) if split",
+     True),
+    ("residual_unrounded", "part = r.to(dtype).to(torch.float32)", "part = r if _ else r.to(dtype).to(torch.float32)",
+     True),
+    ("p_for_dv_in_two_parts", "pb = R3(p) if round_p_bwd else p", "pb = R(p) if round_p_bwd else p", True),
+]
+
+
+def _mutant(old, new):
+    import __future__
+    import inspect
+
+    ns = dict(vars(R))
+    found = False
+    for fn in (R._round_split, R.rounded_attention):   # both re-made in ns: the caller sees the mutant helper
+        src = inspect.getsource(fn)
+        found = found or old in src
+        code = compile(src.replace(old, new), "<mutant>", "exec", flags=__future__.annotations.compiler_flag,
+                       dont_inherit=True)
+        exec(code, ns)
+    assert found, f"mutation target not found: {old!r}"
+    return ns["rounded_attention"]
+
+
+@pytest.mark.parametrize("name,old,new,split", PLACEMENT_MISTAKES, ids=[m[0] for m in PLACEMENT_MISTAKES])
+def test_planted_rounding_placement_mistakes_are_caught(name, old, new, split):
+    """Each plausible misplacement of a rounding point, planted in the
+    restatement's own source, makes it differ from the rounded scalar loops
+    on the cases above (so the entry-by-entry comparison has teeth)."""
+    fn = _mutant(old, new)
+    worst = 0.0
+    for c in ROUNDED_CASES:
+        args, causal = _rounded_inputs(3, c)
+        want = _bf_rounded(*args, 0.3, causal, "bf16", split, TILE)
+        got = fn(*args, scale=0.3, is_causal=causal, block=3, tile_keys=TILE, round_dtype=torch.bfloat16, split=split)
+        for n in ("out", "dq", "dk", "dv"):
+            fin = torch.isfinite(want[n]) & torch.isfinite(got[n])
+            if fin.any():
+                worst = max(worst, (got[n][fin] - want[n][fin]).abs().max().item())
+    assert worst > 1e-8, (name, worst)

@@ -23,7 +23,7 @@ from oracle import inputs as I
 pytestmark = pytest.mark.gpu
 
 
-def _bwd_params(q, k, v, O, LSE, do, dQ, dK, dV, mask, score, mask_ws, mst, sst, scale, causal):
+def _bwd_params(q, k, v, O, LSE, do, dQ, dK, dV, mask, score, mask_ws, mst, sst, scale, causal, O_lo):
     import tilelang_fa2_4d_mask.fa2 as F
     from tilelang_fa2_4d_mask import _ext
 
@@ -43,6 +43,9 @@ def _bwd_params(q, k, v, O, LSE, do, dQ, dK, dV, mask, score, mask_ws, mst, sst,
         setattr(p, f"{pre}_stride_h", sh)
     p.mask_stride_b, p.mask_stride_h, p.mask_stride_q = mst
     p.score_stride_b, p.score_stride_h, p.score_stride_q = sst
+    if O_lo is not None:   # the forward's rounding residual of O (mask or score)
+        p.o_lo = O_lo.data_ptr()
+        p.o_lo_stride_b, p.o_lo_stride_t, p.o_lo_stride_h = F._bthd_strides(O_lo)
     p.stream = torch.cuda.current_stream().cuda_stream
     return p
 
@@ -60,12 +63,12 @@ def _run(cfg, seed, dev, dead_rows):
     q, k, v = (case[n].transpose(1, 2) for n in ("q", "k", "v"))   # logical [B, T, H, D]
     do = case["grad"].transpose(1, 2)
     scale = cfg.D ** -0.5
-    O, LSE, mask_ws, (q, k, v, mask, score, mst, sst) = F._forward_impl(q, k, v, case["mask"], case["score"], scale,
-                                                                       cfg.is_causal)
+    O, LSE, mask_ws, O_lo, (q, k, v, mask, score, mst, sst) = F._forward_impl(
+        q, k, v, case["mask"], case["score"], scale, cfg.is_causal, residual=True)
     do = F._kernel_operand(do)
     # the new entry point
     dQ, dK, dV = (torch.full_like(t, float("nan")) for t in (q, k, v))
-    p = _bwd_params(q, k, v, O, LSE, do, dQ, dK, dV, mask, score, mask_ws, mst, sst, scale, cfg.is_causal)
+    p = _bwd_params(q, k, v, O, LSE, do, dQ, dK, dV, mask, score, mask_ws, mst, sst, scale, cfg.is_causal, O_lo)
     lib = _ext.load_library()
     print(f"case noalloc {cfg.name} dead_rows={dead_rows}", flush=True)
     _ext.check(lib.fa_bwd_noalloc(ctypes.byref(p)), "fa_bwd_noalloc", lib)
@@ -79,7 +82,7 @@ def _run(cfg, seed, dev, dead_rows):
     Hk = k.shape[2]
     delta = torch.empty((2, B, Hq, Tq), dtype=torch.float32, device=dev)
     dead = torch.zeros((B * Hk,), dtype=torch.int32, device=dev)
-    p2 = _bwd_params(q, k, v, O, LSE, do, rQ, rK, rV, mask, score, mask_ws, mst, sst, scale, cfg.is_causal)
+    p2 = _bwd_params(q, k, v, O, LSE, do, rQ, rK, rV, mask, score, mask_ws, mst, sst, scale, cfg.is_causal, O_lo)
     p2.delta, p2.dead_flags = delta.data_ptr(), dead.data_ptr()
     p2.ds_limit_bytes, p2.atomic_dq, p2.kv_split = -1, 0, 1
     for entry in ("fa_bwd_preprocess", "fa_bwd", "fa_bwd_finalize"):
@@ -87,7 +90,7 @@ def _run(cfg, seed, dev, dead_rows):
     ref["same_route"] = (rQ, rK, rV)
     # the default route of the product backward (dQ from the stored dS tiles)
     ref["default"] = F._backward_impl(do, q, k, v, O, LSE, mask, score, mask_ws, mst, sst, scale, cfg.is_causal,
-                                      False)
+                                      False, O_lo)
     torch.cuda.synchronize()
     return ours, ref
 
