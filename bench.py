@@ -21,8 +21,11 @@ is the median, with the 20/80 % quantiles beside it, and
 ``ms_per_step_window`` the synchronised wall time of the whole loop per step
 (flushes included).  ``peak_mem_mib`` is the peak device memory one step
 allocates beyond what is live before it (throughput_check.py:218-243);
-``ds_limit_bytes`` the dS workspace limit in force (an eighth of free device
-memory, at most 8 GiB).
+``ds_limit_bytes`` the dS workspace limit in force (the library default,
+4 GiB, unless ``--ds-limit`` sets one).  ``breakdown`` also times the headline
+fwd and fwd+bwd replayed from a captured HIP graph (the reference's
+``--cudagraph`` mode, benchmark/throughput_check.py:249-250): the same kernels
+without the host work of the Python and autograd layers between launches.
 
 ``roofline`` is for the dominant kernel of the step, the dK/dV kernel launched
 by ``fa_bwd`` on the deterministic path: 4 GEMMs (S, dP, dV, dK), i.e.
@@ -190,6 +193,22 @@ def time_steps(torch, fn, steps: int, warmup: int, record_events, flush):
     per_kernel = {name: statistics.mean(v) for name, v in ev.elapsed_ms().items()}
     return {"ms": statistics.median(per), "ms_p20": q[1], "ms_p80": q[7],
             "ms_window": (t1 - t0) * 1e3 / steps}, per_kernel
+
+
+def graph_of(torch, fn):
+    """``fn`` captured into a HIP graph (after two warm-up calls on a side
+    stream, as torch.cuda.graph requires); returns the graph's replay."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(2):
+            fn()
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    torch.cuda.synchronize()
+    return g
 
 
 def peak_extra_mib(torch, fn, dev) -> float:
@@ -382,6 +401,28 @@ def main() -> int:
         log(f"{name:22s} {ms:8.3f} ms (p20 {tm['ms_p20']:.3f}, p80 {tm['ms_p80']:.3f})  {tf:8.1f} TFLOPS  "
             f"({100 * tf / PEAK_TFLOPS:5.1f}% of peak)  peak extra {results[name]['peak_extra_mib']} MiB  kernels {kern}")
 
+    # the headline fwd and fwd+bwd replayed from captured graphs
+    for name, mode in (("fwd_graph", "fwd"), ("fwd_bwd_graph", "fwd_bwd")):
+        if mode == "fwd":
+            step = fwd(False)
+        else:
+            def step():
+                q.grad = k.grad = v.grad = None
+                api.tilelang_flash_attention(q, k, v, is_causal=False, use_atomic_backward=False).backward(do)
+        g = graph_of(torch, step)
+        tm, _ = time_steps(torch, g.replay, args.steps, args.warmup, record_kernel_events, flush)
+        ms = tm["ms"]
+        tf = conv_flops(mode, False) / (ms * 1e-3) * 1e-12
+        eager = results["fwd" if mode == "fwd" else "fwd_bwd"]["ms"]
+        results[name] = {"ms": round(ms, 4), "ms_p20": round(tm["ms_p20"], 4), "ms_p80": round(tm["ms_p80"], 4),
+                         "tflops": round(tf, 2), "frac_of_peak": round(tf / PEAK_TFLOPS, 4),
+                         "eager_minus_graph_ms": round(eager - ms, 4)}
+        log(f"{name:22s} {ms:8.3f} ms  {tf:8.1f} TFLOPS ({100 * tf / PEAK_TFLOPS:5.1f}% of peak), eager - graph "
+            f"{eager - ms:+.3f} ms")
+        del g
+        q.grad = k.grad = v.grad = None
+        torch.cuda.empty_cache()
+
     side = {}
     if not args.no_side_configs:
         del q, k, v
@@ -451,7 +492,7 @@ def main() -> int:
     fwd_achieved = 4.0 * B * HQ * T * T * D / (fwd_kernel_ms * 1e-3) * 1e-12
     for name, r in results.items():
         causal = "causal" in name
-        km = r["kernel_ms"]
+        km = r.get("kernel_ms", {})
         if "fa_fwd" in km:
             r["fwd_kernel_tflops"] = round(conv_flops("fwd", causal) / (km["fa_fwd"] * 1e-3) * 1e-12, 2)
         if "fa_bwd" in km:

@@ -96,13 +96,17 @@ int launch_status(hipError_t e, const char* what) {
 // With a mask or a score each tile is a pair: dS rounded, then its rounding
 // residual (the dQ kernel adds both products).
 int ds_tile_parts(const FaBwdParams* p) { return p->mask || p->score ? 2 : 1; }
+// Default limit (ds_limit_bytes = 0): a constant, so the route, the slices and
+// the head-group split depend on the problem alone.  The headline shape (B1
+// T8192 Hq32 Hk8 D128) needs exactly 4 GiB non-causal and runs unsliced.
+constexpr int64_t kDsLimitDefault = (int64_t)4 << 30;
 int64_t ds_unit_elems(const FaBwdParams* p) {
   const int64_t nq32 = (p->seqlen_q + 31) / 32, nk32 = (p->seqlen_k + 31) / 32;
   const int64_t plane = fa::ds_row(nq32, nk32, p->is_causal != 0);
   return (int64_t)(p->heads_q / p->heads_k) * plane * 1024 * ds_tile_parts(p);   // one unit: the group's planes
 }
 int64_t ds_slice_units(const FaBwdParams* p) {
-  const int64_t limit = p->ds_limit_bytes == 0 ? (int64_t)8 << 30 : p->ds_limit_bytes;
+  const int64_t limit = p->ds_limit_bytes == 0 ? kDsLimitDefault : p->ds_limit_bytes;
   if (limit < 0) return 0;
   const int64_t units = (int64_t)p->batch * p->heads_k, unit = ds_unit_elems(p);
   if (unit <= 0) return units;
@@ -181,9 +185,11 @@ int choose_split(const FaBwdParams* p) {
   // (key block kt walks the rows from kt on); when the backward runs in slices
   // (long sequences) twice as many keep each slice's tail short (measured:
   // T 16384 causal 10.1 -> 8.9 ms), while a single launch at the headline
-  // size is faster without the split's fp32 slabs.
+  // size is faster without the split's fp32 slabs.  Sliced non-causal
+  // launches aim at one workgroup per CU (equal work: one round), which
+  // halves the split and its slabs (H with a 1 GiB limit: -2.4 %).
   const bool sliced = units < (int64_t)p->batch * p->heads_k;
-  const int64_t target = p->is_causal && sliced ? 1024 : 512;
+  const int64_t target = sliced ? (p->is_causal ? 1024 : kCus) : 512;
   int split = 1;
   while (split * 2 <= G && G % (split * 2) == 0 && base * split < target) split *= 2;
   return split;

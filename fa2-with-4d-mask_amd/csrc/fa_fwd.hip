@@ -116,10 +116,14 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
   constexpr int IPW = NI / kWaves;      // ... staged by each wave
   constexpr int RPI = 1024 / ROWB;      // tile rows per slot
   constexpr int NSTG = 2 * IPW;         // staging registers (x 16 bytes) per lane: K + V
+  // With a score at head dim 128 the registers are short (the score of the
+  // next tile, P and its residual): each wave's Q rows live in LDS instead of
+  // 32 registers (swizzled like K rows, read as the S MFMA's B operand).
+  constexpr bool QLDS = SCORE && D == 128;
   // LDS buffers per tile kind: with four, a workgroup barrier every second
   // phase pair suffices; causal workgroups (short, ragged key ranges) run
-  // faster with three and a barrier every pair.
-  constexpr int NBUF = CAUSAL ? 3 : 4;
+  // faster with three and a barrier every pair; with Q in LDS three fit.
+  constexpr int NBUF = CAUSAL || QLDS ? 3 : 4;
   constexpr int KOFF = 0, VOFF = NBUF * TILEB;
   static_assert(NI % kWaves == 0 && IPW >= 1, "staging split");
   static_assert(NBUF * TILEB <= 65536, "buffer + row offsets fit the 16-bit DS immediate");
@@ -131,7 +135,9 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
   // see few keys (packed documents, steep position biases) would otherwise
   // carry the 16-bit rounding of their few large weights into O.
   constexpr bool PREC = MASK || SCORE;
-  __shared__ __attribute__((aligned(1024))) char smem[2 * NBUF * TILEB];
+  constexpr int QOFF = 2 * NBUF * TILEB;                 // Q rows (QLDS): 32 per wave
+  constexpr int QBYTES = QLDS ? kWaves * 32 * ROWB : 0;
+  __shared__ __attribute__((aligned(1024))) char smem[2 * NBUF * TILEB + QBYTES];
 
   // ---- which (batch, head, query tile) -------------------------------------
   // Logical order (b, kv-head, [query tile rank, head in group]), with a
@@ -166,7 +172,7 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
   const T* __restrict__ vp = (const T*)a.v + b * a.vsb + kvh * a.vsh;
 
   // ---- Q fragment: lane holds Q[qrow][16 ds + 8 hf + 0..7] -------------------
-  V8 qf[DS];
+  V8 qf[QLDS ? 1 : DS];
   auto load_q = [&]() __attribute__((always_inline)) {
     const uint32_t neg = a.qsign < 0.f ? 0x80008000u : 0u;
     const T* src = qp + (int64_t)min(qrow, Tq - 1) * a.qst + hf * 8;
@@ -174,7 +180,7 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
     for (int ds = 0; ds < DS; ++ds) {
       u32x4 x = gload16(src + ds * 16);
       x ^= neg;
-      qf[ds] = as_vec8<T>(x);
+      qf[QLDS ? 0 : ds] = as_vec8<T>(x);
     }
   };
 
@@ -361,6 +367,18 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
       kaddr[ds] = opaque(lds0 + KOFF + l32 * ROWB + (((2 * ds + hf) ^ swz_k<D>(l32)) * 16));
   }
   static_assert(ROWB % 256 == 0 || ROWB == 128, "row starts aligned for the XOR addressing");
+  // Q rows in LDS (QLDS): chunk 2 ds + hf of row l32 at qaddr ^ (32 ds)
+  uint32_t qaddr = 0;
+  if constexpr (QLDS) qaddr = opaque(lds0 + QOFF + (wave * 32 + l32) * ROWB + ((hf ^ swz_k<D>(l32)) * 16));
+  auto put_q = [&]() __attribute__((always_inline)) {
+    const uint32_t neg = a.qsign < 0.f ? 0x80008000u : 0u;
+    const T* src = qp + (int64_t)min(qrow, Tq - 1) * a.qst + hf * 8;
+    u32x4 x[DS];
+#pragma unroll
+    for (int ds = 0; ds < DS; ++ds) x[ds] = gload16(src + ds * 16) ^ neg;
+#pragma unroll
+    for (int ds = 0; ds < DS; ++ds) lds_write16_at(qaddr ^ (uint32_t)(32 * ds), x[ds]);
+  };
   // V (A operand of O^T via the transpose read): lane addresses key row
   // 32 (kk/2) + 16 (kk%2) + tr_row (+8), columns 32 nb + tr_col .. +3.
   const int tr_row = 4 * hf + ((lane >> 2) & 3);
@@ -495,24 +513,35 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
     };
     u32x4 kq[AHEAD];
     V8 vq[AHEAD];
+    u32x4 qv[2];   // Q chunks ds and ds + 1 (QLDS)
 #pragma unroll
     for (int t = 0; t < AHEAD; ++t) {
       kq[t] = rd_s(t);
       vq[t] = rd_pv(t);
     }
-    __builtin_amdgcn_sched_group_barrier(0x100, 3 * AHEAD, 0);
+    if constexpr (QLDS) qv[0] = lds_read16_at(qaddr);
+    __builtin_amdgcn_sched_group_barrier(0x100, 3 * AHEAD + (QLDS ? 1 : 0), 0);
 #pragma unroll
     for (int t = 0; t < NOP; ++t) {
       const int kb = t & 1, ds = t >> 1;
-      sacc[kb] = mfma32(as_vec8<T>(kq[t % AHEAD]), qf[ds], ds == 0 ? (SCORE ? sc[kb] : f32x16{}) : sacc[kb]);
+      const V8 qb = QLDS ? as_vec8<T>(qv[ds & 1]) : qf[QLDS ? 0 : ds];
+      sacc[kb] = mfma32(as_vec8<T>(kq[t % AHEAD]), qb, ds == 0 ? (SCORE ? sc[kb] : f32x16{}) : sacc[kb]);
       oacc[t % NB] = mfma32(vq[t % AHEAD], pk[t / NB], oacc[t % NB]);
       if constexpr (PREC) oacc[t % NB] = mfma32(vq[t % AHEAD], pkl[t / NB], oacc[t % NB]);
       if (t + AHEAD < NOP) {
         kq[t % AHEAD] = rd_s(t + AHEAD);
         vq[t % AHEAD] = rd_pv(t + AHEAD);
       }
+      // Q chunk ds + 1, two ops before its first use (its slot last served ds - 1)
+      const bool qrd = QLDS && kb == 0 && ds + 1 < DS;
+      if (qrd) qv[(ds + 1) & 1] = lds_read16_at(qaddr ^ (uint32_t)(32 * (ds + 1)));
       __builtin_amdgcn_sched_group_barrier(0x008, PREC ? 3 : 2, 0);
-      if (t + AHEAD < NOP) __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
+      if (t + AHEAD < NOP) {
+        if (qrd) __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+        else __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
+      } else if (qrd) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
     }
     __builtin_amdgcn_s_setprio(0);
   };
@@ -635,7 +664,8 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
 #pragma unroll
     for (int u = 0; u < TILEB / (kThreads * 16); ++u) lds_write16(z + (tid + u * kThreads) * 16, u32x4{0, 0, 0, 0});
   }
-  load_q();
+  if constexpr (QLDS) put_q();
+  else load_q();
   if constexpr (MPRE) {
     if (nt_w > 0) fetch_mask(0);
   }

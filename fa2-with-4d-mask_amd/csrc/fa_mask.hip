@@ -233,87 +233,107 @@ __global__ __launch_bounds__(256) void mask_lists_kernel(const MaskArgs a) {
 // One workgroup per (plane, list kind): the units of the lists in count
 // order, largest first, ties by unit, by a counting sort over the counts
 // (0 .. m, m the largest possible count: the tiles, steps or key steps of a
-// list row) with the histogram in the workspace (hist):
+// list row):
 //   1. histogram of the counts (atomic adds);
 //   2. bin offsets, descending: start(c) = #units with a count above c (each
-//      thread sums a contiguous range of bins, a scan over the 256 partial
-//      sums, then each thread writes its range's offsets);
+//      thread sums a contiguous range of bins, a log-step scan over the 256
+//      partial sums, then each thread writes its range's offsets);
 //   3. stable scatter: units in chunks of 256, in unit order; a unit's rank
 //      among the units of its chunk with the same count (the chunk's counts
 //      in LDS) added to its bin's offset, which the chunk's last such unit
 //      then advances.
-// O(n + m) work (the all-pairs ranking before it was O(n^2) in one
-// workgroup).  The histogram is read and written with device-scope atomics
-// (the L2), so no wave reads a stale line from its CU's L1.
-__device__ __forceinline__ int32_t ld_rlx(const int32_t* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_rlx(int32_t* p, int32_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-// Workgroup barrier after which every wave sees the others' histogram
-// atomics (device-scope fences around it: the atomics have completed).
-__device__ __forceinline__ void sync_hist() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-  __syncthreads();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-}
+// O(n + m) work (an all-pairs ranking is O(n^2) in one workgroup).  The
+// histogram sits in LDS when it fits (m < kHistLds), else in the workspace
+// (hist), read and written with device-scope atomics (the L2: no wave reads
+// a stale line from its CU's L1) between device-scope fences.
+constexpr int kHistLds = 4096;
 
-__global__ __launch_bounds__(256) void mask_order_kernel(const MaskArgs a) {
-  const MaskLayout& ml = a.ml;
-  const int pm = blockIdx.x, kind = blockIdx.y, tid = threadIdx.x;
-  const int n = kind == 0 ? ml.nfq : (kind == 1 ? ml.nkb : ml.ndq);
-  const int m = kind == 0 ? ml.nft : (kind == 1 ? ml.nq32 : ml.nk32);   // largest possible count
-  const int64_t stride = 1 + m;
-  const int32_t* cnt = (const int32_t*)(a.ws + (kind == 0 ? ml.lfwd + pm * ml.plfwd
-                                                : (kind == 1 ? ml.lkv + pm * ml.plkv : ml.ldq + pm * ml.pldq)));
-  int32_t* ord = (int32_t*)mask_order(ml, a.ws, pm, kind);
-  int32_t* H = (int32_t*)(a.ws + ml.hist + pm * ml.phist) +
-               (kind == 0 ? 0 : (kind == 1 ? ml.nft + 1 : ml.nft + 1 + ml.nq32 + 1));
-  __shared__ int32_t part[256];
-  __shared__ int32_t cs[256];
+struct LdsHist {
+  int32_t* h;
+  __device__ int32_t ld(int c) const { return h[c]; }
+  __device__ void st(int c, int32_t v) const { h[c] = v; }
+  __device__ void add1(int c) const { atomicAdd(h + c, 1); }
+  __device__ void sync() const { __syncthreads(); }
+};
+struct GlobalHist {
+  int32_t* h;
+  __device__ int32_t ld(int c) const { return __hip_atomic_load(h + c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+  __device__ void st(int c, int32_t v) const { __hip_atomic_store(h + c, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+  __device__ void add1(int c) const { __hip_atomic_fetch_add(h + c, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+  __device__ void sync() const {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    __syncthreads();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  }
+};
 
+template <typename Hist>
+__device__ void order_units(const Hist& H, const int32_t* cnt, int64_t stride, int n, int m, int32_t* ord,
+                            int32_t* part, int32_t* cs) {
+  const int tid = threadIdx.x;
   // 1. histogram
-  for (int c = tid; c <= m; c += 256) st_rlx(H + c, 0);
-  sync_hist();
-  for (int i = tid; i < n; i += 256) __hip_atomic_fetch_add(H + cnt[i * stride], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  sync_hist();
-
-  // 2. descending offsets; thread t owns bins [lo, hi), threads of higher
-  // bins come first in the order
+  for (int c = tid; c <= m; c += 256) H.st(c, 0);
+  H.sync();
+  for (int i = tid; i < n; i += 256) H.add1(cnt[i * stride]);
+  H.sync();
+  // 2. descending offsets: thread t owns bins [lo, hi); the bins of the
+  // threads above it come first in the order
   const int per = (m + 1 + 255) / 256;
   const int lo = min(m + 1, tid * per), hi = min(m + 1, lo + per);
   int32_t sum = 0;
-  for (int c = lo; c < hi; ++c) sum += ld_rlx(H + c);
+  for (int c = lo; c < hi; ++c) sum += H.ld(c);
   part[tid] = sum;
   __syncthreads();
-  int32_t above = 0;   // units with a count in the bins of threads above this one
-  for (int t = tid + 1; t < 256; ++t) above += part[t];
+  // inclusive suffix sums over the 256 partial sums, log steps
+  for (int d = 1; d < 256; d <<= 1) {
+    const int32_t x = tid + d < 256 ? part[tid + d] : 0;
+    __syncthreads();
+    part[tid] += x;
+    __syncthreads();
+  }
+  int32_t above = part[tid] - sum;   // units in the bins of the threads above
   for (int c = hi - 1; c >= lo; --c) {
-    const int32_t h = ld_rlx(H + c);
-    st_rlx(H + c, above);
+    const int32_t h = H.ld(c);
+    H.st(c, above);
     above += h;
   }
-  sync_hist();
-
+  H.sync();
   // 3. stable scatter
   for (int i0 = 0; i0 < n; i0 += 256) {
-    const int i = i0 + tid;
+    const int i = i0 + tid, nc = min(256, n - i0);
     const int c = i < n ? cnt[i * stride] : -1;
     cs[tid] = c;
     __syncthreads();
     int r = 0;
     bool last = true;
-    for (int j = 0; j < 256; ++j) {
+    for (int j = 0; j < nc; ++j) {
       const bool same = cs[j] == c;
       r += (same & (j < tid)) ? 1 : 0;
       last &= !(same & (j > tid));
     }
-    const int32_t base = i < n ? ld_rlx(H + c) : 0;
+    const int32_t base = i < n ? H.ld(c) : 0;
     if (i < n) ord[base + r] = i;
     __syncthreads();   // every offset of this chunk read before any advances
-    if (i < n && last) st_rlx(H + c, base + r + 1);
-    sync_hist();
+    if (i < n && last) H.st(c, base + r + 1);
+    H.sync();
+  }
+}
+
+__global__ __launch_bounds__(256) void mask_order_kernel(const MaskArgs a) {
+  const MaskLayout& ml = a.ml;
+  const int pm = blockIdx.x, kind = blockIdx.y;
+  const int n = kind == 0 ? ml.nfq : (kind == 1 ? ml.nkb : ml.ndq);
+  const int m = kind == 0 ? ml.nft : (kind == 1 ? ml.nq32 : ml.nk32);   // largest possible count
+  const int32_t* cnt = (const int32_t*)(a.ws + (kind == 0 ? ml.lfwd + pm * ml.plfwd
+                                                : (kind == 1 ? ml.lkv + pm * ml.plkv : ml.ldq + pm * ml.pldq)));
+  int32_t* ord = (int32_t*)mask_order(ml, a.ws, pm, kind);
+  __shared__ int32_t part[256], cs[256], hl[kHistLds];
+  if (m < kHistLds) {
+    order_units(LdsHist{hl}, cnt, 1 + m, n, m, ord, part, cs);
+  } else {
+    int32_t* hg = (int32_t*)(a.ws + ml.hist + pm * ml.phist) +
+                  (kind == 0 ? 0 : (kind == 1 ? ml.nft + 1 : ml.nft + 1 + ml.nq32 + 1));
+    order_units(GlobalHist{hg}, cnt, 1 + m, n, m, ord, part, cs);
   }
 }
 

@@ -42,15 +42,14 @@ from torch.autograd.function import once_differentiable
 from . import _ext
 
 # Largest dS workspace (bytes) the backward may allocate to hand dS from the
-# dK/dV kernel to the dQ kernel.  0 = automatic: an eighth of the device memory
-# that is free (to the driver or in torch's cache) at the call, at most 8 GiB
-# (the library's own default; also used under graph capture, where the query is
-# not made); negative = never (dQ is then recomputed from Q, K, V, dO: O(T)
-# extra memory, as the reference's backward).  Below the whole need the
-# backward runs in slices of (batch, kv-head) units.
+# dK/dV kernel to the dQ kernel.  0 = the default, DS_LIMIT_DEFAULT (the
+# library's own default; a constant, so that the backward's route, slices and
+# head-group split depend on the problem alone: calls are bitwise repeatable
+# whatever the allocator holds); negative = never (dQ is then recomputed from
+# Q, K, V, dO: O(T) extra memory, as the reference's backward).  Below the
+# whole need the backward runs in slices of (batch, kv-head) units.
 DS_LIMIT_BYTES = 0
-DS_LIMIT_CAP = 8 << 30
-DS_LIMIT_FREE_FRACTION = 8
+DS_LIMIT_DEFAULT = 4 << 30
 
 
 # Head dims the kernels are built for.
@@ -75,18 +74,10 @@ def _pad_head_dim(x: torch.Tensor, Dp: int) -> torch.Tensor:
     return x if D == Dp else torch.nn.functional.pad(x, (0, Dp - D))
 
 
-def ds_limit_bytes(device: torch.device) -> int:
-    """The dS workspace limit a backward on ``device`` uses now (see DS_LIMIT_BYTES)."""
-    if DS_LIMIT_BYTES != 0:
-        return int(DS_LIMIT_BYTES)
-    if torch.cuda.is_current_stream_capturing():
-        return DS_LIMIT_CAP
-    free, _ = torch.cuda.mem_get_info(device)
-    # the nested statistics: memory_reserved()/memory_allocated() flatten the
-    # whole dictionary each (≈60 µs of host time per backward)
-    st = torch.cuda.memory_stats_as_nested_dict(device)
-    cached = st["reserved_bytes"]["all"]["current"] - st["allocated_bytes"]["all"]["current"] if st else 0
-    return max(1, min(DS_LIMIT_CAP, (free + cached) // DS_LIMIT_FREE_FRACTION))
+def ds_limit_bytes(device: Optional[torch.device] = None) -> int:
+    """The dS workspace limit a backward uses (see DS_LIMIT_BYTES); the same
+    on every device and in every memory state."""
+    return int(DS_LIMIT_BYTES) if DS_LIMIT_BYTES != 0 else DS_LIMIT_DEFAULT
 
 
 def _norm_strides(x: torch.Tensor) -> tuple:

@@ -112,7 +112,7 @@ typedef struct FaBwdParams {
   int32_t dtype;
   void* stream;
   void* ds_tiles;                /* workspace of plan.ds_elems 16-bit values (deterministic path), else unused */
-  int64_t ds_limit_bytes;        /* largest dS workspace the caller accepts; 0 = 8 GiB, < 0 = none
+  int64_t ds_limit_bytes;        /* largest dS workspace the caller accepts; 0 = 4 GiB, < 0 = none
                                     (below the whole need: the backward runs in slices of units) */
   const void* mask_ws;           /* prepared mask, as for fa_fwd; required with a mask */
   const void* o_lo;              /* optional: the o_lo fa_fwd wrote; Delta = sum_d dO (O + o_lo) */

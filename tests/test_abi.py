@@ -189,7 +189,8 @@ BWD_ERRORS = [
     (dict(ds_tiles=None), 8, "needs ds_tiles"),
     (dict(ds_tiles=FAKE, ds_tiles_elems=1024), 8, "the plan needs"),
     # a workspace sized by a plan made without the mask: half the tile pairs
-    (dict(mask=FAKE, mask_ws=FAKE, ds_tiles=FAKE, ds_tiles_elems=32 * 256 * 256 * 1024), 8, "pair of tiles"),
+    (dict(mask=FAKE, mask_ws=FAKE, ds_tiles=FAKE, ds_tiles_elems=32 * 256 * 256 * 1024, ds_limit_bytes=8 << 30), 8,
+     "pair of tiles"),
 ]
 
 
@@ -223,7 +224,8 @@ def test_plan_headline_needs_no_split(lib):
 def test_plan_ds_tiles(lib):
     # causal 8192 x 8192: 256 query steps x 256 key steps, lower triangle with
     # the diagonal = 256 * 257 / 2 tiles of 32 x 32 per head
-    # both modes hand dS over when it fits; the atomic one splits the key
+    # both modes hand dS over when it fits (the default limit, 4 GiB, holds the
+    # headline's 4 GiB exactly); the atomic one splits the key
     # range (fp32 atomics) only below one 256-row block per CU: 2 x 8 heads x
     # 8 blocks = 128 -> 8 ranges (1024 workgroups)
     plan = _plan(lib)
@@ -260,8 +262,10 @@ def test_plan_ds_tiles(lib):
     # with a mask or a score every stored block is a pair of tiles (dS and
     # its rounding residual): twice the elements, and slices of half the units
     for side in (dict(mask=FAKE), dict(score=FAKE), dict(mask=FAKE, score=FAKE)):
-        assert _plan(lib, **side).ds_elems == 2 * 32 * 256 * 256 * 1024
+        assert _plan(lib, ds_limit_bytes=8 << 30, **side).ds_elems == 2 * 32 * 256 * 256 * 1024
         assert _plan(lib, atomic_dq=0, ds_limit_bytes=1 << 30, **side).ds_elems == 2 * unit
+        # the default 4 GiB holds half of them: two slices of four units
+        assert _plan(lib, **side).ds_elems == 4 * 2 * unit
 
 
 def test_det_path_needs_ds_tiles(lib):

@@ -1,7 +1,7 @@
 """The backward over slices of (batch, kv-head) units at a long sequence.
 
 At T = 16384 with the headline's heads (B1 Hq32 Hk8 D128) the dS tiles of all
-units (17 GB, 8.6 GB causal) exceed the default 8 GiB workspace, so the
+units (17 GB, 8.6 GB causal) exceed the default 4 GiB workspace, so the
 backward runs the dK/dV and dQ kernels once per slice of units
 (csrc/fa_api.cpp ``ds_slice_units``).  The same call with a limit that holds
 every unit runs them once.  Checks:
@@ -16,6 +16,11 @@ every unit runs them once.  Checks:
   alone, at an equal split, is bitwise exact);
 * atomic mode, non-causal: sliced and single-launch dQ agree within fp32
   summation order (dK/dV bitwise).
+
+The route, the slices and the head-group split depend on the problem and the
+limit only (the default limit is a constant): the deterministic backward is
+bitwise repeatable whatever the allocator holds, and two limits that give the
+same head-group split give the same bits.
 
 The parity of the slicing itself against the oracle runs at small shapes in
 tests/test_gpu_parity.py (modes ``det_sliced``, ``atomic_sliced``).
@@ -65,3 +70,32 @@ def test_sliced_backward_matches_single_launch(cuda, causal, atomic):
         del a, b
     del sliced, single
     torch.cuda.empty_cache()
+
+
+def test_default_limit_is_stable_and_equal_split_limits_agree(cuda):
+    """T 4096 at the headline's heads, deterministic: two calls under the
+    default limit with 24 GiB allocated in between (a different allocator
+    state) are bitwise equal; a 512 MiB limit (two slices of four units) and a
+    1 GiB one (one launch) both split each head group in two and give the
+    same bits; causal likewise under the default limit."""
+    import tilelang_fa2_4d_mask.fa2 as fa2mod
+
+    assert fa2mod.ds_limit_bytes() == fa2mod.DS_LIMIT_DEFAULT
+    T = 4096
+    g = torch.Generator().manual_seed(12)
+    q, k, v, do = (torch.randn(1, T, h, 128, generator=g).to(torch.bfloat16).to(cuda).transpose(1, 2)
+                   for h in (32, 8, 8, 32))
+    for causal in (False, True):
+        print(f"case T={T} causal={causal}: default limit twice around a 24 GiB allocation", flush=True)
+        a = _grads(q, k, v, do, causal=causal, atomic=False, limit=0)
+        hog = torch.empty(24 << 30, dtype=torch.uint8, device=cuda)
+        b = _grads(q, k, v, do, causal=causal, atomic=False, limit=0)
+        del hog
+        torch.cuda.empty_cache()
+        for name, x, y in zip(("dq", "dk", "dv"), a, b):
+            assert torch.equal(x, y), (causal, name)
+    print(f"case T={T}: 512 MiB (sliced) vs 1 GiB (one launch), equal head-group split", flush=True)
+    a = _grads(q, k, v, do, causal=False, atomic=False, limit=512 << 20)
+    b = _grads(q, k, v, do, causal=False, atomic=False, limit=1 << 30)
+    for name, x, y in zip(("dq", "dk", "dv"), a, b):
+        assert torch.equal(x, y), name

@@ -79,3 +79,20 @@ def test_backward_without_an_output_gradient():
     ops._setup_context(ctx, (q, q, q, None, None, 0.125, False, True, True), (q, q, q, q))
     assert ctx.materialize is False
     assert ops._backward(ctx, None, None, None, None) == (None,) * 9
+
+
+def test_default_ds_limit_is_a_constant():
+    """The backward's dS workspace limit does not depend on the device's
+    memory state (the route, slices and head-group split, hence the bits of
+    the deterministic backward, depend on the problem alone); DS_LIMIT_BYTES
+    overrides it."""
+    _, fa2, _ = _mods()
+    assert fa2.DS_LIMIT_BYTES == 0 and fa2.ds_limit_bytes() == fa2.DS_LIMIT_DEFAULT == 4 << 30
+    old = fa2.DS_LIMIT_BYTES
+    try:
+        fa2.DS_LIMIT_BYTES = 1 << 30
+        assert fa2.ds_limit_bytes() == 1 << 30
+        fa2.DS_LIMIT_BYTES = -1
+        assert fa2.ds_limit_bytes() == -1
+    finally:
+        fa2.DS_LIMIT_BYTES = old
