@@ -273,6 +273,17 @@ def cpu_baseline(seconds: float) -> dict:
         if el >= seconds:
             break
     tflops = flops * runs / el * 1e-12
+    # the forward alone (BASELINE.md's CPU plan times the headline forward
+    # too): eager_ref in chunks of 128 query rows, same sample
+    fruns, t1 = 0, time.perf_counter()
+    with torch.no_grad():
+        while True:
+            E.eager_ref(q, k, v, None, None, scale=D ** -0.5, is_causal=False, ref_block=128)
+            fruns += 1
+            fel = time.perf_counter() - t1
+            if fel >= seconds / 3:
+                break
+    fwd_tflops = 4.0 * B * hq * T * T * D * fruns / fel * 1e-12
     try:
         cores = len(os.sched_getaffinity(0))
     except AttributeError:
@@ -284,6 +295,8 @@ def cpu_baseline(seconds: float) -> dict:
         "kind": "port",
         "sample": (f"oracle eager fp32 fwd+bwd (ref_block=128) at B1 T8192 Hq4 Hk1 D128 non-causal "
                    f"(1/8 of the headline heads), {runs} run(s) in {el:.1f} s; host affinity {cores} cores"),
+        "fwd": {"value": round(fwd_tflops, 4), "unit": "TFLOPS",
+                "sample": f"oracle eager fp32 forward, same sample, {fruns} run(s) in {fel:.1f} s"},
         "config_C": cpu_config_c(min(5.0, seconds / 3)),
     }
 

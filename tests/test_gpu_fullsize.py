@@ -52,6 +52,7 @@ OUTS = ("out", "dq", "dk", "dv")
 # on the 16-bit rounding floor (see the module docstring)
 STRICT = {
     "H": OUTS, "M": OUTS, "H_causal": ("out", "dq"), "P": OUTS, "S": OUTS,
+    "H_fp16": OUTS, "H_causal_fp16": OUTS, "P_fp16": OUTS, "S_fp16": OUTS, "M_fp16": OUTS,
     "R_no_causal": OUTS, "R_causal": ("out", "dq"), "R_random_mask": OUTS, "long_keys_mask": OUTS,
 }
 
@@ -133,12 +134,22 @@ def check(ours, ref, rnd, label, strict):
 
 
 CASES = [("H", True), ("H", False), ("H_causal", True), ("H_causal", False),
-         ("P", True), ("P", False), ("S", True), ("S", False), ("M", True), ("M", False)]
+         ("P", True), ("P", False), ("S", True), ("S", False), ("M", True), ("M", False),
+         # the BASELINE configs in fp16 (the reference's harnesses take --dtype,
+         # benchmark/precision_check.py:352-375), deterministic mode
+         ("H_fp16", False), ("H_causal_fp16", False), ("P_fp16", False), ("S_fp16", False), ("M_fp16", False)]
+
+
+def _config(name):
+    if name.endswith("_fp16"):
+        base = I.CONFIGS[name[: -len("_fp16")]]
+        return base.scaled(name=name, dtype=torch.float16)
+    return I.CONFIGS[name]
 
 
 @pytest.mark.parametrize("name,atomic", CASES, ids=[f"{n}-{'atomic' if a else 'det'}" for n, a in CASES])
 def test_fullsize_vs_oracle(cuda, name, atomic):
-    cfg = I.CONFIGS[name]
+    cfg = _config(name)
     print(f"case {name} atomic={atomic} B{cfg.B} Tq{cfg.Tq} Tk{cfg.Tk} Hq{cfg.Hq} Hk{cfg.Hk} D{cfg.D} "
           f"{cfg.layout} causal={cfg.is_causal} mask={cfg.mask} score={cfg.score}", flush=True)
     case = I.make_case(cfg, seed=0, device=cuda)
