@@ -105,6 +105,12 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
     kf[ds] = as_vec8<T>(gload16(kp + (int64_t)kc * a.kst + ds * 16 + hf * 8));
     vf[ds] = as_vec8<T>(gload16(vp + (int64_t)kc * a.vst + ds * 16 + hf * 8));
   }
+  // The fragments stay in AGPRs for the whole loop (MFMA reads its A and B
+  // operands from AGPRs as well): 64 VGPRs freed, which the masked and score
+  // instances otherwise spill into AGPRs with a copy back per use (their
+  // P / dS residual parts fill the VGPRs).
+#pragma unroll
+  for (int ds = 0; ds < DS; ++ds) asm volatile("" : "+a"(kf[ds]), "+a"(vf[ds]));
 
   // ---- iteration space: (head of the group split, 32-row step) ---------------
   // Without a mask: every step from qstart on, for each head.  With a mask: per
