@@ -48,14 +48,28 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
   using V8 = typename Vec8<T>::type;
   constexpr int DS = D / 16, NB = D / 32, CH = D / 8, ROWB = 2 * D;
   constexpr int QTILE = kStep * ROWB;            // bytes of one Q (or dO) step tile
-  constexpr int DOFF = kNBuf * QTILE;            // dO tiles follow the Q tiles
-  constexpr int LOFF = 2 * kNBuf * QTILE;        // [buf][LSE | -Delta][32] fp32
+  // Six buffers in the plain head-dim-128 instance (the registers for a second
+  // set of LDS base addresses are there since the K/V fragments live in
+  // AGPRs): tile j+3 is written in iteration j and first read in iteration
+  // j+2, and each buffer's previous tile was last read in iteration j-2, so a
+  // workgroup barrier after every second iteration suffices.  Otherwise four
+  // buffers, tile j+2 written in iteration j, a barrier after every iteration.
+  constexpr bool SIX = !MASK && !SCORE && D == 128;
+  constexpr int NBUF = SIX ? 6 : kNBuf;
+  constexpr int AHD = SIX ? 3 : 2;               // tiles written ahead of the step computed
+  // Buffer b: Q tile at b QST, dO tile at b QST + DOFF.  Six buffers
+  // interleave Q and dO; offsets of 64 KB and more go through a second set of
+  // base registers (the DS immediate offset has 16 bits).
+  constexpr int QST = SIX ? 2 * QTILE : QTILE;
+  constexpr int DOFF = SIX ? QTILE : kNBuf * QTILE;
+  constexpr int LOFF = 2 * NBUF * QTILE;         // [buf][LSE | -Delta][32] fp32
   constexpr int LBUF = 2 * kStep * 4;
   constexpr int UQ = kStep * CH / (kKvWaves * 64);  // chunks per thread per tile
   constexpr int OS = D + 8;                      // epilogue staging stride (elements)
   static_assert(UQ >= 1, "tile split");
-  static_assert(DOFF + kNBuf * QTILE <= 65536, "buffer offsets fit the DS immediate");
-  static_assert(kKvWaves * 32 * OS * 2 <= 2 * kNBuf * QTILE, "epilogue staging fits");
+  static_assert(SIX || DOFF + kNBuf * QTILE <= 65536, "buffer offsets fit the DS immediate");
+  static_assert(!SIX || (NBUF - 1) * QST + DOFF + QTILE - 65536 <= 65536, "high buffers fit the second base");
+  static_assert(kKvWaves * 32 * OS * 2 <= 2 * NBUF * QTILE, "epilogue staging fits");
   static_assert(kKvKeys == kKv2Keys && kStep == 32, "prepared-mask lists are built for this shape");
   // With a mask or a score, P and dS enter dV += P^T dO and dK += dS^T Q in
   // several 16-bit parts each (the rounded value and its rounding residuals:
@@ -66,7 +80,7 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
   // followed by the tile of its residuals for the dQ kernel.
   constexpr bool PREC = MASK || SCORE;
   constexpr int NPART = PREC ? 2 : 1;   // 2 KB tiles per stored 32x32 block
-  __shared__ __attribute__((aligned(1024))) char smem[LOFF + kNBuf * LBUF];
+  __shared__ __attribute__((aligned(1024))) char smem[LOFF + NBUF * LBUF];
 
   // ---- which (batch, kv-head, split, key block) ------------------------------
   const int nblk = a.nbk * a.nkt * a.split;
@@ -212,17 +226,33 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
     }
   // LSE / -Delta of rows 8 gi + 4 hf .. +3
   const uint32_t al = opaque(lds0 + LOFF + hf * 16);
+  // second bases, 64 KB up (six buffers): a static offset off >= 64 KB is
+  // reached as base2 + (off - 64 KB), keeping it in the DS immediate
+  constexpr uint32_t kHi = 65536;
+  uint32_t ab2[SIX ? DS : 1], at2[2][SIX ? NB : 1];
+  if constexpr (SIX) {
+#pragma unroll
+    for (int ds = 0; ds < DS; ++ds) ab2[ds] = opaque(ab[ds] + kHi);
+#pragma unroll
+    for (int hi = 0; hi < 2; ++hi)
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) at2[hi][nb] = opaque(at[hi][nb] + kHi);
+  }
+  auto lds_at = [](uint32_t lo, uint32_t hi, uint32_t off) __attribute__((always_inline)) -> uint32_t {
+    return off >= kHi ? hi + (off - kHi) : lo + off;
+  };
 
   // ---- tile staging ------------------------------------------------------------
   // chunk u of thread t: tile row r = idx / CH, logical chunk c = idx % CH
   // (idx = t + 256 u): coalesced rows in, swizzled position out.
-  uint32_t gq[UQ], gd[UQ], sw[UQ];
+  uint32_t gq[UQ], gd[UQ], sw[UQ], sw2[SIX ? UQ : 1];
 #pragma unroll
   for (int u = 0; u < UQ; ++u) {
     const int idx = tid + u * kKvWaves * 64, r = idx / CH, c = idx % CH;
     gq[u] = (uint32_t)(r * a.qst * 2 + c * 16);
     gd[u] = (uint32_t)(r * a.dst * 2 + c * 16);
     sw[u] = opaque(lds0 + r * ROWB + ((c ^ swz_q<D>(r)) * 16));
+    if constexpr (SIX) sw2[u] = opaque(sw[u] + kHi);
   }
   // two staging sets (tiles j+3, j+4 in flight during iteration j): [set]
   u32x4 stq[2][UQ], std_[2][UQ];
@@ -344,8 +374,14 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
     constexpr int S = decltype(Sc)::value;
 #pragma unroll
     for (int u = 0; u < UQ; ++u) {
-      lds_wr16(sw[u] + buf * QTILE, stq[S][u]);
-      lds_wr16(sw[u] + DOFF + buf * QTILE, std_[S][u]);
+      const uint32_t qo = (uint32_t)(buf * QST), dof = (uint32_t)(buf * QST + DOFF);
+      if constexpr (SIX) {
+        lds_wr16(lds_at(sw[u], sw2[u], qo), stq[S][u]);
+        lds_wr16(lds_at(sw[u], sw2[u], dof), std_[S][u]);
+      } else {
+        lds_wr16(sw[u] + qo, stq[S][u]);
+        lds_wr16(sw[u] + dof, std_[S][u]);
+      }
     }
     if (wv == 0) {
       // rows past the tile's end: LSE = +inf (P = 0 whatever S is), -Delta = 0
@@ -457,26 +493,30 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
 #pragma unroll
     for (int c = 0; c < 2; ++c) { ppl[x][c] = V8{}; dsl[x][c] = V8{}; ppl2[x][c] = V8{}; }
 
-  // S/dP of step "it" (tile in buffer BUF) -> parity PAR; dV/dK of step it-2
-  // (buffer (BUF+2)%4, parity PAR) -- one interleaved MFMA stream, with the
-  // P/dS VALU work of step it-1 (parity PAR^1) threaded through it.  EDGE:
-  // some (row, key) of the step is masked (causal diagonal or a mask).
+  // S/dP of step j+1 (tile in buffer BUF+1) and dV/dK of step j-1 (buffer
+  // BUF-1) -- one interleaved MFMA stream, with the P/dS VALU work of step j
+  // (buffer BUF) threaded through it.  EDGE: some (row, key) of the step is
+  // masked (causal diagonal or a mask).
   auto iter = [&](auto BUFc, auto EDGEc, int j, uint32_t mreg, int pos_next) __attribute__((always_inline)) {
     // j: step whose P/dS is computed now; S/dP of j+1; dV/dK of j-1
     constexpr int BUF = decltype(BUFc)::value;          // buffer of step j
     constexpr bool EDGE = decltype(EDGEc)::value != 0;
-    constexpr int BN1 = (BUF + 1) % kNBuf, BM1 = (BUF + kNBuf - 1) % kNBuf;
+    constexpr int BN1 = (BUF + 1) % NBUF, BM1 = (BUF + NBUF - 1) % NBUF;
     constexpr int PJ = BUF & 1, PN = PJ ^ 1;            // parities of j and j +- 1
     const int dkq = key - (it_qs + 4 * hf);              // causal: keep iff dkq <= 8 gi + t
 
     // operand reads for the two MFMA streams, AHEAD ops ahead
     auto rd_sd = [&](int t) __attribute__((always_inline)) -> u32x4 {   // t: ds = t/2, Q (even) / dO (odd)
-      return lds_rd16(ab[t >> 1] + (uint32_t)((t & 1) * DOFF + BN1 * QTILE));
+      const uint32_t off = (uint32_t)((t & 1) * DOFF + BN1 * QST);
+      if constexpr (SIX) return lds_rd16(lds_at(ab[t >> 1], ab2[t >> 1], off));
+      else return lds_rd16(ab[t >> 1] + off);
     };
     auto rd_tr = [&](int t) __attribute__((always_inline)) -> V8 {       // t: c = t / (2 NB), nb, dO (even) / Q (odd)
       const int c = t / (2 * NB), nb = (t / 2) % NB, isq = t & 1;
-      const uint32_t off = (uint32_t)((isq ? 0 : DOFF) + BM1 * QTILE + 16 * c * ROWB);
-      return cat_tr<T>(lds_rdtr(at[0][nb] + off), lds_rdtr(at[1][nb] + off));
+      const uint32_t off = (uint32_t)((isq ? 0 : DOFF) + BM1 * QST + 16 * c * ROWB);
+      if constexpr (SIX)
+        return cat_tr<T>(lds_rdtr(lds_at(at[0][nb], at2[0][nb], off)), lds_rdtr(lds_at(at[1][nb], at2[1][nb], off)));
+      else return cat_tr<T>(lds_rdtr(at[0][nb] + off), lds_rdtr(at[1][nb] + off));
     };
     constexpr int NOP = 2 * DS;                          // == 4 * NB: ops per stream
     // -Delta of the rows of step j+1: initial accumulator of its dP chain
@@ -634,16 +674,28 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
   };
 
   // ---- prologue --------------------------------------------------------------------
-  // Buffer 3 is read as step -1 (with P = dS = 0): zero it.
+  // The last buffer is read as step -1 (with P = dS = 0): zero it.
 #pragma unroll
   for (int u = 0; u < UQ; ++u) {
-    lds_wr16(sw[u] + 3 * QTILE, u32x4{0, 0, 0, 0});
-    lds_wr16(sw[u] + DOFF + 3 * QTILE, u32x4{0, 0, 0, 0});
+    constexpr uint32_t zo = (NBUF - 1) * QST;
+    if constexpr (SIX) {
+      lds_wr16(lds_at(sw[u], sw2[u], zo), u32x4{0, 0, 0, 0});
+      lds_wr16(lds_at(sw[u], sw2[u], zo + DOFF), u32x4{0, 0, 0, 0});
+    } else {
+      lds_wr16(sw[u] + zo, u32x4{0, 0, 0, 0});
+      lds_wr16(sw[u] + zo + DOFF, u32x4{0, 0, 0, 0});
+    }
   }
   load_next(IC<0>{}, IC<0>{}); store_tile(0, IC<0>{});   // tile 0
   load_next(IC<1>{}, IC<1>{}); store_tile(1, IC<1>{});   // tile 1
-  load_next(IC<0>{}, IC<2>{});                           // tile 2 staged (set 0)
-  load_next(IC<1>{}, IC<3>{});                           // tile 3 staged (set 1)
+  if constexpr (SIX) {
+    load_next(IC<0>{}, IC<0>{}); store_tile(2, IC<0>{}); // tile 2
+    load_next(IC<1>{}, IC<0>{});                         // tile 3 staged (set 1)
+    load_next(IC<0>{}, IC<0>{});                         // tile 4 staged (set 0)
+  } else {
+    load_next(IC<0>{}, IC<2>{});                         // tile 2 staged (set 0)
+    load_next(IC<1>{}, IC<3>{});                         // tile 3 staged (set 1)
+  }
   load_ms(n > 0);
   lds_barrier();
   // S / dP of step 0 (parity 0); the dP chain starts from -Delta
@@ -661,34 +713,48 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
   }
 
   // ---- main loop: iteration j computes P/dS(j), S/dP(j+1), dV/dK(j-1) ---------------
-  // j runs over [0, n4) with n4 = n + 1 rounded up to a multiple of 4: the
+  // j runs over [0, nr) with nr = n + 1 rounded up to a multiple of NBUF: the
   // iterations past n - 1 work on zero tiles whose rows carry LSE = +inf, so
   // their P and dS are exactly 0 and they add nothing, while iteration n
-  // contributes dV/dK(n-1).  Four copies of the body with static buffers and
+  // contributes dV/dK(n-1).  NBUF copies of the body with static buffers and
   // a single loop exit keep the accumulators in fixed registers.
-  // Staging first: buffer (j+2)%4 is not read in iteration j, so tile j+2
-  // (loaded during iteration j-1) is written while the MFMA stream runs, and
-  // the loads of tile j+3 get a whole iteration of latency.
+  // Staging first: buffer (j+AHD)%NBUF is not read in iteration j, so tile
+  // j+AHD (loaded two iterations earlier) is written while the MFMA stream
+  // runs, and the loads of tile j+AHD+2 get two iterations of latency.
   auto step = [&](auto BUFc, int j) __attribute__((always_inline)) {
     constexpr int BUF = decltype(BUFc)::value;
-    store_tile((BUF + 2) % kNBuf, IC<BUF & 1>{});   // tile j+2 (staged two iterations ago)
+    constexpr int SET = (BUF + AHD) & 1;              // staging set of tiles j+AHD and j+AHD+2
+    store_tile((BUF + AHD) % NBUF, IC<SET>{});      // tile j+AHD
     // mask word of step j (loaded with tile j), before slot BUF is refilled
-    const uint32_t mcur = MASK && j < n ? mq[MASK ? BUF : 0] >> (4 * hf) : 0u;
+    const uint32_t mcur = MASK && j < n ? mq[MASK ? BUF % 4 : 0] >> (4 * hf) : 0u;
     const int pnext = pq[MASK ? (BUF + 1) % 4 : 0];   // position of step j+1 (loaded with tile j+1)
-    load_next(IC<BUF & 1>{}, IC<BUF>{});            // tile j+4 (its mask word into slot BUF)
+    load_next(IC<SET>{}, IC<BUF % 4>{});            // tile j+AHD+2 (with a mask: j+4, its word into slot BUF)
     // with a mask the keep test runs per entry on every step (a second copy of
     // the body for steps without dropped entries would not fit the register
     // budget); causal alone clears packed entries on the diagonal steps
     iter(BUFc, IC<MASK ? 1 : 0>{}, j, mcur, pnext);
-    lds_barrier();
+    if constexpr (!SIX || (BUF & 1) != 0) lds_barrier();
   };
-  int n4 = n > 0 ? (n + 4) & ~3 : 0;
-  asm volatile("" : "+s"(n4));   // hide the trip count (uniform: scalar register)
-  for (int j = 0; j < n4; j += 4) {
-    step(IC<0>{}, j);
-    step(IC<1>{}, j + 1);
-    step(IC<2>{}, j + 2);
-    step(IC<3>{}, j + 3);
+  if constexpr (SIX) {
+    int nr = n > 0 ? (n + 6) / 6 * 6 : 0;
+    asm volatile("" : "+s"(nr));   // hide the trip count (uniform: scalar register)
+    for (int j = 0; j < nr; j += 6) {
+      step(IC<0>{}, j);
+      step(IC<1>{}, j + 1);
+      step(IC<2>{}, j + 2);
+      step(IC<3>{}, j + 3);
+      step(IC<4>{}, j + 4);
+      step(IC<5>{}, j + 5);
+    }
+  } else {
+    int nr = n > 0 ? (n + 4) & ~3 : 0;
+    asm volatile("" : "+s"(nr));
+    for (int j = 0; j < nr; j += 4) {
+      step(IC<0>{}, j);
+      step(IC<1>{}, j + 1);
+      step(IC<2>{}, j + 2);
+      step(IC<3>{}, j + 3);
+    }
   }
 
   mfma_acc_drain();   // before the epilogue reads the AGPR accumulators
