@@ -22,7 +22,8 @@
 // VALU pipes busy at the same time.
 //
 // Q/dO step tiles (32 rows) live in 4 LDS buffers (tiles j-1 and j+1 are read
-// in iteration j while j+2 is written), rows unpadded with one XOR swizzle of
+// in iteration j while j+2 is written; 6 buffers and tile j+3 in the plain
+// head-dim-128 instance), rows unpadded with one XOR swizzle of
 // their 16-byte chunks that keeps both the ds_read_b128 pattern (16 rows) and
 // the transpose-read pattern (4 rows x 4 chunks) conflict-free.  Tiles are
 // staged through registers: loaded with buffer loads (loop-invariant lane
@@ -717,7 +718,8 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
   // iterations past n - 1 work on zero tiles whose rows carry LSE = +inf, so
   // their P and dS are exactly 0 and they add nothing, while iteration n
   // contributes dV/dK(n-1).  NBUF copies of the body with static buffers and
-  // a single loop exit keep the accumulators in fixed registers.
+  // a single loop exit keep the accumulators in fixed registers (an exit
+  // after each copy made the register allocator spill).
   // Staging first: buffer (j+AHD)%NBUF is not read in iteration j, so tile
   // j+AHD (loaded two iterations earlier) is written while the MFMA stream
   // runs, and the loads of tile j+AHD+2 get two iterations of latency.
