@@ -330,6 +330,11 @@ static int check_bwd(const FaBwdParams* p, int split) {
   const int64_t qspan = (int64_t)(p->seqlen_q + 32) * 2 * (p->q_stride_t > p->do_stride_t ? p->q_stride_t : p->do_stride_t);
   if (qspan >= (1LL << 32))
     return fail(FA_ERR_STRIDE, "seqlen_q * q/dout time stride too large (%lld bytes, the limit is 2^32)", (long long)qspan);
+  // The dK/dV kernel reads a step's 32 score rows through one buffer with
+  // 32-bit offsets, as the forward does a wave's.
+  if (p->score && (31 * p->score_stride_q + (int64_t)p->seqlen_k + 64) * 4 >= (1LL << 32))
+    return fail(FA_ERR_STRIDE, "score query stride %lld: 32 score rows must span less than 4 GiB",
+                (long long)p->score_stride_q);
   if (!p->lse) return fail(FA_ERR_NULL, "lse is NULL");
   if (!p->delta) return fail(FA_ERR_NULL, "delta is NULL");
   if (!p->dead_flags) return fail(FA_ERR_NULL, "dead_flags is NULL");

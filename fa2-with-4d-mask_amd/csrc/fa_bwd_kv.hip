@@ -401,26 +401,23 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
   }
 
   // ---- score of a step (lane's 16 query rows at its key) -----------------------
+  // One range-checked buffer per step from its first row (the host keeps 32
+  // rows below 4 GiB): rows past Tq read 0 (their P is 0: LSE = +inf); the
+  // lane's offset (row 4 hf, key kc) is loop-invariant and element (g, t),
+  // row 8 g + 4 hf + t, adds 8 g + t rows as a scalar offset.  Iteration j
+  // loads step j+1's elements one by one, each right after step j's has been
+  // used, so they get an iteration to arrive.
   float sreg[SCORE ? 16 : 1];
-  auto load_ms = [&](bool live) __attribute__((always_inline)) {
-    if constexpr (SCORE) {
-      // padding steps reread the last real step's rows (harmless).  Element
-      // (g, t) is row it_qs + 8 g + 4 hf + t: a lane pointer per step plus a
-      // uniform row offset per element; on a step that reaches past Tq the
-      // rows are clamped to Tq - 1 (their P is 0: LSE = +inf)
-      const int h = live ? it_h : kvh * a.G + g0 + gsz - 1;
-      const float* pl = a.score + b * a.ssb + h * a.ssh + (int64_t)(it_qs + 4 * hf) * a.ssq + kc;
-      if (it_qs + 32 <= Tq) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) sreg[i] = pl[(int64_t)(8 * (i >> 2) + (i & 3)) * a.ssq];
-      } else {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int q = min(it_qs + 8 * (i >> 2) + 4 * hf + (i & 3), Tq - 1);
-          sreg[i] = a.score[b * a.ssb + h * a.ssh + (int64_t)q * a.ssq + kc];
-        }
-      }
-    }
+  const uint32_t s_lane = SCORE ? (uint32_t)(((int64_t)4 * hf * a.ssq + kc) * 4) : 0u;
+  const uint32_t s_row = (uint32_t)a.ssq * 4u;
+  auto score_rs = [&](int h, int qs, bool live) __attribute__((always_inline)) {
+    const uint32_t nrec = live ? (uint32_t)(((int64_t)min(Tq - qs, 32) - 1) * a.ssq * 4 + (int64_t)Tk * 4) : 0u;
+    return __builtin_amdgcn_make_buffer_rsrc((void*)(a.score + b * a.ssb + (int64_t)h * a.ssh + (int64_t)qs * a.ssq),
+                                             (short)0, (int)nrec, 0x00020000);
+  };
+  auto load_s = [&](const __amdgpu_buffer_rsrc_t& rs, int i) __attribute__((always_inline)) {
+    sreg[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                            rs, s_lane, (uint32_t)(8 * (i >> 2) + (i & 3)) * s_row, 0));
   };
 
   // ---- dS tiles for the dQ kernel --------------------------------------------------
@@ -506,6 +503,20 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
     constexpr int PJ = BUF & 1, PN = PJ ^ 1;            // parities of j and j +- 1
     const int dkq = key - (it_qs + 4 * hf);              // causal: keep iff dkq <= 8 gi + t
 
+    // score buffer of step j+1 (its position: queued with its tile with a
+    // mask, else the next row step / head)
+    int hn = 0, qn = 0;
+    if constexpr (SCORE) {
+      if constexpr (MASK) {
+        hn = h_first + (pos_next >> psh);
+        qn = kStep * (pos_next & ((1 << psh) - 1));
+      } else {
+        hn = it_h;
+        qn = DESC ? it_qs - kStep : it_qs + kStep;
+        if (DESC ? qn < qstart : qn >= Tq) { ++hn; qn = qfirst; }
+      }
+    }
+    const auto srs_next = score_rs(min(hn, h_end - 1), qn, SCORE && j + 1 < n);
     // operand reads for the two MFMA streams, AHEAD ops ahead
     auto rd_sd = [&](int t) __attribute__((always_inline)) -> u32x4 {   // t: ds = t/2, Q (even) / dO (odd)
       const uint32_t off = (uint32_t)((t & 1) * DOFF + BN1 * QST);
@@ -633,6 +644,7 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
         const int i = t * EPS + e;
         if ((i & 3) == 1 && i + 3 < 16) read_l((i >> 2) + 1);   // LSE of the next row group
         pe[t & 1][e] = elem_exp(i);
+        if constexpr (SCORE) load_s(srs_next, i);   // step j+1's element i
       }
       if (t > 0) {
 #pragma unroll
@@ -669,9 +681,8 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
         }
       }
     }
-    // next step's dS descriptor and position, then its mask / score
+    // next step's dS descriptor and position
     next_step(j, mreg, pos_next);
-    load_ms(j + 1 < n);
   };
 
   // ---- prologue --------------------------------------------------------------------
@@ -697,7 +708,11 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
     load_next(IC<0>{}, IC<2>{});                         // tile 2 staged (set 0)
     load_next(IC<1>{}, IC<3>{});                         // tile 3 staged (set 1)
   }
-  load_ms(n > 0);
+  if constexpr (SCORE) {
+    const auto rs0 = score_rs(it_h, it_qs, n > 0);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) load_s(rs0, i);
+  }
   lds_barrier();
   // S / dP of step 0 (parity 0); the dP chain starts from -Delta
   f32x16 nd0;

@@ -163,6 +163,7 @@ NOALLOC_ERRORS = [
     (dict(dq=None), 1, "dq is NULL"),
     (dict(head_dim=32), 3, "head_dim 32"),
     (dict(mask=FAKE), 8, "prepared workspace"),
+    (dict(score=FAKE, score_stride_q=1 << 26), 5, "32 score rows"),
 ]
 
 
@@ -184,6 +185,7 @@ BWD_ERRORS = [
     (dict(delta=None), 1, "delta is NULL"),
     (dict(dead_flags=None), 1, "dead_flags is NULL"),
     (dict(dk_stride_h=100), 5, "multiples of 8"),
+    (dict(score=FAKE, score_stride_q=1 << 26), 5, "32 score rows"),
     (dict(head_dim=32), 3, "head_dim 32"),
     (dict(mask=FAKE, ds_tiles=FAKE, ds_tiles_elems=1 << 40), 8, "prepared workspace"),
     (dict(ds_tiles=None), 8, "needs ds_tiles"),
