@@ -128,9 +128,12 @@ int ds_slices(const FaBwdParams* p) {
 // dK/dV kernel with fp32-atomic dQ (atomic), or a dQ kernel that recomputes
 // S, P and dP (deterministic).
 enum Route { kDsAtomic, kDsDet, kFusedAtomic, kRecomputeDet };
+// Without the dS workspace, a mask or a score takes the recompute route in
+// both modes: its kernels carry P and dS in several 16-bit parts there (the
+// fused atomic kernel rounds them once).
 Route route_of(const FaBwdParams* p) {
   const bool ds = ds_elems(p) > 0;
-  if (p->atomic_dq) return ds ? kDsAtomic : kFusedAtomic;
+  if (p->atomic_dq) return ds ? kDsAtomic : (p->mask || p->score ? kRecomputeDet : kFusedAtomic);
   return ds ? kDsDet : kRecomputeDet;
 }
 

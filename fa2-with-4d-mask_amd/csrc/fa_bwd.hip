@@ -467,6 +467,7 @@ __global__ __launch_bounds__(256, 1) void dq_kernel(const BwdArgs a) {
   constexpr int U = BN * CH / 256;
   constexpr int OS = D + 8;
   static_assert(4 * 32 * OS <= 2 * (KT + VT), "dQ staging fits");
+  constexpr bool PREC = MASK || SCORE;
   __shared__ __attribute__((aligned(16))) T smem[2 * (KT + VT)];
 
   const int nblk = a.B * a.Hq * a.nqt;
@@ -596,18 +597,35 @@ __global__ __launch_bounds__(256, 1) void dq_kernel(const BwdArgs a) {
             sacc[kb][i] = p * (pacc[kb][i] - delta_q) * scale;
           }
         }
-      // dQ^T += K^T dS^T: A = K^T via transpose reads, B = dS^T from registers
+      // dQ^T += K^T dS^T: A = K^T via transpose reads, B = dS^T from registers.
+      // With a mask or a score dS enters in two 16-bit parts (the rounded value
+      // and its rounding residual), as in the dK/dV and dQ-from-dS kernels.
 #pragma unroll
       for (int kk2 = 0; kk2 < 4; ++kk2) {
         const int kb = kk2 >> 1, c = kk2 & 1;
-        const V8 dsb = pack8<T>(sacc[kb][8 * c + 0], sacc[kb][8 * c + 1], sacc[kb][8 * c + 2], sacc[kb][8 * c + 3],
-                                sacc[kb][8 * c + 4], sacc[kb][8 * c + 5], sacc[kb][8 * c + 6], sacc[kb][8 * c + 7]);
+        V8 dsb, dsl;
+        if constexpr (PREC) {
+          u32x4 wh, wl;
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            uint32_t h2, l2;
+            split2<T>(sacc[kb][8 * c + 2 * k], sacc[kb][8 * c + 2 * k + 1], &h2, &l2);
+            wh[k] = h2;
+            wl[k] = l2;
+          }
+          dsb = as_vec8<T>(wh);
+          dsl = as_vec8<T>(wl);
+        } else {
+          dsb = pack8<T>(sacc[kb][8 * c + 0], sacc[kb][8 * c + 1], sacc[kb][8 * c + 2], sacc[kb][8 * c + 3],
+                         sacc[kb][8 * c + 4], sacc[kb][8 * c + 5], sacc[kb][8 * c + 6], sacc[kb][8 * c + 7]);
+        }
         const int row = kb * 32 + 16 * c + tr_row;
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
           const int col = nb * 32 + tr_col;
           const V8 ak = cat_tr<T>(lds_read_tr(ks + row * KS + col), lds_read_tr(ks + (row + 8) * KS + col));
           qacc[nb] = mfma32(ak, dsb, qacc[nb]);
+          if constexpr (PREC) qacc[nb] = mfma32(ak, dsl, qacc[nb]);
         }
       }
     }

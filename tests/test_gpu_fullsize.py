@@ -158,7 +158,7 @@ def test_fullsize_vs_oracle(cuda, name, atomic):
           STRICT[name])
 
 
-NO_WS_CASES = [("H", True), ("H", False), ("H_causal", True), ("H_causal", False)]
+NO_WS_CASES = [("H", True), ("H", False), ("H_causal", True), ("H_causal", False), ("P", True), ("S", False)]
 
 
 @pytest.mark.parametrize("name,atomic", NO_WS_CASES,
@@ -166,13 +166,15 @@ NO_WS_CASES = [("H", True), ("H", False), ("H_causal", True), ("H_causal", False
 def test_fullsize_without_ds_workspace(cuda, name, atomic):
     """The backward routes that keep memory O(T) (no dS workspace allowed):
     atomic mode runs the fused dK/dV kernel that adds dQ with fp32 atomics,
-    the deterministic mode a dQ kernel that recomputes S, P and dP.  The
+    the deterministic mode a dQ kernel that recomputes S, P and dP; with a
+    mask or a score both modes take the recompute route, whose kernels carry
+    P and dS in several 16-bit parts (P and S here: the strict cells).  The
     library falls back to them when the dS tiles do not fit the limit; here
-    they are forced at the headline shape and held to the same cells."""
+    they are forced and held to the same cells as the default route."""
     import tilelang_fa2_4d_mask.fa2 as fa2mod
 
     cfg = I.CONFIGS[name]
-    route = "fused atomic" if atomic else "recompute"
+    route = "fused atomic" if atomic and cfg.mask is None and cfg.score is None else "recompute"
     print(f"case {name} no dS workspace ({route}) B{cfg.B} T{cfg.Tq} Hq{cfg.Hq} Hk{cfg.Hk} D{cfg.D}", flush=True)
     case = I.make_case(cfg, seed=4, device=cuda)
     fa2mod.DS_LIMIT_BYTES = -1
