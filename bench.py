@@ -41,8 +41,11 @@ M: MQA long KV, bshd) are timed after the headline and reported under
 ``configs`` with dense-convention TFLOPS and GB/s against their algorithmic
 bytes (each tensor once; mask at its passed head count), the HBM fraction of
 8 TB/s, and for the masked ones the live TFLOPS (dense convention times the
-kept fraction of pairs) and its fraction of peak instead of a dense fraction.
-``cpu_baseline`` also times BASELINE configs[0] (C) on the host.
+kept fraction of pairs) and its fraction of peak instead of a dense fraction;
+each also replays its fwd and deterministic fwd+bwd from captured graphs
+(``fwd_graph``, ``fwd_bwd_graph``: eager minus graph is the host time the
+GPU waits for).  ``cpu_baseline`` also times BASELINE configs[0] (C) on the
+host.
 
 Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline] [--no-side-configs]
 """
@@ -484,6 +487,20 @@ def main() -> int:
                 log(f"{name} {mode:15s} {ms:8.3f} ms  {e['tflops_dense_conv']:8.1f} TFLOPS (dense conv.)"
                     f"  {e['gbps']:8.1f} GB/s of {nbytes / 1e9:.3f} GB algorithmic  peak extra {e['peak_extra_mib']} MiB"
                     f"  kernels {kern}")
+            # the same steps replayed from captured graphs: what the host adds
+            # per call (eager minus graph)
+            for mode, fn in (("fwd_graph", sfwd), ("fwd_bwd_graph", sfb(False))):
+                g = graph_of(torch, fn)
+                tm, _ = time_steps(torch, g.replay, max(3, args.steps // 2), max(1, args.warmup // 2),
+                                   record_kernel_events, flush)
+                ms = tm["ms"]
+                eager = entry["fwd" if mode == "fwd_graph" else "fwd_bwd"]["ms"]
+                entry[mode] = {"ms": round(ms, 4), "ms_p20": round(tm["ms_p20"], 4), "ms_p80": round(tm["ms_p80"], 4),
+                               "eager_minus_graph_ms": round(eager - ms, 4)}
+                log(f"{name} {mode:15s} {ms:8.3f} ms  eager - graph {eager - ms:+.3f} ms")
+                del g
+                xq.grad = xk.grad = xv.grad = None
+                torch.cuda.empty_cache()
             if x["mask"] is not None:
                 entry["mask_keep_fraction"] = round(keep, 4)
             entry["config"] = {"B": bq, "Tq": tq, "Tk": tk, "Hq": hq, "Hk": hk, "D": d, "layout": x["layout"],
