@@ -148,8 +148,8 @@ typedef struct FaBwdPlan {
                                     (batch, kv-head) units: all units when they fit ds_limit_bytes, else
                                     as many as fit, in nearly equal slices that fa_bwd runs one after the
                                     other); 0 when not even one unit fits: dQ is then recomputed
-                                    (atomic_dq = 0) or added per key block by the fused dK/dV kernel
-                                    (atomic_dq = 1) */
+                                    (atomic_dq = 0, or with a mask or a score) or added per key block by
+                                    the fused dK/dV kernel (atomic_dq = 1 without mask and score) */
   int32_t dkv_accum_zeroed;      /* 1: dk_accum/dv_accum must be zeroed by the caller (fused atomic kernel) */
   int32_t dq_split;              /* atomic_dq = 1 with dS tiles: key ranges whose dQ partials are added
                                     (2-8) when the 256-row query blocks are fewer than the CUs; 1: each
@@ -192,18 +192,18 @@ int fa_bwd_preprocess(const FaBwdParams* p);
  * storing dS into ds_tiles for fa_bwd_finalize (when ds_tiles holds a slice of the
  * (batch, kv-head) units, fa_bwd runs the dK/dV and the dQ kernel per slice and
  * fa_bwd_finalize only converts).  With plan.ds_elems = 0 and
- * atomic_dq = 1: one fused kernel that also adds dQ into dq_accum with fp32
- * atomics (dK/dV added into zeroed dk_accum/dv_accum when kv_split > 1); with
- * atomic_dq = 0: the dK/dV kernel only.  Must follow fa_bwd_preprocess on the
- * same stream. */
+ * atomic_dq = 1 without mask and score: one fused kernel that also adds dQ
+ * into dq_accum with fp32 atomics (dK/dV added into zeroed dk_accum/dv_accum
+ * when kv_split > 1); otherwise (atomic_dq = 0, or a mask or a score): the
+ * dK/dV kernel only.  Must follow fa_bwd_preprocess on the same stream. */
 int fa_bwd(const FaBwdParams* p);
 
 /* Backward finalisation.  dQ: from ds_tiles, dQ = scale dS K, written in dtype
  * (atomic_dq = 0, or plan.dq_split = 1) or added as fp32 partials over
  * plan.dq_split key ranges into dq_accum with atomics and converted (atomic_dq = 1,
  * plan.dq_split > 1); without ds_tiles,
- * recomputed from S, P and dP (atomic_dq = 0) or converted from the dq_accum the
- * fused kernel filled (atomic_dq = 1).  dk, dv from dk_accum/dv_accum when
+ * recomputed from S, P and dP (atomic_dq = 0, or a mask or a score) or converted
+ * from the dq_accum the fused kernel filled (atomic_dq = 1 without them).  dk, dv from dk_accum/dv_accum when
  * kv_split > 1.  Replaces the casts of python/fa2.py:535-536, the group sum of
  * python/fa2.py:548-549 and autograd's cast of the fp32 dQ the reference returns
  * (python/fa2.py:527, 556); the dS-based dQ replaces the per-64-key dQ atomics of
