@@ -23,7 +23,8 @@ CSRC = HERE / "csrc"
 BUILD = HERE / "_build"
 LIBDIR = HERE / "tilelang_fa2_4d_mask" / "_lib"
 LIB = LIBDIR / "libfa2_4d_mask.so"
-SOURCES = ["fa_fwd.hip", "fa_bwd.hip", "fa_bwd_kv.hip", "fa_bwd_dq.hip", "fa_mask.hip", "fa_noalloc.hip", "fa_api.cpp"]
+SOURCES = ["fa_fwd.hip", "fa_bwd.hip", "fa_bwd_kv.hip", "fa_bwd_dq.hip", "fa_wide.hip", "fa_mask.hip", "fa_noalloc.hip",
+           "fa_api.cpp"]
 # Per-file extra flags.  fa_bwd_kv.hip keeps its dK/dV accumulators in AGPRs
 # through inline asm and wants every other MFMA result in VGPRs (read by VALU).
 EXTRA_FLAGS = {"fa_bwd_kv.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}

@@ -54,7 +54,7 @@ int check_dims(int32_t B, int32_t Tq, int32_t Tk, int32_t Hq, int32_t Hk, int32_
     return fail(FA_ERR_SHAPE, "sizes must be >= 1 (B=%d Tq=%d Tk=%d Hq=%d Hk=%d)", B, Tq, Tk, Hq, Hk);
   if (Hq % Hk != 0)
     return fail(FA_ERR_SHAPE, "query heads (%d) must be divisible by key/value heads (%d)", Hq, Hk);
-  if (D != 64 && D != 128) return fail(FA_ERR_HEAD_DIM, "head_dim %d not supported (64, 128)", D);
+  if (D != 64 && D != 128 && D != 256) return fail(FA_ERR_HEAD_DIM, "head_dim %d not supported (64, 128, 256)", D);
   if (dtype != FA_DTYPE_BF16 && dtype != FA_DTYPE_FP16) return fail(FA_ERR_DTYPE, "unsupported dtype code %d", dtype);
   if (!std::isfinite(scale)) return fail(FA_ERR_SCALE, "scale must be finite");
   // 32-bit indices inside the kernels: rows of every head must fit.
@@ -106,6 +106,7 @@ int64_t ds_unit_elems(const FaBwdParams* p) {
   return (int64_t)(p->heads_q / p->heads_k) * plane * 1024 * ds_tile_parts(p);   // one unit: the group's planes
 }
 int64_t ds_slice_units(const FaBwdParams* p) {
+  if (p->head_dim > 128) return 0;   // head dim 256: dQ is always recomputed
   const int64_t limit = p->ds_limit_bytes == 0 ? kDsLimitDefault : p->ds_limit_bytes;
   if (limit < 0) return 0;
   const int64_t units = (int64_t)p->batch * p->heads_k, unit = ds_unit_elems(p);
@@ -131,7 +132,10 @@ enum Route { kDsAtomic, kDsDet, kFusedAtomic, kRecomputeDet };
 // Without the dS workspace, a mask or a score takes the recompute route in
 // both modes: its kernels carry P and dS in several 16-bit parts there (the
 // fused atomic kernel rounds them once).
+// Head dim 256 always takes the recompute route (its dK/dV kernels store no
+// dS tiles and add no atomics): both modes give the deterministic result.
 Route route_of(const FaBwdParams* p) {
+  if (p->head_dim > 128) return kRecomputeDet;
   const bool ds = ds_elems(p) > 0;
   if (p->atomic_dq) return ds ? kDsAtomic : (p->mask || p->score ? kRecomputeDet : kFusedAtomic);
   return ds ? kDsDet : kRecomputeDet;
@@ -161,6 +165,12 @@ int dq_split_of(const FaBwdParams* p) {
   return split;
 }
 
+// keys per workgroup of the dK/dV launch(es) of the route
+int kv_block_keys(const FaBwdParams* p) {
+  if (p->head_dim > 128) return fa::kv_wide_block_keys();
+  return route_of(p) == kFusedAtomic ? fa::dkdv_block_keys() : fa::dkdv2_block_keys();
+}
+
 // dQ accumulated with fp32 atomics into dq_accum (then converted)
 bool dq_atomics(const FaBwdParams* p) {
   const Route r = route_of(p);
@@ -179,7 +189,7 @@ int dq_rows(const FaBwdParams* p) {
 int choose_split(const FaBwdParams* p) {
   if (p->kv_split > 0) return p->kv_split;
   const int G = p->heads_q / p->heads_k;
-  const int kb = route_of(p) == kFusedAtomic ? fa::dkdv_block_keys() : fa::dkdv2_block_keys();
+  const int kb = kv_block_keys(p);
   const int nkt = (p->seqlen_k + kb - 1) / kb;
   const Route r = route_of(p);
   const int64_t units = r == kDsAtomic || r == kDsDet ? ds_slice_units(p) : (int64_t)p->batch * p->heads_k;
@@ -296,7 +306,8 @@ int fa_fwd(const FaFwdParams* p) {
   a.ssb = p->score_stride_b; a.ssh = p->score_stride_h; a.ssq = p->score_stride_q;
   a.B = p->batch; a.Tq = p->seqlen_q; a.Tk = p->seqlen_k; a.Hq = p->heads_q; a.Hk = p->heads_k;
   a.G = p->heads_q / p->heads_k;
-  a.nqt = (p->seqlen_q + fa::fwd_block_rows() - 1) / fa::fwd_block_rows();
+  const int fwd_rows = p->head_dim > 128 ? fa::fwd_wide_block_rows() : fa::fwd_block_rows();
+  a.nqt = (p->seqlen_q + fwd_rows - 1) / fwd_rows;
   float sl2b;
   fill_scales(p->scale, &a.scale_log2, &a.qsign, &a.zero_scale, &sl2b);
   if (p->mask) {
@@ -307,7 +318,9 @@ int fa_fwd(const FaFwdParams* p) {
     a.olo = p->o_lo;
     a.olsb = p->o_lo_stride_b; a.olst = p->o_lo_stride_t; a.olsh = p->o_lo_stride_h;
   }
-  return launch_status(fa::launch_fwd(a, p->head_dim, p->dtype, p->is_causal != 0, (hipStream_t)p->stream), "fa_fwd");
+  const hipStream_t s = (hipStream_t)p->stream;
+  if (p->head_dim > 128) return launch_status(fa::launch_fwd_wide(a, p->dtype, p->is_causal != 0, s), "fa_fwd");
+  return launch_status(fa::launch_fwd(a, p->head_dim, p->dtype, p->is_causal != 0, s), "fa_fwd");
 }
 
 static int check_bwd(const FaBwdParams* p, int split) {
@@ -422,7 +435,7 @@ static fa::BwdArgs bwd_args(const FaBwdParams* p, int split) {
   a.ssb = p->score_stride_b; a.ssh = p->score_stride_h; a.ssq = p->score_stride_q;
   a.B = p->batch; a.Tq = p->seqlen_q; a.Tk = p->seqlen_k; a.Hq = p->heads_q; a.Hk = p->heads_k;
   a.G = p->heads_q / p->heads_k;
-  const int kb = route_of(p) == kFusedAtomic ? fa::dkdv_block_keys() : fa::dkdv2_block_keys();
+  const int kb = kv_block_keys(p);
   a.nkt = (p->seqlen_k + kb - 1) / kb;
   a.nqt = (p->seqlen_q + fa::dq_block_rows() - 1) / fa::dq_block_rows();
   a.bk0 = 0;
@@ -454,7 +467,10 @@ int fa_bwd(const FaBwdParams* p) {
   const fa::BwdArgs a = bwd_args(p, split);
   const bool causal = p->is_causal != 0;
 
-  if (route_of(p) == kFusedAtomic) {
+  if (p->head_dim > 128) {
+    // head dim 256: dV and dK launches here, dQ (recomputed) in fa_bwd_finalize
+    if ((st = launch_status(fa::launch_bwd_kv_wide(a, p->dtype, causal, s), "dkdv"))) return st;
+  } else if (route_of(p) == kFusedAtomic) {
     if ((st = launch_status(fa::launch_bwd_dkdv(a, p->head_dim, p->dtype, causal, s), "dkdv"))) return st;
   } else if (!a.ds || ds_slices(p) == 1) {
     // pipelined dK/dV (+ dS tiles when the plan has them) here, dQ in fa_bwd_finalize

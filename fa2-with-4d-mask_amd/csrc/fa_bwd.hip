@@ -459,7 +459,10 @@ constexpr int kDqBN = 64;    // keys per tile
 template <typename T, int D, bool CAUSAL, bool MASK, bool SCORE>
 __global__ __launch_bounds__(256, 1) void dq_kernel(const BwdArgs a) {
   using V8 = typename Vec8<T>::type;
-  constexpr int BM = kDqBM, BN = kDqBN;
+  // head dim 256: 32-key tiles (the staging and S/dP registers of 64 keys
+  // beside 256 of Q/dO fragments and dQ accumulators spill)
+  constexpr int BM = kDqBM, BN = D > 128 ? 32 : kDqBN;
+  constexpr int NKB = BN / 32;   // 32-key blocks per tile
   constexpr int DS = D / 16, NB = D / 32, CH = D / 8;
   constexpr int KS = D + 40;   // K: row-wise and transposed reads
   constexpr int VS = D + 8;    // V: row-wise reads only
@@ -561,9 +564,9 @@ __global__ __launch_bounds__(256, 1) void dq_kernel(const BwdArgs a) {
     const T* vs = ks + KT;
     const bool active = !CAUSAL || (k0 <= q0w + 31);
     if (active) {
-      f32x16 sacc[2], pacc[2];
+      f32x16 sacc[NKB], pacc[NKB];
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
+      for (int kb = 0; kb < NKB; ++kb) {
         sacc[kb] = f32x16{};
         pacc[kb] = f32x16{};
 #pragma unroll
@@ -576,7 +579,7 @@ __global__ __launch_bounds__(256, 1) void dq_kernel(const BwdArgs a) {
       }
       const bool edge = MASK || (k0 + BN > Tk) || (CAUSAL && k0 + BN - 1 > q0w);
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+      for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
         for (int gi = 0; gi < 4; ++gi) {
           const int kk = k0 + kb * 32 + gi * 8 + hf * 4;
@@ -601,7 +604,7 @@ __global__ __launch_bounds__(256, 1) void dq_kernel(const BwdArgs a) {
       // With a mask or a score dS enters in two 16-bit parts (the rounded value
       // and its rounding residual), as in the dK/dV and dQ-from-dS kernels.
 #pragma unroll
-      for (int kk2 = 0; kk2 < 4; ++kk2) {
+      for (int kk2 = 0; kk2 < 2 * NKB; ++kk2) {
         const int kb = kk2 >> 1, c = kk2 & 1;
         V8 dsb, dsl;
         if constexpr (PREC) {
@@ -709,6 +712,7 @@ hipError_t launch_pre_t(const PreArgs& a, int D, hipStream_t s) {
   const dim3 grid((unsigned)((a.Tq + 63) / 64), (unsigned)a.Hq, (unsigned)a.B), block(256);
   if (D == 128) hipLaunchKernelGGL((preprocess_kernel<T, 128>), grid, block, 0, s, a);
   else if (D == 64) hipLaunchKernelGGL((preprocess_kernel<T, 64>), grid, block, 0, s, a);
+  else if (D == 256) hipLaunchKernelGGL((preprocess_kernel<T, 256>), grid, block, 0, s, a);
   else return hipErrorInvalidValue;
   return hipGetLastError();
 }
@@ -737,9 +741,11 @@ hipError_t launch_bwd_dq(const BwdArgs& a, int D, int dtype, bool causal, hipStr
   if (dtype == 0) {
     if (D == 128) return causal ? launch_dq_t<bf16, 128, true>(a, s) : launch_dq_t<bf16, 128, false>(a, s);
     if (D == 64) return causal ? launch_dq_t<bf16, 64, true>(a, s) : launch_dq_t<bf16, 64, false>(a, s);
+    if (D == 256) return causal ? launch_dq_t<bf16, 256, true>(a, s) : launch_dq_t<bf16, 256, false>(a, s);
   } else {
     if (D == 128) return causal ? launch_dq_t<f16, 128, true>(a, s) : launch_dq_t<f16, 128, false>(a, s);
     if (D == 64) return causal ? launch_dq_t<f16, 64, true>(a, s) : launch_dq_t<f16, 64, false>(a, s);
+    if (D == 256) return causal ? launch_dq_t<f16, 256, true>(a, s) : launch_dq_t<f16, 256, false>(a, s);
   }
   return hipErrorInvalidValue;
 }

@@ -1,0 +1,585 @@
+// Attention kernels for head dims above 128 on gfx950 (MI355X): instances at
+// head dim 256 (the host zero-pads other head dims in (128, 256], which is
+// exact).  The reference's TileLang kernels take the head dim as a
+// compile-time constant of any size (python/fa2.py:33); these restate their
+// maths (forward python/fa2.py:22-139, backward :181-302 / :305-426) with
+// tiles that operands of 512 bytes per row fit:
+//
+//   fwd_wide_kernel  one workgroup of 4 waves (one per SIMD, 512 registers
+//                    each) per (128 query rows, query head, batch).  Each wave
+//                    owns 32 rows: its Q fragment (64 registers) and its O^T
+//                    accumulator (128) stay in registers while it walks the
+//                    keys in tiles of 32:
+//                      S^T = K Q^T     16 MFMAs, A = K rows from LDS
+//                      online softmax  base 2, O and l rescaled only when a
+//                                      row's maximum grows
+//                      O^T += V^T P^T  16 MFMAs, A = V^T by transpose reads,
+//                                      B = P straight from the S registers
+//                    K/V tiles are double-buffered in LDS (rows padded so that
+//                    the K row reads and the V transpose reads spread over the
+//                    banks), staged through registers one tile ahead.
+//   kv_wide_kernel   one workgroup of 4 waves per (128 keys, kv-head, batch
+//                    [, head-group split]).  Each wave owns 32 keys with their
+//                    K (and V) fragments in registers and walks the query rows
+//                    of every head of its group in steps of 32 (Q/dO tiles
+//                    double-buffered in LDS).  Two launches:
+//                      WHICH 0 (dV)  S = Q K^T, P = exp2(S c - LSE),
+//                                    dV^T += dO^T P
+//                      WHICH 1 (dK)  S, dP = dO V^T - Delta, dS = P (dP - Delta),
+//                                    dK^T += Q^T dS  (times scale at the end)
+//                    A wave holding both accumulators (256 registers) and both
+//                    fragments (128) beside its working set would not fit the
+//                    register file at this head dim, so the dK launch
+//                    recomputes S.
+// dQ comes from the recompute kernel of fa_bwd.hip (dq_kernel), Delta and the
+// backward's LSE from its preprocess kernel.  Conventions as in the head-dim
+// 64/128 kernels: masked entries get P = 0 by select after the exp; rows past
+// Tq carry LSE = +inf (P = 0); keys past Tk read key Tk-1 (finite) and are
+// masked; with a mask or a score, P and dS enter their products in several
+// 16-bit parts (P to fp32 precision in dV, dS to about 16 bits; P_hi + P_lo
+// in O) and the forward writes O's rounding residual when asked.
+#include "fa_common.h"
+#include "fa_kernels.h"
+
+namespace fa {
+namespace {
+
+constexpr int kWD = 256;         // head dim of these instances
+constexpr int kWRows = 128;      // forward: query rows per workgroup
+constexpr int kWKeys = 32;       // forward: keys per tile
+constexpr int kWKvKeys = 128;    // dK/dV: keys per workgroup (4 waves x 32), 32-row steps
+
+template <typename T>
+__device__ __forceinline__ u32x2 pack4w(float x0, float x1, float x2, float x3) {
+  typedef T T4 __attribute__((ext_vector_type(4)));
+  T4 v;
+  v[0] = (T)x0; v[1] = (T)x1; v[2] = (T)x2; v[3] = (T)x3;
+  return __builtin_bit_cast(u32x2, v);
+}
+
+// ---------------------------------------------------------------------------
+// forward
+// ---------------------------------------------------------------------------
+template <typename T, bool CAUSAL, bool MASK, bool SCORE>
+__global__ __launch_bounds__(256, 1) void fwd_wide_kernel(const FwdArgs a) {
+  using V8 = typename Vec8<T>::type;
+  constexpr int D = kWD, DS = D / 16, NB = D / 32, CH = D / 8;
+  constexpr int BM = kWRows, BN = kWKeys;
+  // padded row strides (elements): K rows read 16 bytes per lane over 16
+  // rows, V read by 4-row transpose reads
+  constexpr int KS = D + 8, VS = D + 16;
+  constexpr int KT = BN * KS, VT = BN * VS;
+  constexpr int U = BN * CH / 256;      // 16-byte chunks per thread per tile and kind
+  constexpr int OS = D + 8;             // epilogue staging stride
+  static_assert(4 * 32 * OS <= 2 * (KT + VT), "O staging fits in the tile buffers");
+  constexpr bool PREC = MASK || SCORE;
+  __shared__ __attribute__((aligned(16))) T smem[2 * (KT + VT)];
+
+  // (batch, kv-head, [query tile rank, head in group]); longest workgroups
+  // first when causal (query tile nqt-1-rank)
+  const int nblk = a.B * a.Hq * a.nqt;
+  const int W = xcd_remap(blockIdx.x, nblk);
+  const int per_kv = a.G * a.nqt;
+  const int bk = W / per_kv;
+  const int rem = W - bk * per_kv;
+  const int qt_rank = rem / a.G;
+  const int g = rem - qt_rank * a.G;
+  const int b = bk / a.Hk, kvh = bk - b * a.Hk;
+  const int h = kvh * a.G + g;
+  const int qt = a.nqt - 1 - qt_rank;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, hf = lane >> 5;
+  const int Tq = a.Tq, Tk = a.Tk;
+  const int q0 = qt * BM, q0w = q0 + wave * 32, qrow = q0w + l32;
+  const int qrow_c = min(qrow, Tq - 1);
+  const float c2 = a.scale_log2;
+
+  // Q fragment (B of S^T): lane holds Q[qrow][16 ds + 8 hf .. +7]; a negative
+  // scale is folded into Q's sign (and the score's)
+  V8 qf[DS];
+  {
+    const uint32_t neg = a.qsign < 0.f ? 0x80008000u : 0u;
+    const T* src = (const T*)a.q + b * a.qsb + h * a.qsh + (int64_t)qrow_c * a.qst + hf * 8;
+#pragma unroll
+    for (int ds = 0; ds < DS; ++ds) qf[ds] = as_vec8<T>(gload16(src + ds * 16) ^ neg);
+  }
+  const T* __restrict__ kp = (const T*)a.k + b * a.ksb + kvh * a.ksh;
+  const T* __restrict__ vp = (const T*)a.v + b * a.vsb + kvh * a.vsh;
+  const uint32_t* mbits = nullptr;
+  if constexpr (MASK) {
+    const int pm = mask_plane(a.ml, b, h);
+    mbits = (const uint32_t*)(a.mws + a.ml.bits + pm * a.ml.pbits) + (int64_t)qrow_c * a.ml.wk;
+  }
+  // score rows of the wave through one range-checked buffer from its first
+  // row (the host keeps 32 rows below 4 GiB); keys past Tk read the next row
+  // or zeros and are masked
+  const int srow0 = min(q0 + 32 * __builtin_amdgcn_readfirstlane(wave), Tq - 1);
+  const __amdgpu_buffer_rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc(
+      SCORE ? (void*)(a.score + b * a.ssb + h * a.ssh + (int64_t)srow0 * a.ssq) : nullptr, (short)0,
+      SCORE ? (int)(((int64_t)min(Tq - 1 - srow0, 31) * a.ssq + Tk) * 4) : 0, 0x00020000);
+  const uint32_t soff_row = (uint32_t)((int64_t)(qrow_c - srow0) * a.ssq * 4) + hf * 16;
+
+  const int kv_end = CAUSAL ? min(Tk, q0 + BM) : Tk;
+  const int nt = (kv_end + BN - 1) / BN;
+
+  // staging: chunk u of thread t is row idx / CH, chunk idx % CH of the tile
+  // (idx = t + 256 u); keys past Tk read key Tk-1
+  u32x4 kreg[U], vreg[U];
+  auto load_tile = [&](int k0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int idx = tid + u * 256, r = idx / CH, c = idx % CH;
+      const int kk = min(k0 + r, Tk - 1);
+      kreg[u] = gload16(kp + (int64_t)kk * a.kst + c * 8);
+      vreg[u] = gload16(vp + (int64_t)kk * a.vst + c * 8);
+    }
+  };
+  auto store_tile = [&](int buf) __attribute__((always_inline)) {
+    T* ks = smem + buf * (KT + VT);
+    T* vs = ks + KT;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int idx = tid + u * 256, r = idx / CH, c = idx % CH;
+      lds_write16(ks + r * KS + c * 8, kreg[u]);
+      lds_write16(vs + r * VS + c * 8, vreg[u]);
+    }
+  };
+
+  f32x16 oacc[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) oacc[nb] = f32x16{};
+  float m_run = kNegInf, l_run = 0.f;
+  // transpose-read lane pattern: rows 4 hf + (lane / 4) % 4 (+8), columns
+  // 16 ((lane / 16) % 2) + 4 (lane % 4) of each 32-column block
+  const int tr_row = 4 * hf + ((lane >> 2) & 3);
+  const int tr_col = ((lane >> 4) & 1) * 16 + (lane & 3) * 4;
+
+  load_tile(0);
+  store_tile(0);
+  __syncthreads();
+  for (int j = 0; j < nt; ++j) {
+    const int k0 = j * BN;
+    const bool more = j + 1 < nt;
+    if (more) load_tile(k0 + BN);
+    const T* ks = smem + (j & 1) * (KT + VT);
+    const T* vs = ks + KT;
+    // causal: a tile wholly above the wave's rows adds nothing
+    const bool active = !CAUSAL || k0 <= q0w + 31;
+    if (active) {
+      // lane entry i: key k0 + 8 (i/4) + 4 hf + i%4 of row qrow
+      f32x16 s = f32x16{};
+      if constexpr (SCORE) {
+#pragma unroll
+        for (int gi = 0; gi < 4; ++gi) {
+          const f32x4 x = __builtin_bit_cast(
+              f32x4, __builtin_amdgcn_raw_buffer_load_b128(srs, soff_row + (uint32_t)(k0 + gi * 8) * 4, 0, 0));
+#pragma unroll
+          for (int t = 0; t < 4; ++t) s[gi * 4 + t] = a.qsign < 0.f ? -x[t] : x[t];
+        }
+      }
+      uint32_t mw = ~0u;
+      if constexpr (MASK) mw = mbits[k0 >> 5] >> (4 * hf);
+#pragma unroll
+      for (int ds = 0; ds < DS; ++ds)
+        s = mfma32(as_vec8<T>(lds_read16(ks + l32 * KS + ds * 16 + hf * 8)), qf[ds], s);
+
+      float x[16];
+      const bool edge = MASK || a.zero_scale || (k0 + BN > Tk) || (CAUSAL && k0 + BN - 1 > q0w);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) x[i] = s[i];
+      if (edge) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int kk = k0 + 8 * (i >> 2) + 4 * hf + (i & 3);
+          bool keep = kk < Tk;
+          if constexpr (CAUSAL) keep = keep && kk <= qrow;
+          if constexpr (MASK) keep = keep && ((mw >> (8 * (i >> 2) + (i & 3))) & 1u);
+          x[i] = keep ? (a.zero_scale ? 0.f : x[i]) : kNegInf;
+        }
+      }
+      float mx = x[0];
+#pragma unroll
+      for (int i = 1; i < 16; ++i) mx = fmaxf(mx, x[i]);
+      const float mt = half_max(mx) * c2;   // the row's largest logit of the tile (scaled)
+      if (wave_any(mt > m_run)) {
+        const float m_new = fmaxf(m_run, mt);
+        const float alpha = m_run == kNegInf ? 0.f : exp2_fast(m_run - m_new);
+        l_run *= alpha;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) oacc[nb] *= alpha;
+        m_run = m_new;
+      }
+      const float mneg = m_run == kNegInf ? 0.f : -m_run;
+      float p[16], lsum = 0.f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        p[i] = exp2_fast(fmaf(x[i], c2, mneg));
+        lsum += p[i];
+      }
+      l_run += lsum;
+      // P packed per 16-key step c: slot t <-> key 16 c + 8 (t/4) + 4 hf + t%4
+      V8 pk[2], pkl[PREC ? 2 : 1];
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        pk[c] = pack8<T>(p[8 * c + 0], p[8 * c + 1], p[8 * c + 2], p[8 * c + 3], p[8 * c + 4], p[8 * c + 5],
+                         p[8 * c + 6], p[8 * c + 7]);
+        if constexpr (PREC) {
+          float r[8];
+#pragma unroll
+          for (int t = 0; t < 8; ++t) r[t] = p[8 * c + t] - (float)(T)p[8 * c + t];
+          pkl[c] = pack8<T>(r[0], r[1], r[2], r[3], r[4], r[5], r[6], r[7]);
+        }
+      }
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const int row = 16 * c + tr_row;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+          const int col = nb * 32 + tr_col;
+          const V8 av = cat_tr<T>(lds_read_tr(vs + row * VS + col), lds_read_tr(vs + (row + 8) * VS + col));
+          oacc[nb] = mfma32(av, pk[c], oacc[nb]);
+          if constexpr (PREC) oacc[nb] = mfma32(av, pkl[c], oacc[nb]);
+        }
+      }
+    }
+    if (more) store_tile((j + 1) & 1);
+    __syncthreads();
+  }
+
+  // ---- epilogue: O = acc / l (NaN for a row with no kept key), LSE ---------------
+  const float l_tot = half_sum(l_run);
+  const float inv = 1.0f / l_tot;
+  T* os = smem + wave * 32 * OS;   // wave-private rows; the loop ended with a barrier
+  constexpr int NU = 32 * CH / 64;
+  auto put_rows = [&](bool resid, T* dst, int64_t sb, int64_t st, int64_t sh) __attribute__((always_inline)) {
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int gi = 0; gi < 4; ++gi) {
+        float v[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const float o = oacc[nb][gi * 4 + t] * inv;
+          v[t] = resid ? o - (float)(T)o : o;
+        }
+        lds_write8(os + l32 * OS + nb * 32 + gi * 8 + hf * 4, pack4w<T>(v[0], v[1], v[2], v[3]));
+      }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    u32x4 ov[NU];
+#pragma unroll
+    for (int u = 0; u < NU; ++u) {
+      const int idx = lane + u * 64;
+      ov[u] = lds_read16(os + (idx / CH) * OS + (idx % CH) * 8);
+    }
+    T* op = dst + b * sb + h * sh;
+#pragma unroll
+    for (int u = 0; u < NU; ++u) {
+      const int idx = lane + u * 64, r = idx / CH, c = idx % CH;
+      if (q0w + r < Tq) gstore16(op + (int64_t)(q0w + r) * st + c * 8, ov[u]);
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  };
+  put_rows(false, (T*)a.o, a.osb, a.ost, a.osh);
+  if (hf == 0 && qrow < Tq)
+    a.lse[((int64_t)b * a.Hq + h) * Tq + qrow] = (l_tot > 0.f) ? m_run + log2_fast(l_tot) : kPosInf;
+  if constexpr (PREC) {
+    if (a.olo) put_rows(true, (T*)a.olo, a.olsb, a.olst, a.olsh);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dV (WHICH 0) / dK (WHICH 1)
+// ---------------------------------------------------------------------------
+template <typename T, bool CAUSAL, bool MASK, bool SCORE, int WHICH>
+__global__ __launch_bounds__(256, 1) void kv_wide_kernel(const BwdArgs a) {
+  using V8 = typename Vec8<T>::type;
+  constexpr int D = kWD, DS = D / 16, NB = D / 32, CH = D / 8;
+  constexpr bool DK = WHICH == 1;
+  // padded row stride of the Q / dO tiles (row reads and transpose reads)
+  constexpr int QS = D + 40;
+  constexpr int QT = 32 * QS;
+  constexpr int U = 32 * CH / 256;      // 16-byte chunks per thread per tile and kind
+  constexpr int OS = D + 8;
+  static_assert(4 * 32 * OS <= 4 * QT, "epilogue staging fits in the tile buffers");
+  constexpr bool PREC = MASK || SCORE;
+  __shared__ __attribute__((aligned(16))) T smem[4 * QT];          // [buf][Q | dO]
+  __shared__ __attribute__((aligned(16))) float lsd[2][2][32];     // [buf][LSE | -Delta][row]
+
+  const int nblk = a.nbk * a.nkt * a.split;
+  const int W = xcd_remap(blockIdx.x, nblk);
+  const int per_bk = a.split * a.nkt;
+  const int bkl = W / per_bk;
+  const int bk = a.bk0 + bkl;
+  const int rem = W - bkl * per_bk;
+  const int sp = rem / a.nkt;
+  const int kt = rem - sp * a.nkt;    // ascending: causal work shrinks with the block
+  const int b = bk / a.Hk, kvh = bk - b * a.Hk;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, hf = lane >> 5;
+  const int Tq = a.Tq, Tk = a.Tk;
+  const int kt0 = kt * kWKvKeys, kw0 = kt0 + wave * 32;
+  const int key = kw0 + l32, kc = min(key, Tk - 1);
+  const float c2 = a.scale_log2;
+
+  // K (and V) fragments, B of S = Q K^T and dP = dO V^T: lane holds
+  // K[key][16 ds + 8 hf .. +7]
+  V8 kf[DS], vf[DK ? DS : 1];
+  {
+    const T* kp = (const T*)a.k + b * a.ksb + kvh * a.ksh + (int64_t)kc * a.kst + hf * 8;
+    const T* vp = (const T*)a.v + b * a.vsb + kvh * a.vsh + (int64_t)kc * a.vst + hf * 8;
+#pragma unroll
+    for (int ds = 0; ds < DS; ++ds) {
+      kf[ds] = as_vec8<T>(gload16(kp + ds * 16));
+      if constexpr (DK) vf[ds] = as_vec8<T>(gload16(vp + ds * 16));
+    }
+  }
+
+  // steps: (head of the group split, 32-row step from qstart), rows above the
+  // key block are masked when causal
+  const int gsz = a.G / a.split;
+  const int h_first = kvh * a.G + sp * gsz;
+  const int qstart = CAUSAL ? (kt0 / 32) * 32 : 0;
+  const int nst = qstart < Tq ? (Tq - qstart + 31) / 32 : 0;
+  const int n = gsz * nst;
+
+  // staging of step j: Q / dO rows (past Tq: row Tq-1, whose P is 0 there),
+  // LSE (+inf past Tq) and -Delta (0 past Tq) of its rows
+  u32x4 qreg[U], dreg[U];
+  float lreg = 0.f;
+  auto load_step = [&](int j) __attribute__((always_inline)) {
+    const int hh = h_first + j / nst, qs = qstart + 32 * (j % nst);
+    const T* qh = (const T*)a.q + b * a.qsb + (int64_t)hh * a.qsh;
+    const T* dh = (const T*)a.dout + b * a.dsb + (int64_t)hh * a.dsh;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int idx = tid + u * 256, r = idx / CH, c = idx % CH;
+      const int qq = min(qs + r, Tq - 1);
+      qreg[u] = gload16(qh + (int64_t)qq * a.qst + c * 8);
+      dreg[u] = gload16(dh + (int64_t)qq * a.dst + c * 8);
+    }
+    if (tid < 64) {
+      const int qq = qs + l32;
+      const int64_t ri = ((int64_t)b * a.Hq + hh) * Tq + qq;
+      lreg = hf == 0 ? (qq < Tq ? a.lse[ri] : kPosInf) : (qq < Tq ? -a.delta[ri] : 0.f);
+    }
+  };
+  auto store_step = [&](int buf) __attribute__((always_inline)) {
+    T* qs_ = smem + buf * 2 * QT;
+    T* ds_ = qs_ + QT;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int idx = tid + u * 256, r = idx / CH, c = idx % CH;
+      lds_write16(qs_ + r * QS + c * 8, qreg[u]);
+      lds_write16(ds_ + r * QS + c * 8, dreg[u]);
+    }
+    if (tid < 64) lsd[buf][hf][l32] = lreg;
+  };
+
+  f32x16 acc[NB];   // dV^T or dK^T [32 nb + 8 (i/4) + 4 hf + i%4][key]
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) acc[nb] = f32x16{};
+  const int tr_row = 4 * hf + ((lane >> 2) & 3);
+  const int tr_col = ((lane >> 4) & 1) * 16 + (lane & 3) * 4;
+  const uint32_t s_lane = SCORE ? (uint32_t)(((int64_t)4 * hf * a.ssq + kc) * 4) : 0u;
+  const uint32_t s_row = (uint32_t)a.ssq * 4u;
+
+  if (n > 0) {
+    load_step(0);
+    store_step(0);
+  }
+  __syncthreads();
+  for (int j = 0; j < n; ++j) {
+    const bool more = j + 1 < n;
+    if (more) load_step(j + 1);
+    const int buf = j & 1;
+    const int hh = h_first + j / nst, qs = qstart + 32 * (j % nst);
+    const T* qt_ = smem + buf * 2 * QT;
+    const T* dt_ = qt_ + QT;
+    // causal: a step wholly above the wave's keys adds nothing
+    const bool active = !CAUSAL || qs + 31 >= kw0;
+    if (active) {
+      // lane entry i: row qs + 8 (i/4) + 4 hf + i%4 at key `key`
+      f32x16 s = f32x16{};
+      if constexpr (SCORE) {
+        const uint32_t nrec = (uint32_t)(((int64_t)min(Tq - qs, 32) - 1) * a.ssq * 4 + (int64_t)Tk * 4);
+        const auto rs = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(a.score + b * a.ssb + (int64_t)hh * a.ssh + (int64_t)qs * a.ssq), (short)0, (int)nrec, 0x00020000);
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          s[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                               rs, s_lane, (uint32_t)(8 * (i >> 2) + (i & 3)) * s_row, 0));
+      }
+      uint32_t mw = ~0u;
+      if constexpr (MASK) {
+        const uint32_t* bt = (const uint32_t*)(a.mws + a.ml.bitsT + mask_plane(a.ml, b, hh) * a.ml.pbitsT);
+        mw = bt[((int64_t)(kc >> 5) * a.ml.wq + (qs >> 5)) * 32 + (kc & 31)] >> (4 * hf);
+      }
+#pragma unroll
+      for (int ds = 0; ds < DS; ++ds)
+        s = mfma32(as_vec8<T>(lds_read16(qt_ + l32 * QS + ds * 16 + hf * 8)), kf[ds], s);
+      f32x16 dp = f32x16{};
+      if constexpr (DK) {
+#pragma unroll
+        for (int gi = 0; gi < 4; ++gi) {
+          const f32x4 d4 = *(const f32x4*)&lsd[buf][1][8 * gi + 4 * hf];
+#pragma unroll
+          for (int t = 0; t < 4; ++t) dp[gi * 4 + t] = d4[t];
+        }
+#pragma unroll
+        for (int ds = 0; ds < DS; ++ds)
+          dp = mfma32(as_vec8<T>(lds_read16(dt_ + l32 * QS + ds * 16 + hf * 8)), vf[ds], dp);
+      }
+      float p[16];
+#pragma unroll
+      for (int gi = 0; gi < 4; ++gi) {
+        const f32x4 l4 = *(const f32x4*)&lsd[buf][0][8 * gi + 4 * hf];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const int i = gi * 4 + t, row = qs + 8 * gi + 4 * hf + t;
+          const float sv = a.zero_scale ? 0.f : s[i];
+          float pv = exp2_fast(fmaf(sv, c2, -l4[t]));
+          bool keep = key < Tk;
+          if constexpr (CAUSAL) keep = keep && key <= row;
+          if constexpr (MASK) keep = keep && ((mw >> (8 * gi + t)) & 1u);
+          pv = keep ? pv : 0.f;
+          p[i] = DK ? pv * dp[i] : pv;   // dK: dS = P (dP - Delta) (scale applied at the end)
+        }
+      }
+      // packed per 16-row step c: slot t <-> row 16 c + 8 (t/4) + 4 hf + t%4;
+      // P in three parts (dV), dS in two (dK) with a mask or a score
+      constexpr int NP = PREC ? (DK ? 2 : 3) : 1;
+      V8 pk[2][NP];
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        if constexpr (PREC) {
+          u32x4 w[NP];
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            uint32_t x0, x1, x2 = 0;
+            if constexpr (DK) split2<T>(p[8 * c + 2 * k], p[8 * c + 2 * k + 1], &x0, &x1);
+            else split3<T>(p[8 * c + 2 * k], p[8 * c + 2 * k + 1], &x0, &x1, &x2);
+            w[0][k] = x0;
+            w[1][k] = x1;
+            if constexpr (NP == 3) w[NP - 1][k] = x2;
+          }
+#pragma unroll
+          for (int x = 0; x < NP; ++x) pk[c][x] = as_vec8<T>(w[x]);
+        } else {
+          pk[c][0] = pack8<T>(p[8 * c + 0], p[8 * c + 1], p[8 * c + 2], p[8 * c + 3], p[8 * c + 4], p[8 * c + 5],
+                              p[8 * c + 6], p[8 * c + 7]);
+        }
+      }
+      // dV^T += dO^T P (A = dO^T) / dK^T += Q^T dS (A = Q^T), transpose reads
+      const T* at = DK ? qt_ : dt_;
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const int row = 16 * c + tr_row;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+          const int col = nb * 32 + tr_col;
+          const V8 av = cat_tr<T>(lds_read_tr(at + row * QS + col), lds_read_tr(at + (row + 8) * QS + col));
+#pragma unroll
+          for (int x = 0; x < NP; ++x) acc[nb] = mfma32(av, pk[c][x], acc[nb]);
+        }
+      }
+    }
+    if (more) store_step((j + 1) & 1);
+    __syncthreads();
+  }
+
+  // ---- epilogue: dK (times scale) or dV (NaN for a kv-head with a dead row) --------
+  const bool nan_out = !DK && a.dead[b * a.Hk + kvh] != 0;
+  const float nanv = __builtin_nanf("");
+  const float mul = DK ? a.scale : 1.f;
+  if (a.split == 1) {
+    T* stg = smem + wave * 32 * OS;   // wave-private rows; the loop ended with a barrier
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int gi = 0; gi < 4; ++gi) {
+        const u32x2 v = nan_out ? pack4w<T>(nanv, nanv, nanv, nanv)
+                                : pack4w<T>(acc[nb][gi * 4 + 0] * mul, acc[nb][gi * 4 + 1] * mul,
+                                            acc[nb][gi * 4 + 2] * mul, acc[nb][gi * 4 + 3] * mul);
+        lds_write8(stg + l32 * OS + nb * 32 + gi * 8 + hf * 4, v);
+      }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    constexpr int NU = 32 * CH / 64;
+    u32x4 ov[NU];
+#pragma unroll
+    for (int u = 0; u < NU; ++u) {
+      const int idx = lane + u * 64;
+      ov[u] = lds_read16(stg + (idx / CH) * OS + (idx % CH) * 8);
+    }
+    T* dst = DK ? (T*)a.dk + b * a.dksb + kvh * a.dksh : (T*)a.dv + b * a.dvsb + kvh * a.dvsh;
+    const int64_t dstt = DK ? a.dkst : a.dvst;
+#pragma unroll
+    for (int u = 0; u < NU; ++u) {
+      const int idx = lane + u * 64, r = idx / CH, c = idx % CH;
+      if (kw0 + r < Tk) gstore16(dst + (int64_t)(kw0 + r) * dstt + c * 8, ov[u]);
+    }
+  } else {
+    // head-group split: fp32 slabs [split][B, Tk, Hk, D], summed in a fixed order later
+    const int64_t slab = (int64_t)sp * a.B * Tk * a.Hk * D;
+    float* dst = DK ? a.dk_accum : a.dv_accum;
+    if (key < Tk) {
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int gi = 0; gi < 4; ++gi) {
+          const int d = nb * 32 + gi * 8 + hf * 4;
+          const int64_t o = slab + (((int64_t)b * Tk + key) * a.Hk + kvh) * D + d;
+          f32x4 v4;
+#pragma unroll
+          for (int t = 0; t < 4; ++t) v4[t] = nan_out ? nanv : acc[nb][gi * 4 + t] * mul;
+          *(f32x4*)(dst + o) = v4;
+        }
+    }
+  }
+}
+
+template <typename T, bool CAUSAL>
+hipError_t launch_fwd_w(const FwdArgs& a, hipStream_t s) {
+  const dim3 grid((unsigned)(a.B * a.Hq * a.nqt)), block(256);
+  const bool m = a.mask != nullptr, sc = a.score != nullptr;
+  if (m && sc) hipLaunchKernelGGL((fwd_wide_kernel<T, CAUSAL, true, true>), grid, block, 0, s, a);
+  else if (m) hipLaunchKernelGGL((fwd_wide_kernel<T, CAUSAL, true, false>), grid, block, 0, s, a);
+  else if (sc) hipLaunchKernelGGL((fwd_wide_kernel<T, CAUSAL, false, true>), grid, block, 0, s, a);
+  else hipLaunchKernelGGL((fwd_wide_kernel<T, CAUSAL, false, false>), grid, block, 0, s, a);
+  return hipGetLastError();
+}
+
+template <typename T, bool CAUSAL, int WHICH>
+hipError_t launch_kv_w(const BwdArgs& a, hipStream_t s) {
+  const dim3 grid((unsigned)(a.nbk * a.nkt * a.split)), block(256);
+  const bool m = a.mask != nullptr, sc = a.score != nullptr;
+  if (m && sc) hipLaunchKernelGGL((kv_wide_kernel<T, CAUSAL, true, true, WHICH>), grid, block, 0, s, a);
+  else if (m) hipLaunchKernelGGL((kv_wide_kernel<T, CAUSAL, true, false, WHICH>), grid, block, 0, s, a);
+  else if (sc) hipLaunchKernelGGL((kv_wide_kernel<T, CAUSAL, false, true, WHICH>), grid, block, 0, s, a);
+  else hipLaunchKernelGGL((kv_wide_kernel<T, CAUSAL, false, false, WHICH>), grid, block, 0, s, a);
+  return hipGetLastError();
+}
+
+template <typename T, bool CAUSAL>
+hipError_t launch_kv_both(const BwdArgs& a, hipStream_t s) {
+  const hipError_t e = launch_kv_w<T, CAUSAL, 0>(a, s);
+  return e != hipSuccess ? e : launch_kv_w<T, CAUSAL, 1>(a, s);
+}
+
+}  // namespace
+
+int fwd_wide_block_rows() { return kWRows; }
+int kv_wide_block_keys() { return kWKvKeys; }
+
+hipError_t launch_fwd_wide(const FwdArgs& a, int dtype, bool causal, hipStream_t s) {
+  if (dtype == 0) return causal ? launch_fwd_w<bf16, true>(a, s) : launch_fwd_w<bf16, false>(a, s);
+  return causal ? launch_fwd_w<f16, true>(a, s) : launch_fwd_w<f16, false>(a, s);
+}
+
+hipError_t launch_bwd_kv_wide(const BwdArgs& a, int dtype, bool causal, hipStream_t s) {
+  if (dtype == 0) return causal ? launch_kv_both<bf16, true>(a, s) : launch_kv_both<bf16, false>(a, s);
+  return causal ? launch_kv_both<f16, true>(a, s) : launch_kv_both<f16, false>(a, s);
+}
+
+}  // namespace fa

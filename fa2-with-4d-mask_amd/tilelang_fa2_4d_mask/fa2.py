@@ -24,10 +24,12 @@ What differs on purpose:
   live-tile lists) and the workspace is kept for the backward, so the kernels
   skip tiles without a kept entry (the reference streams every tile's mask
   bytes, python/fa2.py:107-114, 261-280);
-* the kernels exist for head dims 64 and 128 (the reference compiles any D,
-  python/fa2.py:33); other D up to 128 run zero-padded to the next of those,
-  which is exact (see ``kernel_head_dim``), at the price of padded copies of
-  the operands.
+* the kernels exist for head dims 64, 128 and 256 (the reference compiles
+  any D, python/fa2.py:33); other D up to 256 run zero-padded to the next of
+  those, which is exact (see ``kernel_head_dim``), at the price of padded
+  copies of the operands.  Head dim 256 has kernels of its own (128-row
+  forward blocks, dK and dV in two launches, dQ recomputed in both backward
+  modes: no dS workspace, no atomics).
 """
 
 from __future__ import annotations
@@ -53,7 +55,7 @@ DS_LIMIT_DEFAULT = 4 << 30
 
 
 # Head dims the kernels are built for.
-KERNEL_HEAD_DIMS = (64, 128)
+KERNEL_HEAD_DIMS = (64, 128, 256)
 
 
 def kernel_head_dim(D: int) -> int:

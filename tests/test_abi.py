@@ -121,7 +121,8 @@ def bwd_params(**over):
 
 FWD_ERRORS = [
     (dict(head_dim=96), 3, "head_dim 96"),
-    (dict(head_dim=256), 3, "head_dim 256"),
+    (dict(head_dim=192), 3, "head_dim 192"),
+    (dict(head_dim=512), 3, "head_dim 512"),
     (dict(dtype=5), 4, "dtype"),
     (dict(heads_k=5), 2, "divisible"),
     (dict(batch=0), 2, "sizes must be"),
@@ -291,6 +292,21 @@ def test_plan_mqa_splits_the_group(lib):
     assert plan.kv_split == 4 and plan.dkv_accum_elems == 16384 * 64 and plan.dkv_accum_zeroed == 1
     plan = _plan(lib, kv_split=8, **m)
     assert plan.kv_split == 8
+
+
+def test_plan_head_dim_256_recomputes_dq(lib):
+    # head dim 256: dQ recomputed in both modes (no dS tiles, no fp32 dQ
+    # atomics); dK/dV over 128-key blocks, the group split while a launch has
+    # fewer than 512 workgroups (fp32 slabs, fully overwritten)
+    w = dict(seqlen_q=4096, seqlen_k=4096, heads_q=32, heads_k=8, head_dim=256)
+    for atomic in (0, 1):
+        for limit in (0, -1, 8 << 30):
+            plan = _plan(lib, atomic_dq=atomic, ds_limit_bytes=limit, **w)
+            assert plan.ds_elems == 0 and plan.needs_dq_accum == 0 and plan.dq_accum_elems == 0, (atomic, limit)
+            assert plan.dq_split == 1 and plan.kv_split == 2 and plan.dkv_accum_zeroed == 0
+            assert plan.dkv_accum_elems == 2 * 4096 * 8 * 256
+    plan = _plan(lib, atomic_dq=1, seqlen_q=8192, seqlen_k=8192, heads_q=8, heads_k=8, head_dim=256)
+    assert plan.kv_split == 1 and plan.dkv_accum_elems == 0
 
 
 def test_missing_library_fails_loudly(tmp_path):

@@ -211,9 +211,10 @@ def test_scale_values(cuda, scale, mode):
     check(ours, ref, label=f"scale={scale}/{mode}")
 
 
-def test_dead_rows_policy(cuda):
+@pytest.mark.parametrize("d", [64, 256])
+def test_dead_rows_policy(cuda, d):
     """Rows with no kept key: O row NaN, dQ row exactly 0, dV of that kv-head NaN."""
-    cfg = C("dead", 2, 256, 256, 4, 2, 64, mask="bernoulli")
+    cfg = C("dead", 2, 256, 256, 4, 2, d, mask="bernoulli")
     case = I.make_case(cfg, seed=2)
     m = case["mask"].clone()
     m[0, 1, 17, :] = False     # batch 0, head 1 (kv-head 0)
@@ -235,6 +236,7 @@ def test_dead_rows_policy(cuda):
 
 SCORE_DEAD = [
     C("score_dead_mask", 2, 256, 256, 4, 2, 64, mask="bernoulli", score="normal"),
+    C("score_dead_mask_causal_d256", 1, 200, 200, 4, 2, 256, is_causal=True, mask="bernoulli", score="normal"),
     C("score_dead_mask_causal", 1, 320, 320, 4, 2, 128, is_causal=True, mask="bernoulli", score="normal"),
     C("score_dead_nomask", 2, 256, 200, 4, 2, 128, score="normal"),
     C("score_dead_nomask_causal", 1, 300, 300, 4, 1, 64, is_causal=True, score="normal"),
@@ -523,4 +525,92 @@ def test_random_configs_vs_oracle(cuda, seed):
     # group (several ulps at large |dV|).  The same bar against the exact
     # gradients (float64 throughout, same inputs) pins that the kernels' own
     # error is no larger.
+    check(ours, run_exact_cpu(case, cfg), label=f"{cfg.name} {mode} vs float64", **bars)
+
+
+# ---------------------------------------------------------------------------
+# Head dims above 128 (the reference compiles any D, python/fa2.py:33): kernels
+# at 256 (fa_wide.hip; dQ recomputed in both backward modes), other head dims
+# in (128, 256] zero-padded to 256 by the host.
+# ---------------------------------------------------------------------------
+WIDE_D = [
+    C("d256_mha", 2, 200, 200, 4, 4, 256),
+    C("d256_gqa_causal", 1, 300, 300, 8, 2, 256, is_causal=True),
+    C("d256_causal_tq_gt_tk", 1, 333, 130, 4, 2, 256, is_causal=True),
+    C("d256_tq_lt_tk_mqa", 1, 130, 333, 4, 1, 256),
+    C("d256_mask", 2, 200, 200, 4, 2, 256, mask="bernoulli", mask_heads=4, keep_prob=0.5),
+    C("d256_packed_docs", 1, 256, 256, 4, 2, 256, mask="packed_docs", mask_heads=1,
+      extra={"packed": {"lo": 16, "hi": 128}}),
+    C("d256_score_fp16", 1, 160, 224, 4, 2, 256, torch.float16, score="normal"),
+    C("d256_mask_score_causal_bshd", 1, 257, 257, 8, 2, 256, layout="bshd", is_causal=True, mask="bernoulli",
+      score="normal"),
+    C("d192_padded", 1, 200, 240, 4, 2, 192),
+    C("d160_causal_fp16", 1, 180, 180, 4, 4, 160, torch.float16, is_causal=True),
+]
+
+
+@pytest.mark.parametrize("mode", ["atomic", "det_ds", "atomic_fused"])
+@pytest.mark.parametrize("cfg", WIDE_D, ids=[c.name for c in WIDE_D])
+def test_head_dim_256(cuda, cfg, mode):
+    """Output and gradients at head dims above 128 against the CPU oracle and
+    against the same graph in float64, at the small-shape bar; gradients shaped
+    like the inputs."""
+    print(f"case {cfg.name} mode={mode}", flush=True)
+    atomic, ds_limit = MODES[mode]
+    case = I.make_case(cfg, seed=5)
+    ours = run_ours(case, cfg, atomic=atomic, ds_limit=ds_limit)
+    ref = run_oracle_cpu(case, cfg)
+    for name in ("dq", "dk", "dv", "out"):
+        assert ours[name].shape == ref[name].shape, name
+    check(ours, ref, label=f"{cfg.name}/{mode}")
+    check(ours, run_exact_cpu(case, cfg), label=f"{cfg.name}/{mode} vs float64")
+
+
+def test_head_dim_256_modes_agree_bitwise(cuda):
+    """At head dim 256 both backward modes run the deterministic recompute route:
+    repeated calls and the two modes give the same bits."""
+    cfg = C("d256_det", 1, 384, 384, 8, 2, 256, is_causal=True, mask="bernoulli", score="normal")
+    case = I.make_case(cfg, seed=9)
+    a = run_ours(case, cfg, atomic=False)
+    b = run_ours(case, cfg, atomic=False)
+    c = run_ours(case, cfg, atomic=True)
+    for n in a:
+        assert torch.equal(a[n], b[n]) and torch.equal(a[n], c[n]), n
+
+
+def _random_case_wide(seed):
+    import random
+
+    r = random.Random(5000 + seed)
+    hk = r.choice([1, 2, 3])
+    g = r.choice([1, 2, 4])
+    d = r.choice([256, 256, 256, 192, 160, 144])
+    tq = r.choice([r.randint(1, 48), r.randint(49, 400)])
+    tk = tq if r.random() < 0.4 else r.choice([r.randint(1, 48), r.randint(49, 400)])
+    causal = r.random() < 0.3
+    mask, mask_heads, keep = None, 0, 0.75
+    u = r.random()
+    if u < 0.35:
+        mask, mask_heads, keep = "bernoulli", r.choice([1, hk * g]), r.choice([0.3, 0.6, 0.9])
+    elif u < 0.5 and tq == tk and tq >= 32:
+        mask, mask_heads = "packed_docs", 1
+    score = "normal" if r.random() < 0.4 else None
+    cfg = C(f"wide{seed}", r.choice([1, 2]), tq, tk, hk * g, hk, d,
+            torch.float16 if r.random() < 0.3 else torch.bfloat16, is_causal=causal, mask=mask,
+            mask_heads=mask_heads, score=score, keep_prob=keep, layout=r.choice(["bhsd", "bshd"]),
+            extra={"packed": {"lo": 16, "hi": 128}} if mask == "packed_docs" else {})
+    return cfg, r.choice(list(MODES))
+
+
+@pytest.mark.parametrize("seed", list(range(24)))
+def test_random_wide_configs_vs_oracle(cuda, seed):
+    cfg, mode = _random_case_wide(seed)
+    print(f"case {cfg.name} B{cfg.B} Tq{cfg.Tq} Tk{cfg.Tk} Hq{cfg.Hq} Hk{cfg.Hk} D{cfg.D} {cfg.dtype} "
+          f"{cfg.layout} causal={cfg.is_causal} mask={cfg.mask}/{cfg.mask_heads}/{cfg.keep_prob} "
+          f"score={cfg.score} mode={mode}", flush=True)
+    case = I.make_case(cfg, seed=seed)
+    atomic, ds_limit = MODES[mode]
+    ours = run_ours(case, cfg, atomic=atomic, ds_limit=ds_limit)
+    bars = dict(mean_rel=2.0 ** -7, abs_bar=4e-2, rel_bar=2.0 ** -5) if min(cfg.Tq, cfg.Tk) < 16 else {}
+    check(ours, run_oracle_cpu(case, cfg), label=f"{cfg.name} {mode}", **bars)
     check(ours, run_exact_cpu(case, cfg), label=f"{cfg.name} {mode} vs float64", **bars)

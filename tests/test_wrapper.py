@@ -151,14 +151,15 @@ def test_function_refuses_cpu_tensors():
 
 
 def test_kernel_head_dim_padding_rule():
-    """Head dims the kernels are built for run as they are; others up to 128 run
+    """Head dims the kernels are built for run as they are; others up to 256 run
     at the next built one (zero-padded, exact); larger ones are passed through for
     the library to reject."""
     from tilelang_fa2_4d_mask import fa2
 
-    assert fa2.KERNEL_HEAD_DIMS == (64, 128)
+    assert fa2.KERNEL_HEAD_DIMS == (64, 128, 256)
     assert [fa2.kernel_head_dim(d) for d in (8, 32, 63, 64, 65, 96, 112, 128)] == [64, 64, 64, 64, 128, 128, 128, 128]
-    assert fa2.kernel_head_dim(160) == 160 and fa2.kernel_head_dim(256) == 256
+    assert [fa2.kernel_head_dim(d) for d in (129, 160, 192, 255, 256)] == [256] * 5
+    assert fa2.kernel_head_dim(257) == 257 and fa2.kernel_head_dim(512) == 512
     x = torch.randn(2, 3, 4, 96)
     y = fa2._pad_head_dim(x, 128)
     assert y.shape == (2, 3, 4, 128) and torch.equal(y[..., :96], x) and not y[..., 96:].any()
