@@ -26,8 +26,10 @@ LIB = LIBDIR / "libfa2_4d_mask.so"
 SOURCES = ["fa_fwd.hip", "fa_bwd.hip", "fa_bwd_kv.hip", "fa_bwd_dq.hip", "fa_wide.hip", "fa_mask.hip", "fa_noalloc.hip",
            "fa_api.cpp"]
 # Per-file extra flags.  fa_bwd_kv.hip keeps its dK/dV accumulators in AGPRs
-# through inline asm and wants every other MFMA result in VGPRs (read by VALU).
-EXTRA_FLAGS = {"fa_bwd_kv.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+# through inline asm and wants every other MFMA result in VGPRs (read by
+# VALU); fa_wide.hip keeps its MFMA operands in AGPRs and every MFMA result in
+# VGPRs.
+EXTRA_FLAGS = {"fa_bwd_kv.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"], "fa_wide.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 ARCH = "gfx950"
 
 

@@ -48,6 +48,8 @@ constexpr int kWD = 256;         // head dim of these instances
 constexpr int kWRows = 128;      // forward: query rows per workgroup
 constexpr int kWKeys = 32;       // forward: keys per tile
 constexpr int kWKvKeys = 128;    // dK/dV: keys per workgroup (4 waves x 32), 32-row steps
+constexpr float kWLift = 8.f;    // forward: largest exponent of p against the running maximum
+
 
 template <typename T>
 __device__ __forceinline__ u32x2 pack4w(float x0, float x1, float x2, float x3) {
@@ -65,28 +67,39 @@ __global__ __launch_bounds__(256, 1) void fwd_wide_kernel(const FwdArgs a) {
   using V8 = typename Vec8<T>::type;
   constexpr int D = kWD, DS = D / 16, NB = D / 32, CH = D / 8;
   constexpr int BM = kWRows, BN = kWKeys;
-  // padded row strides (elements): K rows read 16 bytes per lane over 16
-  // rows, V read by 4-row transpose reads
-  constexpr int KS = D + 8, VS = D + 16;
+  // padded row strides (elements): K rows are read 16 bytes per lane over 16
+  // rows (a stride of 4 mod 64 banks), V by 4-row transpose reads of 64
+  // bytes per row (16 mod 64): both conflict-free
+  constexpr int KS = D + 8, VS = D + 32;
   constexpr int KT = BN * KS, VT = BN * VS;
   constexpr int U = BN * CH / 256;      // 16-byte chunks per thread per tile and kind
   constexpr int OS = D + 8;             // epilogue staging stride
   static_assert(4 * 32 * OS <= 2 * (KT + VT), "O staging fits in the tile buffers");
   constexpr bool PREC = MASK || SCORE;
+  // two K buffers, then two V buffers
   __shared__ __attribute__((aligned(16))) T smem[2 * (KT + VT)];
 
-  // (batch, kv-head, [query tile rank, head in group]); longest workgroups
-  // first when causal (query tile nqt-1-rank)
-  const int nblk = a.B * a.Hq * a.nqt;
-  const int W = xcd_remap(blockIdx.x, nblk);
-  const int per_kv = a.G * a.nqt;
-  const int bk = W / per_kv;
-  const int rem = W - bk * per_kv;
-  const int qt_rank = rem / a.G;
-  const int g = rem - qt_rank * a.G;
-  const int b = bk / a.Hk, kvh = bk - b * a.Hk;
-  const int h = kvh * a.G + g;
-  const int qt = a.nqt - 1 - qt_rank;
+  // Causal: query tiles longest first (rank r = tile nqt-1-r), the rank
+  // varying slowest so that every XCD (blocks go round-robin over the 8)
+  // gets an equal share of each length.  Otherwise (equal work) logical
+  // order (batch, kv-head, tile, head in group) contiguous per XCD, so each
+  // XCD's L2 serves few kv-heads' K/V.
+  int b, h, qt;
+  if constexpr (CAUSAL) {
+    const int bh = a.B * a.Hq;
+    const int r = blockIdx.x / bh, i = blockIdx.x - r * bh;
+    b = i / a.Hq;
+    h = i - b * a.Hq;
+    qt = a.nqt - 1 - r;
+  } else {
+    const int W = xcd_remap(blockIdx.x, a.B * a.Hq * a.nqt);
+    const int per_kv = a.G * a.nqt;
+    const int bk = W / per_kv, rem = W - bk * per_kv;
+    qt = rem / a.G;
+    b = bk / a.Hk;
+    h = (bk - b * a.Hk) * a.G + (rem - qt * a.G);
+  }
+  const int kvh = h / a.G;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, hf = lane >> 5;
@@ -104,6 +117,11 @@ __global__ __launch_bounds__(256, 1) void fwd_wide_kernel(const FwdArgs a) {
 #pragma unroll
     for (int ds = 0; ds < DS; ++ds) qf[ds] = as_vec8<T>(gload16(src + ds * 16) ^ neg);
   }
+  // The fragment stays in AGPRs (MFMA reads its operands there too): 64
+  // VGPRs that the pipelined loop needs, which the compiler otherwise shuffles
+  // through AGPRs every iteration.
+#pragma unroll
+  for (int ds = 0; ds < DS; ++ds) asm volatile("" : "+a"(qf[ds]));
   const T* __restrict__ kp = (const T*)a.k + b * a.ksb + kvh * a.ksh;
   const T* __restrict__ vp = (const T*)a.v + b * a.vsb + kvh * a.vsh;
   const uint32_t* mbits = nullptr;
@@ -123,27 +141,64 @@ __global__ __launch_bounds__(256, 1) void fwd_wide_kernel(const FwdArgs a) {
   const int kv_end = CAUSAL ? min(Tk, q0 + BM) : Tk;
   const int nt = (kv_end + BN - 1) / BN;
 
-  // staging: chunk u of thread t is row idx / CH, chunk idx % CH of the tile
-  // (idx = t + 256 u); keys past Tk read key Tk-1
+  // staging: chunk u of thread t is row idx / CH, chunk idx % CH of a tile
+  // (idx = t + 256 u), loaded through a descriptor from the tile's first key
+  // whose records end after key Tk-1 (keys past Tk read zeros: their P is 0),
+  // with loop-invariant lane offsets
   u32x4 kreg[U], vreg[U];
-  auto load_tile = [&](int k0) __attribute__((always_inline)) {
+  uint32_t goff_k[U], goff_v[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int idx = tid + u * 256, r = idx / CH, c = idx % CH;
+    goff_k[u] = (uint32_t)(r * a.kst * 2 + c * 16);
+    goff_v[u] = (uint32_t)(r * a.vst * 2 + c * 16);
+  }
+  auto tile_rs = [&](const T* base, int64_t st, int t) __attribute__((always_inline)) {
+    const int rows = min(Tk - t * BN, BN);
+    const uint32_t nrec = rows > 0 ? (uint32_t)((int64_t)(rows - 1) * st * 2 + 2 * D) : 0u;
+    return __builtin_amdgcn_make_buffer_rsrc((void*)(base + (rows > 0 ? (int64_t)t * BN * st : 0)), (short)0,
+                                             (int)nrec, 0x00020000);
+  };
+  auto load_k = [&](int t) __attribute__((always_inline)) {
+    const auto rs = tile_rs(kp, a.kst, t);
+#pragma unroll
+    for (int u = 0; u < U; ++u) kreg[u] = __builtin_amdgcn_raw_buffer_load_b128(rs, goff_k[u], 0, 0);
+  };
+  auto load_v = [&](int t) __attribute__((always_inline)) {
+    const auto rs = tile_rs(vp, a.vst, t);
+#pragma unroll
+    for (int u = 0; u < U; ++u) vreg[u] = __builtin_amdgcn_raw_buffer_load_b128(rs, goff_v[u], 0, 0);
+  };
+  auto kbuf = [&](int t) __attribute__((always_inline)) { return smem + (t & 1) * KT; };
+  auto vbuf = [&](int t) __attribute__((always_inline)) { return smem + 2 * KT + (t & 1) * VT; };
+  auto store_k = [&](int t) __attribute__((always_inline)) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int idx = tid + u * 256, r = idx / CH, c = idx % CH;
-      const int kk = min(k0 + r, Tk - 1);
-      kreg[u] = gload16(kp + (int64_t)kk * a.kst + c * 8);
-      vreg[u] = gload16(vp + (int64_t)kk * a.vst + c * 8);
+      lds_write16(kbuf(t) + r * KS + c * 8, kreg[u]);
     }
   };
-  auto store_tile = [&](int buf) __attribute__((always_inline)) {
-    T* ks = smem + buf * (KT + VT);
-    T* vs = ks + KT;
+  auto store_v = [&](int t) __attribute__((always_inline)) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int idx = tid + u * 256, r = idx / CH, c = idx % CH;
-      lds_write16(ks + r * KS + c * 8, kreg[u]);
-      lds_write16(vs + r * VS + c * 8, vreg[u]);
+      lds_write16(vbuf(t) + r * VS + c * 8, vreg[u]);
     }
+  };
+  // score of tile t (the initial accumulator of its S chain) and the mask
+  // word of tile t (bit 8 gi + i%4 <-> entry i, after the 4 hf shift)
+  auto score_of = [&](int t, f32x16& sc) __attribute__((always_inline)) {
+#pragma unroll
+    for (int gi = 0; gi < 4; ++gi) {
+      const f32x4 x = __builtin_bit_cast(
+          f32x4, __builtin_amdgcn_raw_buffer_load_b128(srs, soff_row + (uint32_t)(t * BN + gi * 8) * 4, 0, 0));
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sc[gi * 4 + e] = a.qsign < 0.f ? -x[e] : x[e];
+    }
+  };
+  auto mask_of = [&](int t) __attribute__((always_inline)) -> uint32_t {
+    if constexpr (MASK) return mbits[min(t * BN, Tk - 1) >> 5] >> (4 * hf);
+    else return ~0u;
   };
 
   f32x16 oacc[NB];
@@ -155,95 +210,148 @@ __global__ __launch_bounds__(256, 1) void fwd_wide_kernel(const FwdArgs a) {
   const int tr_row = 4 * hf + ((lane >> 2) & 3);
   const int tr_col = ((lane >> 4) & 1) * 16 + (lane & 3) * 4;
 
-  load_tile(0);
-  store_tile(0);
+  // Iteration j (0 .. nt): O += V(j-1)^T P(j-1) with the masking and row
+  // maximum of tile j threaded through it, the rescale when a maximum grows,
+  // then S(j+1) = K(j+1) Q^T with the exp, row sum and packing of P(j)
+  // threaded through it -- one MFMA stream with the softmax VALU work in its
+  // gaps.  Staging: K(j+2) and V(j) are loaded at the start of iteration j
+  // and written at its end (K buffer j%2, last read in iteration j-1 by
+  // S(j); V buffer j%2, last read in iteration j-1 by PV(j-2)), then a
+  // barrier.  Past the tiles (iteration nt, S of tile nt) the work runs on
+  // stale buffers and is discarded: every entry of a tile t >= nt (or wholly
+  // above a causal wave's rows) is dropped, so its P is 0.
+  V8 pk[2], pkl[PREC ? 2 : 1];
+#pragma unroll
+  for (int c = 0; c < 2; ++c) pk[c] = V8{};
+#pragma unroll
+  for (int c = 0; c < (PREC ? 2 : 1); ++c) pkl[c] = V8{};
+  f32x16 sc = f32x16{}, s_cur;
+  uint32_t mw_cur = mask_of(0), mw_nx = mask_of(1);
+  // prologue: K(0), K(1) and a zeroed V buffer 1 (read as V(-1) with P = 0)
+  load_k(0);
+  store_k(0);
+  load_k(1);
+  store_k(1);
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int idx = tid + u * 256, r = idx / CH, c = idx % CH;
+    lds_write16(vbuf(1) + r * VS + c * 8, u32x4{0, 0, 0, 0});
+  }
+  if constexpr (SCORE) score_of(0, sc);
   __syncthreads();
-  for (int j = 0; j < nt; ++j) {
-    const int k0 = j * BN;
-    const bool more = j + 1 < nt;
-    if (more) load_tile(k0 + BN);
-    const T* ks = smem + (j & 1) * (KT + VT);
-    const T* vs = ks + KT;
-    // causal: a tile wholly above the wave's rows adds nothing
-    const bool active = !CAUSAL || k0 <= q0w + 31;
-    if (active) {
-      // lane entry i: key k0 + 8 (i/4) + 4 hf + i%4 of row qrow
-      f32x16 s = f32x16{};
-      if constexpr (SCORE) {
+  {
+    const T* ks = kbuf(0);
+    s_cur = sc;
 #pragma unroll
-        for (int gi = 0; gi < 4; ++gi) {
-          const f32x4 x = __builtin_bit_cast(
-              f32x4, __builtin_amdgcn_raw_buffer_load_b128(srs, soff_row + (uint32_t)(k0 + gi * 8) * 4, 0, 0));
-#pragma unroll
-          for (int t = 0; t < 4; ++t) s[gi * 4 + t] = a.qsign < 0.f ? -x[t] : x[t];
-        }
-      }
-      uint32_t mw = ~0u;
-      if constexpr (MASK) mw = mbits[k0 >> 5] >> (4 * hf);
-#pragma unroll
-      for (int ds = 0; ds < DS; ++ds)
-        s = mfma32(as_vec8<T>(lds_read16(ks + l32 * KS + ds * 16 + hf * 8)), qf[ds], s);
+    for (int ds = 0; ds < DS; ++ds) s_cur = mfma32(as_vec8<T>(lds_read16(ks + l32 * KS + ds * 16 + hf * 8)), qf[ds], s_cur);
+  }
+  if constexpr (SCORE) score_of(1, sc);
 
-      float x[16];
-      const bool edge = MASK || a.zero_scale || (k0 + BN > Tk) || (CAUSAL && k0 + BN - 1 > q0w);
-#pragma unroll
-      for (int i = 0; i < 16; ++i) x[i] = s[i];
+  constexpr int AH = 3;   // LDS operand reads in flight per MFMA stream
+#pragma nounroll
+  for (int j = 0; j <= nt; ++j) {
+    load_k(j + 2);
+    load_v(j);
+    const int k0 = j * BN;
+    // Dropped entries of tile j to -inf (kept ones to 0 with scale 0) on the
+    // tiles that have any: keep word bit 8 gi + e <-> entry 4 gi + e, key
+    // k0 + 8 gi + 4 hf + e (keys below Tk, and up to the row when causal, are
+    // a prefix of the bit positions); no bit past the tiles or for a tile
+    // wholly above a causal wave's rows.
+    {
+      const bool live = j < nt && (!CAUSAL || k0 <= q0w + 31);
+      const bool edge = !live || MASK || a.zero_scale || (k0 + BN > Tk) || (CAUSAL && k0 + BN - 1 > q0w);
       if (edge) {
+        const int lim = CAUSAL ? min(Tk, qrow + 1) : Tk;
+        const int nk = lim - (k0 + 4 * hf);
+        uint32_t keepw = !live || nk <= 0 ? 0u : (nk >= 32 ? ~0u : (1u << nk) - 1u);
+        if constexpr (MASK) keepw &= mw_cur;
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          const int kk = k0 + 8 * (i >> 2) + 4 * hf + (i & 3);
-          bool keep = kk < Tk;
-          if constexpr (CAUSAL) keep = keep && kk <= qrow;
-          if constexpr (MASK) keep = keep && ((mw >> (8 * (i >> 2) + (i & 3))) & 1u);
-          x[i] = keep ? (a.zero_scale ? 0.f : x[i]) : kNegInf;
-        }
-      }
-      float mx = x[0];
-#pragma unroll
-      for (int i = 1; i < 16; ++i) mx = fmaxf(mx, x[i]);
-      const float mt = half_max(mx) * c2;   // the row's largest logit of the tile (scaled)
-      if (wave_any(mt > m_run)) {
-        const float m_new = fmaxf(m_run, mt);
-        const float alpha = m_run == kNegInf ? 0.f : exp2_fast(m_run - m_new);
-        l_run *= alpha;
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) oacc[nb] *= alpha;
-        m_run = m_new;
-      }
-      const float mneg = m_run == kNegInf ? 0.f : -m_run;
-      float p[16], lsum = 0.f;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        p[i] = exp2_fast(fmaf(x[i], c2, mneg));
-        lsum += p[i];
-      }
-      l_run += lsum;
-      // P packed per 16-key step c: slot t <-> key 16 c + 8 (t/4) + 4 hf + t%4
-      V8 pk[2], pkl[PREC ? 2 : 1];
-#pragma unroll
-      for (int c = 0; c < 2; ++c) {
-        pk[c] = pack8<T>(p[8 * c + 0], p[8 * c + 1], p[8 * c + 2], p[8 * c + 3], p[8 * c + 4], p[8 * c + 5],
-                         p[8 * c + 6], p[8 * c + 7]);
-        if constexpr (PREC) {
-          float r[8];
-#pragma unroll
-          for (int t = 0; t < 8; ++t) r[t] = p[8 * c + t] - (float)(T)p[8 * c + t];
-          pkl[c] = pack8<T>(r[0], r[1], r[2], r[3], r[4], r[5], r[6], r[7]);
-        }
-      }
-#pragma unroll
-      for (int c = 0; c < 2; ++c) {
-        const int row = 16 * c + tr_row;
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) {
-          const int col = nb * 32 + tr_col;
-          const V8 av = cat_tr<T>(lds_read_tr(vs + row * VS + col), lds_read_tr(vs + (row + 8) * VS + col));
-          oacc[nb] = mfma32(av, pk[c], oacc[nb]);
-          if constexpr (PREC) oacc[nb] = mfma32(av, pkl[c], oacc[nb]);
+          const bool keep = (keepw >> (8 * (i >> 2) + (i & 3))) & 1u;
+          s_cur[i] = keep ? (a.zero_scale ? 0.f : s_cur[i]) : kNegInf;
         }
       }
     }
-    if (more) store_tile((j + 1) & 1);
+
+    // ---- block 1: PV(j-1) || maximum of tile j --------------------------------------
+    float mx = kNegInf;
+    {
+      const T* vs = vbuf(j - 1);
+      auto rd_v = [&](int t) __attribute__((always_inline)) -> V8 {   // t: c = t / NB, nb = t % NB
+        const int row = 16 * (t / NB) + tr_row, col = (t % NB) * 32 + tr_col;
+        return cat_tr<T>(lds_read_tr(vs + row * VS + col), lds_read_tr(vs + (row + 8) * VS + col));
+      };
+      V8 vq[AH];
+#pragma unroll
+      for (int t = 0; t < AH; ++t) vq[t] = rd_v(t);
+#pragma unroll
+      for (int t = 0; t < 2 * NB; ++t) {
+        const int c = t / NB, nb = t % NB;
+        oacc[nb] = mfma32(vq[t % AH], pk[c], oacc[nb]);
+        if constexpr (PREC) oacc[nb] = mfma32(vq[t % AH], pkl[c], oacc[nb]);
+        if (t + AH < 2 * NB) vq[t % AH] = rd_v(t + AH);
+        mx = fmaxf(mx, s_cur[t]);
+        __builtin_amdgcn_sched_group_barrier(0x008, PREC ? 2 : 1, 0);
+        if (t + AH < 2 * NB) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 1, 0);
+      }
+    }
+    // The running maximum moves only when a row's maximum exceeds it by more
+    // than kWLift (p stays below 2^kWLift meanwhile: O and l are fp32): the
+    // rescale (O in AGPRs, read, scaled and written back) is rare.
+    const float mt = half_max(mx) * c2;   // the row's largest logit of tile j (scaled)
+    if (wave_any(mt > m_run + kWLift)) {
+      const float m_new = fmaxf(m_run, mt);
+      const float alpha = m_run == kNegInf ? 0.f : exp2_fast(m_run - m_new);
+      l_run *= alpha;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) oacc[nb] *= alpha;
+      m_run = m_new;
+    }
+    const float mneg = m_run == kNegInf ? 0.f : -m_run;
+
+    // ---- block 2: S(j+1) || P(j) ---------------------------------------------------
+    {
+      const T* ks = kbuf(j + 1);
+      auto rd_k = [&](int ds) __attribute__((always_inline)) -> u32x4 {
+        return lds_read16(ks + l32 * KS + ds * 16 + hf * 8);
+      };
+      u32x4 kq[AH];
+#pragma unroll
+      for (int t = 0; t < AH; ++t) kq[t] = rd_k(t);
+      f32x16 s_nxt = sc;
+      float p[16], lsum = 0.f;
+#pragma unroll
+      for (int ds = 0; ds < DS; ++ds) {
+        s_nxt = mfma32(as_vec8<T>(kq[ds % AH]), qf[ds], s_nxt);
+        if (ds + AH < DS) kq[ds % AH] = rd_k(ds + AH);
+        p[ds] = exp2_fast(fmaf(s_cur[ds], c2, mneg));
+        lsum += p[ds];
+        if ((ds & 7) == 7) {
+          const int c = ds >> 3;
+          pk[c] = pack8<T>(p[8 * c + 0], p[8 * c + 1], p[8 * c + 2], p[8 * c + 3], p[8 * c + 4], p[8 * c + 5],
+                           p[8 * c + 6], p[8 * c + 7]);
+          if constexpr (PREC) {
+            float r[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) r[e] = p[8 * c + e] - (float)(T)p[8 * c + e];
+            pkl[c] = pack8<T>(r[0], r[1], r[2], r[3], r[4], r[5], r[6], r[7]);
+          }
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+        if (ds + AH < DS) __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
+        __builtin_amdgcn_sched_group_barrier(0x002, PREC ? 5 : 3, 1);
+      }
+      l_run += lsum;
+      s_cur = s_nxt;
+    }
+    // score / mask word of tile j+2 (the S chain above has taken tile j+1's)
+    if constexpr (SCORE) score_of(j + 2, sc);
+    mw_cur = mw_nx;
+    mw_nx = mask_of(j + 2);
+    store_k(j + 2);
+    store_v(j);
     __syncthreads();
   }
 
@@ -334,6 +442,14 @@ __global__ __launch_bounds__(256, 1) void kv_wide_kernel(const BwdArgs a) {
       kf[ds] = as_vec8<T>(gload16(kp + ds * 16));
       if constexpr (DK) vf[ds] = as_vec8<T>(gload16(vp + ds * 16));
     }
+  }
+  // The fragments stay in AGPRs (MFMA reads its operands there too); the
+  // dK or dV accumulator takes 128 VGPRs (results in VGPRs: this file is
+  // built with VGPR-form MFMAs).
+#pragma unroll
+  for (int ds = 0; ds < DS; ++ds) {
+    asm volatile("" : "+a"(kf[ds]));
+    if constexpr (DK) asm volatile("" : "+a"(vf[ds]));
   }
 
   // steps: (head of the group split, 32-row step from qstart), rows above the
