@@ -44,7 +44,7 @@ enum FaStatus {
   FA_OK = 0,
   FA_ERR_NULL = 1,        /* a required pointer is NULL */
   FA_ERR_SHAPE = 2,       /* non-positive size, Hq % Hk != 0, ... */
-  FA_ERR_HEAD_DIM = 3,    /* head_dim not supported by a kernel instance */
+  FA_ERR_HEAD_DIM = 3,    /* head_dim not supported by a kernel instance (64, 128, 256) */
   FA_ERR_DTYPE = 4,       /* dtype not FA_DTYPE_BF16 / FA_DTYPE_FP16 */
   FA_ERR_STRIDE = 5,      /* head-dim stride != 1 or misaligned base */
   FA_ERR_SCALE = 6,       /* scale is NaN or infinite */
