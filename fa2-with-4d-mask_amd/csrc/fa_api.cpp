@@ -437,7 +437,8 @@ static fa::BwdArgs bwd_args(const FaBwdParams* p, int split) {
   a.G = p->heads_q / p->heads_k;
   const int kb = kv_block_keys(p);
   a.nkt = (p->seqlen_k + kb - 1) / kb;
-  a.nqt = (p->seqlen_q + fa::dq_block_rows() - 1) / fa::dq_block_rows();
+  const int dq_rows_rc = p->head_dim > 128 ? fa::dq_wide_block_rows() : fa::dq_block_rows();
+  a.nqt = (p->seqlen_q + dq_rows_rc - 1) / dq_rows_rc;
   a.bk0 = 0;
   a.nbk = p->batch * p->heads_k;
   a.split = split;
@@ -512,6 +513,8 @@ int fa_bwd_finalize(const FaBwdParams* p) {
       a.nqt = (p->seqlen_q + a.dq_rows - 1) / a.dq_rows;
       if (ds_slices(p) == 1 && (st = launch_status(fa::launch_bwd_dq_ds(a, p->head_dim, p->dtype, causal, s), "dq")))
         return st;
+    } else if (p->head_dim > 128) {
+      if ((st = launch_status(fa::launch_bwd_dq_wide(a, p->dtype, causal, s), "dq"))) return st;
     } else {
       if ((st = launch_status(fa::launch_bwd_dq(a, p->head_dim, p->dtype, causal, s), "dq"))) return st;
     }

@@ -193,11 +193,13 @@ hipError_t launch_bwd_dq_ds(const BwdArgs& a, int D, int dtype, bool causal, hip
 hipError_t launch_convert(const CvtArgs& a, int dtype, hipStream_t s);
 // Head dim 256 (fa_wide.hip): forward, 128 query rows per workgroup; dK and
 // dV in two launches over 128-key workgroups (grid nbk x nkt x split, dK/dV
-// written like the dK/dV kernel's: dtype, or fp32 slabs with a split); dQ
-// from launch_bwd_dq.
+// written like the dK/dV kernel's: dtype, or fp32 slabs with a split).
 hipError_t launch_fwd_wide(const FwdArgs& a, int dtype, bool causal, hipStream_t s);
 hipError_t launch_bwd_kv_wide(const BwdArgs& a, int dtype, bool causal, hipStream_t s);
+// dQ recomputed at head dim 256, 128 query rows per workgroup (grid B Hq nqt).
+hipError_t launch_bwd_dq_wide(const BwdArgs& a, int dtype, bool causal, hipStream_t s);
 int fwd_wide_block_rows();
+int dq_wide_block_rows();
 int kv_wide_block_keys();
 // Bool mask -> prepared mask workspace (bits, transposed bits, block states, lists).
 hipError_t launch_mask_prepare(const MaskArgs& a, hipStream_t s);

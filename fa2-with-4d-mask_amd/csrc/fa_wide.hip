@@ -48,6 +48,7 @@ constexpr int kWD = 256;         // head dim of these instances
 constexpr int kWRows = 128;      // forward: query rows per workgroup
 constexpr int kWKeys = 32;       // forward: keys per tile
 constexpr int kWKvKeys = 128;    // dK/dV: keys per workgroup (4 waves x 32), 32-row steps
+constexpr int kWDqRows = 128;    // dQ: query rows per workgroup (4 waves x 32), 32-key tiles
 constexpr float kWLift = 8.f;    // forward: largest exponent of p against the running maximum
 
 
@@ -655,6 +656,323 @@ __global__ __launch_bounds__(256, 1) void kv_wide_kernel(const BwdArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// dQ (recomputed): dQ = scale sum_k dS K, dS = P (dP - Delta)
+// ---------------------------------------------------------------------------
+// Chunk swizzle of the unpadded 512-byte rows of the dQ kernel's K and V
+// tiles: chunk c of row r sits at chunk c ^ swz(r) (low four bits), so that
+// 16 rows read at one chunk (ds_read_b128) and 4 rows x 4 chunks
+// (ds_read_b64_tr_b16) both hit 64 distinct banks.
+__device__ __forceinline__ int swz_w(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
+
+// 16 bytes per lane from a buffer straight into LDS: lane l's bytes land at
+// lds_addr + 16 l (lds_addr wave-uniform).  (A plain device function: inside
+// the kernel template the builtin kept its host-side stub from being emitted.)
+__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t rs, uint32_t lds_addr, uint32_t voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (FA_LDS void*)(uintptr_t)lds_addr, 16, voff, 0, 0, 0);
+}
+
+template <typename T, bool CAUSAL, bool MASK, bool SCORE>
+__global__ __launch_bounds__(256, 1) void dq_wide_kernel(const BwdArgs a) {
+  using V8 = typename Vec8<T>::type;
+  constexpr int D = kWD, DS = D / 16, NB = D / 32, CH = D / 8;
+  constexpr int BM = kWDqRows, BN = kWKeys;
+  constexpr int TILEB = BN * D * 2;       // bytes of one K or V tile (32 rows of 512 bytes)
+  // K tile t is read as rows by S(t) in iteration t-1 and transposed by
+  // dQ(t) in iteration t+1, and written in iteration t-2: four buffers; V tile
+  // t only by dP(t) in iteration t-1: two
+  constexpr int NKB = 4, NVB = 2;
+  constexpr int KOFF = 0, VOFF = NKB * TILEB;
+  constexpr int OS = D + 8;               // epilogue staging stride (elements)
+  static_assert(4 * 32 * OS * 2 <= (NKB + NVB) * TILEB, "dQ staging fits in the tile buffers");
+  constexpr bool PREC = MASK || SCORE;
+  __shared__ __attribute__((aligned(1024))) char smem[(NKB + NVB) * TILEB];
+
+  // blocks as in the forward: causal longest first across all XCDs
+  int b, h, qt;
+  if constexpr (CAUSAL) {
+    const int bh = a.B * a.Hq;
+    const int r = blockIdx.x / bh, i = blockIdx.x - r * bh;
+    b = i / a.Hq;
+    h = i - b * a.Hq;
+    qt = a.nqt - 1 - r;
+  } else {
+    const int W = xcd_remap(blockIdx.x, a.B * a.Hq * a.nqt);
+    const int per_kv = a.G * a.nqt;
+    const int bk = W / per_kv, rem = W - bk * per_kv;
+    qt = rem / a.G;
+    b = bk / a.Hk;
+    h = (bk - b * a.Hk) * a.G + (rem - qt * a.G);
+  }
+  const int kvh = h / a.G;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, hf = lane >> 5;
+  const int Tq = a.Tq, Tk = a.Tk;
+  const int q0 = qt * BM, q0w = q0 + wave * 32, qrow = q0w + l32;
+  const int qrow_c = min(qrow, Tq - 1);
+  const float c2 = a.scale_log2;
+
+  // Q and dO fragments (B of S^T = K Q^T and dP^T = V dO^T), kept in AGPRs;
+  // rows past Tq read row Tq-1 (their LSE is +inf there: P = 0)
+  V8 qf[DS], dof[DS];
+  {
+    const T* qs = (const T*)a.q + b * a.qsb + h * a.qsh + (int64_t)qrow_c * a.qst + hf * 8;
+    const T* ds_ = (const T*)a.dout + b * a.dsb + h * a.dsh + (int64_t)qrow_c * a.dst + hf * 8;
+#pragma unroll
+    for (int ds = 0; ds < DS; ++ds) {
+      qf[ds] = as_vec8<T>(gload16(qs + ds * 16));
+      dof[ds] = as_vec8<T>(gload16(ds_ + ds * 16));
+    }
+  }
+#pragma unroll
+  for (int ds = 0; ds < DS; ++ds) asm volatile("" : "+a"(qf[ds]), "+a"(dof[ds]));
+  const int64_t ri = ((int64_t)b * a.Hq + h) * Tq + qrow_c;
+  const float lse_q = qrow < Tq ? a.lse[ri] : kPosInf;
+  const float ndelta = qrow < Tq ? -a.delta[ri] : 0.f;
+
+  const T* __restrict__ kp = (const T*)a.k + b * a.ksb + kvh * a.ksh;
+  const T* __restrict__ vp = (const T*)a.v + b * a.vsb + kvh * a.vsh;
+  const uint32_t* mbits = nullptr;
+  if constexpr (MASK) {
+    const int pm = mask_plane(a.ml, b, h);
+    mbits = (const uint32_t*)(a.mws + a.ml.bits + pm * a.ml.pbits) + (int64_t)qrow_c * a.ml.wk;
+  }
+  const int srow0 = min(q0 + 32 * __builtin_amdgcn_readfirstlane(wave), Tq - 1);
+  const __amdgpu_buffer_rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc(
+      SCORE ? (void*)(a.score + b * a.ssb + h * a.ssh + (int64_t)srow0 * a.ssq) : nullptr, (short)0,
+      SCORE ? (int)(((int64_t)min(Tq - 1 - srow0, 31) * a.ssq + Tk) * 4) : 0, 0x00020000);
+  const uint32_t soff_row = (uint32_t)((int64_t)(qrow_c - srow0) * a.ssq * 4) + hf * 16;
+
+  const int kv_end = CAUSAL ? min(Tk, q0 + BM) : Tk;
+  const int nt = (kv_end + BN - 1) / BN;
+
+  // ---- staging: direct-to-LDS buffer loads --------------------------------------
+  // Load u (0..3) of wave w writes the 1 KB of tile rows 8 w + 2 u, +1: lane l
+  // lands at physical chunk l % 32 of row 8 w + 2 u + l / 32 and so fetches
+  // logical chunk (l % 32) ^ swz(row); rows past Tk read zeros.
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(FA_LDS char*)smem;
+  uint32_t goff_k[4], goff_v[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int r = 8 * wave + 2 * u + (lane >> 5), c = (lane & 31) ^ swz_w(r);
+    goff_k[u] = (uint32_t)(r * a.kst * 2 + c * 16);
+    goff_v[u] = (uint32_t)(r * a.vst * 2 + c * 16);
+  }
+  auto tile_rs = [&](const T* base, int64_t st, int t) __attribute__((always_inline)) {
+    const int rows = min(Tk - t * BN, BN);
+    const uint32_t nrec = rows > 0 ? (uint32_t)((int64_t)(rows - 1) * st * 2 + 2 * D) : 0u;
+    return __builtin_amdgcn_make_buffer_rsrc((void*)(base + (rows > 0 ? (int64_t)t * BN * st : 0)), (short)0,
+                                             (int)nrec, 0x00020000);
+  };
+  auto load_tiles = [&](int tk, int tv) __attribute__((always_inline)) {   // K(tk), V(tv)
+    const auto rk = tile_rs(kp, a.kst, tk), rv = tile_rs(vp, a.vst, tv);
+    const uint32_t dk = lds0 + KOFF + (tk & (NKB - 1)) * TILEB + 8 * wave * 512;
+    const uint32_t dv = lds0 + VOFF + (tv & (NVB - 1)) * TILEB + 8 * wave * 512;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      lds_dma16(rk, dk + u * 1024, goff_k[u]);
+      lds_dma16(rv, dv + u * 1024, goff_v[u]);
+    }
+  };
+  auto loads_done = [&]() __attribute__((always_inline)) { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); };
+
+  // ---- LDS read addresses ------------------------------------------------------
+  // rows (A of S and dP): row l32, logical chunk 2 ds + hf -> byte
+  // (row_base + 16 ((hf ^ swz(l32)))) ^ (32 ds) (row bases 512-aligned)
+  const uint32_t arow = lds0 + l32 * 512 + 16 * (hf ^ swz_w(l32));
+  // transposed (A of dQ^T = K^T dS^T): rows 16 c + tr_row (+8), columns
+  // 32 nb + tr_col: byte (base + 16 ((tc ^ swz(row)))) ^ (64 nb) + c 8 KB
+  const int tr_row = 4 * hf + ((lane >> 2) & 3);
+  const int tr_col = ((lane >> 4) & 1) * 16 + (lane & 3) * 4;
+  uint32_t atr[2];
+#pragma unroll
+  for (int hi = 0; hi < 2; ++hi) {
+    const int r = tr_row + 8 * hi;
+    atr[hi] = lds0 + r * 512 + 16 * ((tr_col >> 3) ^ swz_w(r)) + (tr_col & 7) * 2;
+  }
+  auto rd_row = [&](uint32_t buf, int ds) __attribute__((always_inline)) -> u32x4 {
+    return *(const FA_LDS u32x4*)(uintptr_t)((arow ^ (uint32_t)(32 * ds)) + buf);
+  };
+  auto rd_tr = [&](uint32_t buf, int c, int nb) __attribute__((always_inline)) -> V8 {
+    const uint32_t o = buf + (uint32_t)(c * 16 * 512);
+    return cat_tr<T>(__builtin_amdgcn_ds_read_tr16_b64_v4i16((FA_LDS s16x4*)(uintptr_t)((atr[0] ^ (uint32_t)(64 * nb)) + o)),
+                     __builtin_amdgcn_ds_read_tr16_b64_v4i16((FA_LDS s16x4*)(uintptr_t)((atr[1] ^ (uint32_t)(64 * nb)) + o)));
+  };
+  auto kbuf = [&](int t) __attribute__((always_inline)) { return (uint32_t)(KOFF + (t & (NKB - 1)) * TILEB); };
+  auto vbuf = [&](int t) __attribute__((always_inline)) { return (uint32_t)(VOFF + (t & (NVB - 1)) * TILEB); };
+
+  auto score_of = [&](int t, f32x16& sc) __attribute__((always_inline)) {
+#pragma unroll
+    for (int gi = 0; gi < 4; ++gi) {
+      const f32x4 x = __builtin_bit_cast(
+          f32x4, __builtin_amdgcn_raw_buffer_load_b128(srs, soff_row + (uint32_t)(t * BN + gi * 8) * 4, 0, 0));
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sc[gi * 4 + e] = x[e];
+    }
+  };
+  auto mask_of = [&](int t) __attribute__((always_inline)) -> uint32_t {
+    if constexpr (MASK) return mbits[min(t * BN, Tk - 1) >> 5] >> (4 * hf);
+    else return ~0u;
+  };
+
+  f32x16 acc[NB];    // dQ^T [32 nb + 8 (i/4) + 4 hf + i%4][q]
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) acc[nb] = f32x16{};
+  f32x16 nd;         // -Delta of the lane's row: initial accumulator of every dP chain
+#pragma unroll
+  for (int i = 0; i < 16; ++i) nd[i] = ndelta;
+  V8 dk_[2], dkl[PREC ? 2 : 1];   // dS(j-1) packed per 16-key step (and its residual)
+#pragma unroll
+  for (int c = 0; c < 2; ++c) dk_[c] = V8{};
+#pragma unroll
+  for (int c = 0; c < (PREC ? 2 : 1); ++c) dkl[c] = V8{};
+  f32x16 sc = f32x16{}, s_cur, dp_cur;
+  uint32_t mw_cur = mask_of(0), mw_nx = mask_of(1);
+
+  // prologue: K(0), V(0), K(1), V(1); K buffer 3 zeroed (read as K(-1) with dS = 0)
+#pragma unroll
+  for (int u = 0; u < TILEB / (256 * 16); ++u)
+    *(FA_LDS u32x4*)(uintptr_t)(lds0 + KOFF + 3 * TILEB + (tid + u * 256) * 16) = u32x4{0, 0, 0, 0};
+  load_tiles(0, 0);
+  load_tiles(1, 1);
+  if constexpr (SCORE) score_of(0, sc);
+  loads_done();
+  __syncthreads();
+  s_cur = sc;
+  dp_cur = nd;
+#pragma unroll
+  for (int ds = 0; ds < DS; ++ds) {
+    s_cur = mfma32(as_vec8<T>(rd_row(kbuf(0), ds)), qf[ds], s_cur);
+    dp_cur = mfma32(as_vec8<T>(rd_row(vbuf(0), ds)), dof[ds], dp_cur);
+  }
+  if constexpr (SCORE) score_of(1, sc);
+
+  constexpr int AH = 3;
+#pragma nounroll
+  for (int j = 0; j <= nt; ++j) {
+    load_tiles(j + 2, j + 2);
+    const int k0 = j * BN;
+    // keep word of tile j (bit 8 gi + e <-> entry 4 gi + e, key k0 + 8 gi + 4 hf
+    // + e): keys below Tk and, causal, up to the row; none past the tiles
+    uint32_t keepw;
+    {
+      const bool live = j < nt && (!CAUSAL || k0 <= q0w + 31);
+      const int lim = CAUSAL ? min(Tk, qrow + 1) : Tk;
+      const int nk = lim - (k0 + 4 * hf);
+      keepw = !live || nk <= 0 ? 0u : (nk >= 32 ? ~0u : (1u << nk) - 1u);
+      if constexpr (MASK) keepw &= mw_cur;
+    }
+    if (a.zero_scale) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) s_cur[i] = 0.f;
+    }
+
+    // ---- block 1: dQ(j-1) || P(j) ----------------------------------------------
+    float p[16];
+    {
+      const uint32_t kb = kbuf(j - 1);
+      V8 kq[AH];
+#pragma unroll
+      for (int t = 0; t < AH; ++t) kq[t] = rd_tr(kb, t / NB, t % NB);
+#pragma unroll
+      for (int t = 0; t < 2 * NB; ++t) {
+        const int c = t / NB, nb = t % NB;
+        acc[nb] = mfma32(kq[t % AH], dk_[c], acc[nb]);
+        if constexpr (PREC) acc[nb] = mfma32(kq[t % AH], dkl[c], acc[nb]);
+        if (t + AH < 2 * NB) kq[t % AH] = rd_tr(kb, (t + AH) / NB, (t + AH) % NB);
+        // P of entry t: selected to 0 when dropped (whatever the exp gives)
+        const float pv = exp2_fast(fmaf(s_cur[t], c2, -lse_q));
+        p[t] = (keepw >> (8 * (t >> 2) + (t & 3))) & 1u ? pv : 0.f;
+        __builtin_amdgcn_sched_group_barrier(0x008, PREC ? 2 : 1, 0);
+        if (t + AH < 2 * NB) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+      }
+    }
+
+    // ---- block 2: S(j+1), dP(j+1) || dS(j) ---------------------------------------
+    {
+      const uint32_t kb = kbuf(j + 1), vb = vbuf(j + 1);
+      u32x4 xk[AH], xv[AH];
+#pragma unroll
+      for (int t = 0; t < AH; ++t) { xk[t] = rd_row(kb, t); xv[t] = rd_row(vb, t); }
+      f32x16 s_nxt = sc, dp_nxt = nd;
+      float dsv[16];
+#pragma unroll
+      for (int ds = 0; ds < DS; ++ds) {
+        s_nxt = mfma32(as_vec8<T>(xk[ds % AH]), qf[ds], s_nxt);
+        dp_nxt = mfma32(as_vec8<T>(xv[ds % AH]), dof[ds], dp_nxt);
+        if (ds + AH < DS) { xk[ds % AH] = rd_row(kb, ds + AH); xv[ds % AH] = rd_row(vb, ds + AH); }
+        dsv[ds] = p[ds] * dp_cur[ds];
+        if ((ds & 7) == 7) {
+          const int c = ds >> 3;
+          if constexpr (PREC) {
+            u32x4 wh, wl;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+              uint32_t h2, l2;
+              split2<T>(dsv[8 * c + 2 * k], dsv[8 * c + 2 * k + 1], &h2, &l2);
+              wh[k] = h2;
+              wl[k] = l2;
+            }
+            dk_[c] = as_vec8<T>(wh);
+            dkl[c] = as_vec8<T>(wl);
+          } else {
+            dk_[c] = pack8<T>(dsv[8 * c + 0], dsv[8 * c + 1], dsv[8 * c + 2], dsv[8 * c + 3], dsv[8 * c + 4],
+                              dsv[8 * c + 5], dsv[8 * c + 6], dsv[8 * c + 7]);
+          }
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 1);
+        if (ds + AH < DS) __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
+        __builtin_amdgcn_sched_group_barrier(0x002, PREC ? 4 : 2, 1);
+      }
+      s_cur = s_nxt;
+      dp_cur = dp_nxt;
+    }
+    if constexpr (SCORE) score_of(j + 2, sc);
+    mw_cur = mw_nx;
+    mw_nx = mask_of(j + 2);
+    loads_done();
+    __syncthreads();
+  }
+
+  // ---- epilogue: dQ = scale acc, through wave-private LDS rows ----------------------
+  const float scale = a.scale;
+  T* os = (T*)smem + wave * 32 * OS;
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+    for (int gi = 0; gi < 4; ++gi)
+      lds_write8(os + l32 * OS + nb * 32 + gi * 8 + hf * 4,
+                 pack4w<T>(acc[nb][gi * 4 + 0] * scale, acc[nb][gi * 4 + 1] * scale, acc[nb][gi * 4 + 2] * scale,
+                           acc[nb][gi * 4 + 3] * scale));
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  constexpr int NU = 32 * CH / 64;
+  u32x4 ov[NU];
+#pragma unroll
+  for (int u = 0; u < NU; ++u) {
+    const int idx = lane + u * 64;
+    ov[u] = lds_read16(os + (idx / CH) * OS + (idx % CH) * 8);
+  }
+  T* dqp = (T*)a.dq + b * a.dqsb + h * a.dqsh;
+#pragma unroll
+  for (int u = 0; u < NU; ++u) {
+    const int idx = lane + u * 64, r = idx / CH, c = idx % CH;
+    if (q0w + r < Tq) gstore16(dqp + (int64_t)(q0w + r) * a.dqst + c * 8, ov[u]);
+  }
+}
+
+template <typename T, bool CAUSAL>
+hipError_t launch_dq_w(const BwdArgs& a, hipStream_t s) {
+  const dim3 grid((unsigned)(a.B * a.Hq * a.nqt)), block(256);
+  const bool m = a.mask != nullptr, sc = a.score != nullptr;
+  if (m && sc) hipLaunchKernelGGL((dq_wide_kernel<T, CAUSAL, true, true>), grid, block, 0, s, a);
+  else if (m) hipLaunchKernelGGL((dq_wide_kernel<T, CAUSAL, true, false>), grid, block, 0, s, a);
+  else if (sc) hipLaunchKernelGGL((dq_wide_kernel<T, CAUSAL, false, true>), grid, block, 0, s, a);
+  else hipLaunchKernelGGL((dq_wide_kernel<T, CAUSAL, false, false>), grid, block, 0, s, a);
+  return hipGetLastError();
+}
+
 template <typename T, bool CAUSAL>
 hipError_t launch_fwd_w(const FwdArgs& a, hipStream_t s) {
   const dim3 grid((unsigned)(a.B * a.Hq * a.nqt)), block(256);
@@ -686,6 +1004,12 @@ hipError_t launch_kv_both(const BwdArgs& a, hipStream_t s) {
 }  // namespace
 
 int fwd_wide_block_rows() { return kWRows; }
+int dq_wide_block_rows() { return kWDqRows; }
+
+hipError_t launch_bwd_dq_wide(const BwdArgs& a, int dtype, bool causal, hipStream_t s) {
+  if (dtype == 0) return causal ? launch_dq_w<bf16, true>(a, s) : launch_dq_w<bf16, false>(a, s);
+  return causal ? launch_dq_w<f16, true>(a, s) : launch_dq_w<f16, false>(a, s);
+}
 int kv_wide_block_keys() { return kWKvKeys; }
 
 hipError_t launch_fwd_wide(const FwdArgs& a, int dtype, bool causal, hipStream_t s) {
