@@ -544,6 +544,7 @@ WIDE_D = [
     C("d256_score_fp16", 1, 160, 224, 4, 2, 256, torch.float16, score="normal"),
     C("d256_mask_score_causal_bshd", 1, 257, 257, 8, 2, 256, layout="bshd", is_causal=True, mask="bernoulli",
       score="normal"),
+    C("d256_causal_tq_lt_tk_mask", 1, 100, 300, 4, 2, 256, is_causal=True, mask="bernoulli", mask_heads=4),
     C("d192_padded", 1, 200, 240, 4, 2, 192),
     C("d160_causal_fp16", 1, 180, 180, 4, 4, 160, torch.float16, is_causal=True),
 ]
