@@ -54,6 +54,7 @@ STRICT = {
     "H": OUTS, "M": OUTS, "H_causal": ("out", "dq"), "P": OUTS, "S": OUTS,
     "H_fp16": OUTS, "H_causal_fp16": OUTS, "P_fp16": OUTS, "S_fp16": OUTS, "M_fp16": OUTS,
     "R_no_causal": OUTS, "R_causal": ("out", "dq"), "R_random_mask": OUTS, "long_keys_mask": OUTS,
+    "W256": OUTS, "W256_causal": ("out", "dq"),
 }
 
 
@@ -140,7 +141,17 @@ CASES = [("H", True), ("H", False), ("H_causal", True), ("H_causal", False),
          ("H_fp16", False), ("H_causal_fp16", False), ("P_fp16", False), ("S_fp16", False), ("M_fp16", False)]
 
 
+# head dim 256 (the reference takes any D, python/fa2.py:33) at a
+# BASELINE-sized shape: the FLOPs of config H's heads at T 4096
+WIDE = {
+    "W256": I.AttnConfig("W256", 1, 4096, 4096, 16, 4, 256, torch.bfloat16),
+    "W256_causal": I.AttnConfig("W256_causal", 1, 4096, 4096, 16, 4, 256, torch.bfloat16, is_causal=True),
+}
+
+
 def _config(name):
+    if name in WIDE:
+        return WIDE[name]
     if name.endswith("_fp16"):
         base = I.CONFIGS[name[: -len("_fp16")]]
         return base.scaled(name=name, dtype=torch.float16)
@@ -152,6 +163,22 @@ def test_fullsize_vs_oracle(cuda, name, atomic):
     cfg = _config(name)
     print(f"case {name} atomic={atomic} B{cfg.B} Tq{cfg.Tq} Tk{cfg.Tk} Hq{cfg.Hq} Hk{cfg.Hk} D{cfg.D} "
           f"{cfg.layout} causal={cfg.is_causal} mask={cfg.mask} score={cfg.score}", flush=True)
+    case = I.make_case(cfg, seed=0, device=cuda)
+    ours = run_ours(case, cfg, atomic=atomic)
+    check(ours, run_oracle(case, cfg), run_rounded(case, cfg), f"{name}/{'atomic' if atomic else 'det'}",
+          STRICT[name])
+
+
+WIDE_CASES = [("W256", True), ("W256", False), ("W256_causal", False)]
+
+
+@pytest.mark.parametrize("name,atomic", WIDE_CASES, ids=[f"{n}-{'atomic' if a else 'det'}" for n, a in WIDE_CASES])
+def test_fullsize_head_dim_256(cuda, name, atomic):
+    """Head dim 256 at a BASELINE-sized shape, against both oracles (both modes
+    run the same deterministic recompute route there)."""
+    cfg = _config(name)
+    print(f"case {name} atomic={atomic} B{cfg.B} T{cfg.Tq} Hq{cfg.Hq} Hk{cfg.Hk} D{cfg.D} causal={cfg.is_causal}",
+          flush=True)
     case = I.make_case(cfg, seed=0, device=cuda)
     ours = run_ours(case, cfg, atomic=atomic)
     check(ours, run_oracle(case, cfg), run_rounded(case, cfg), f"{name}/{'atomic' if atomic else 'det'}",
