@@ -106,7 +106,9 @@ def packed_docs_mask(torch, dev, batch: int, t: int, gen, lo: int = 128, hi: int
 
 def side_configs(torch, dev):
     """The other BASELINE configs as bench lines: P (packed-document mask), S
-    (score + sparse mask), M (MQA, long KV, bshd).  Yields (name, inputs)."""
+    (score + sparse mask), M (MQA, long KV, bshd); then D256, head dim 256 at
+    config H's FLOPs per head pair (not a BASELINE config: the reference takes
+    any head dim, python/fa2.py:33).  Yields (name, inputs)."""
     g = torch.Generator(device="cpu")
     g.manual_seed(0)
 
@@ -135,6 +137,11 @@ def side_configs(torch, dev):
     b, tq, tk, hq, hk, d = 1, 2048, 16384, 32, 1, 64
     yield "M", dict(q=rnd((b, tq, hq, d)), k=rnd((b, tk, hk, d)), v=rnd((b, tk, hk, d)), do=rnd((b, tq, hq, d)),
                     mask=None, score=None, layout="bshd", dims=(b, tq, tk, hq, hk, d))
+    # D256: B1 T4096 Hq16 Hk4 D256, bhsd
+    b, t, hq, hk, d = 1, 4096, 16, 4, 256
+    q, k, v, do = rnd((b, t, hq, d)), rnd((b, t, hk, d)), rnd((b, t, hk, d)), rnd((b, t, hq, d))
+    yield "D256", dict(q=q.transpose(1, 2), k=k.transpose(1, 2), v=v.transpose(1, 2), do=do.transpose(1, 2),
+                       mask=None, score=None, layout="bhsd", dims=(b, t, t, hq, hk, d))
 
 
 def side_bytes(x, mode: str) -> float:
