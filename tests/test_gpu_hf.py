@@ -36,11 +36,11 @@ pytestmark = pytest.mark.gpu
 transformers = pytest.importorskip("transformers")
 
 
-def _model(attn, layers):
+def _model(attn, layers, head_dim=64):
     from transformers import LlamaConfig, LlamaModel
 
     cfg = LlamaConfig(vocab_size=128, hidden_size=256, intermediate_size=512, num_hidden_layers=layers,
-                      num_attention_heads=4, num_key_value_heads=2, head_dim=64, max_position_embeddings=512,
+                      num_attention_heads=4, num_key_value_heads=2, head_dim=head_dim, max_position_embeddings=512,
                       attn_implementation=attn)
     torch.manual_seed(0)
     return LlamaModel(cfg)
@@ -73,19 +73,20 @@ def _register(name, mask_fn, records):
     AttentionMaskInterface.register(name, mask_fn)
 
 
+@pytest.mark.parametrize("head_dim", [64, 256])
 @pytest.mark.parametrize("style", ["sdpa", "eager"])
 @pytest.mark.parametrize("padding", [False, True], ids=["nopad", "leftpad"])
-def test_llama_with_fa2_attention(cuda, style, padding):
+def test_llama_with_fa2_attention(cuda, style, padding, head_dim):
     from transformers.masking_utils import eager_mask, sdpa_mask
 
     name = f"tilelang_fa2_{style}"
     records = []
     _register(name, sdpa_mask if style == "sdpa" else eager_mask, records)
-    print(f"case llama {style} masks, padding={padding}", flush=True)
+    print(f"case llama {style} masks, padding={padding}, head_dim={head_dim}", flush=True)
 
     layers = 1 if padding else 2
-    ours = _model(name, layers).to(device=cuda, dtype=torch.bfloat16)
-    ref = _model("eager", layers)
+    ours = _model(name, layers, head_dim).to(device=cuda, dtype=torch.bfloat16)
+    ref = _model("eager", layers, head_dim)
     ref.load_state_dict({k: v.float().cpu() for k, v in ours.state_dict().items()})
     ref.eval()
     ours.eval()

@@ -75,10 +75,11 @@ def test_torch_compile_fullgraph(cuda):
         assert torch.equal(a, b), name
 
 
+@pytest.mark.parametrize("d", [64, 256])
 @pytest.mark.parametrize("backward", [False, True], ids=["fwd", "fwd_bwd"])
-def test_graph_capture_replays(cuda, backward):
+def test_graph_capture_replays(cuda, backward, d):
     api = _api()
-    q0, k0, v0, do0, mask0, score0 = _inputs(cuda, 2)
+    q0, k0, v0, do0, mask0, score0 = _inputs(cuda, 2, D=d)
     sq, sk, sv, sdo, smask, sscore = (x.clone() for x in (q0, k0, v0, do0, mask0, score0))
     if backward:
         sq, sk, sv = (x.requires_grad_(True) for x in (sq, sk, sv))
@@ -101,12 +102,12 @@ def test_graph_capture_replays(cuda, backward):
     torch.cuda.current_stream().wait_stream(s)
     if backward:
         sq.grad = sk.grad = sv.grad = None
-    print(f"case graph capture backward={backward}", flush=True)
+    print(f"case graph capture backward={backward} D={d}", flush=True)
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
         static_out = step()
     for rep in range(3):
-        q, k, v, do, mask, score = _inputs(cuda, 10 + rep)
+        q, k, v, do, mask, score = _inputs(cuda, 10 + rep, D=d)
         with torch.no_grad():
             for dst, src in ((sq, q), (sk, k), (sv, v), (sdo, do), (smask, mask), (sscore, score)):
                 dst.copy_(src)

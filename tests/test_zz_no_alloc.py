@@ -10,7 +10,8 @@ existing backward entry points on the same inputs:
 * two calls in a row on one GPU, the second on a smaller problem without dead
   rows after a first one with dead rows in every kv-head: the flags the first
   call raised in the shared scratch must not leak into the second (its dV
-  would turn NaN).
+  would turn NaN); then a third at head dim 256 (its own kernels, the same
+  route).
 """
 
 import ctypes
@@ -99,7 +100,8 @@ def test_noalloc_backward_matches_the_workspace_backward(cuda):
     C = I.AttnConfig
     first = C("noalloc_big", 2, 300, 400, 8, 2, 128, is_causal=True, mask="bernoulli", score="normal")
     second = C("noalloc_small", 1, 100, 150, 4, 1, 64, mask="bernoulli")
-    for cfg, dead in ((first, True), (second, False)):
+    third = C("noalloc_d256", 1, 160, 200, 4, 2, 256, is_causal=True, mask="bernoulli", score="normal")
+    for cfg, dead in ((first, True), (second, False), (third, False)):
         ours, ref = _run(cfg, seed=4, dev=cuda, dead_rows=dead)
         for name, a, b, c in zip(("dq", "dk", "dv"), ours, ref["same_route"], ref["default"]):
             assert torch.equal(torch.isnan(a), torch.isnan(b)), (cfg.name, name)
