@@ -260,31 +260,33 @@ def cpu_config_c(seconds: float) -> dict:
 
 
 def cpu_baseline(seconds: float) -> dict:
-    """Eager fp32 oracle (oracle/eager.py) on the host cores, fwd+bwd, on a bounded
-    sample of the headline workload: one kv-head group (Hq=4, Hk=1) at full T;
-    BASELINE configs[0] (C) beside it."""
+    """The fp32 oracle (oracle/eager.py) on the host cores at the whole headline
+    workload (B1 T8192 Hq32 Hk8 D128, non-causal): fwd+bwd by the closed-form
+    chunked gradients (``eager_grads_chunked``: the eager graph's gradients,
+    pinned against autograd in the CPU suite, one [B, Hq, 128, T] slab at a
+    time instead of autograd's saved [B, Hq, T, T] probabilities), the forward
+    by ``eager_ref`` in chunks of 128 query rows; BASELINE configs[0] (C)
+    beside them.  Each runs at least once and repeats until ``seconds`` (the
+    forward ``seconds / 3``) have passed."""
     import torch
 
     from oracle import eager as E
 
-    hq, hk = 4, 1
     g = torch.Generator(device="cpu")
     g.manual_seed(0)
-    q = torch.randn((B, T, hq, D), generator=g).to(torch.bfloat16).transpose(1, 2)
-    k = torch.randn((B, T, hk, D), generator=g).to(torch.bfloat16).transpose(1, 2)
-    v = torch.randn((B, T, hk, D), generator=g).to(torch.bfloat16).transpose(1, 2)
-    do = torch.randn((B, T, hq, D), generator=g).to(torch.bfloat16).transpose(1, 2)
-    flops = 14.0 * B * hq * T * T * D
+    q = torch.randn((B, T, HQ, D), generator=g).to(torch.bfloat16).transpose(1, 2)
+    k = torch.randn((B, T, HK, D), generator=g).to(torch.bfloat16).transpose(1, 2)
+    v = torch.randn((B, T, HK, D), generator=g).to(torch.bfloat16).transpose(1, 2)
+    do = torch.randn((B, T, HQ, D), generator=g).to(torch.bfloat16).transpose(1, 2)
+    flops = 14.0 * B * HQ * T * T * D
     runs, t0 = 0, time.perf_counter()
     while True:
-        E.eager_fwd_bwd(q, k, v, None, None, do, scale=D ** -0.5, is_causal=False, ref_block=128)
+        E.eager_grads_chunked(q, k, v, None, None, do, scale=D ** -0.5, is_causal=False, block=128)
         runs += 1
         el = time.perf_counter() - t0
         if el >= seconds:
             break
     tflops = flops * runs / el * 1e-12
-    # the forward alone (BASELINE.md's CPU plan times the headline forward
-    # too): eager_ref in chunks of 128 query rows, same sample
     fruns, t1 = 0, time.perf_counter()
     with torch.no_grad():
         while True:
@@ -293,7 +295,7 @@ def cpu_baseline(seconds: float) -> dict:
             fel = time.perf_counter() - t1
             if fel >= seconds / 3:
                 break
-    fwd_tflops = 4.0 * B * hq * T * T * D * fruns / fel * 1e-12
+    fwd_tflops = 4.0 * B * HQ * T * T * D * fruns / fel * 1e-12
     try:
         cores = len(os.sched_getaffinity(0))
     except AttributeError:
@@ -303,10 +305,12 @@ def cpu_baseline(seconds: float) -> dict:
         "unit": "TFLOPS",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": (f"oracle eager fp32 fwd+bwd (ref_block=128) at B1 T8192 Hq4 Hk1 D128 non-causal "
-                   f"(1/8 of the headline heads), {runs} run(s) in {el:.1f} s; host affinity {cores} cores"),
-        "fwd": {"value": round(fwd_tflops, 4), "unit": "TFLOPS",
-                "sample": f"oracle eager fp32 forward, same sample, {fruns} run(s) in {fel:.1f} s"},
+        "sample": (f"the whole headline workload (B1 T8192 Hq32 Hk8 D128 bf16 inputs, fp32 maths, non-causal): "
+                   f"oracle fwd+bwd by closed-form chunked gradients (block 128), {runs} run(s) in {el:.1f} s; "
+                   f"host affinity {cores} cores"),
+        "ms_per_step": round(el / runs * 1e3, 1),
+        "fwd": {"value": round(fwd_tflops, 4), "unit": "TFLOPS", "ms": round(fel / fruns * 1e3, 1),
+                "sample": f"oracle eager forward (ref_block 128), same inputs, {fruns} run(s) in {fel:.1f} s"},
         "config_C": cpu_config_c(min(5.0, seconds / 3)),
     }
 
