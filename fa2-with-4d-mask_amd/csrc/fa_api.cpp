@@ -10,6 +10,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <vector>
 
 #include "fa2_4d_mask.h"
 #include "fa_kernels.h"
@@ -105,20 +106,86 @@ int64_t ds_unit_elems(const FaBwdParams* p) {
   const int64_t plane = fa::ds_row(nq32, nk32, p->is_causal != 0);
   return (int64_t)(p->heads_q / p->heads_k) * plane * 1024 * ds_tile_parts(p);   // one unit: the group's planes
 }
+int64_t ds_limit_of(const FaBwdParams* p) { return p->ds_limit_bytes == 0 ? kDsLimitDefault : p->ds_limit_bytes; }
+
+// Row ranges.  Without a mask, when not even one unit's tiles fit the limit,
+// the dS route runs over ranges of query rows instead of groups of units:
+// each range's dK/dV launch covers every unit (the workgroups of the whole
+// problem, each over the range's rows) and adds its partial dK/dV to fp32
+// sums; its dQ launch completes dQ for the range's rows.  Ranges start on
+// 512-row boundaries (whole dQ row blocks); their count is the smallest the
+// limit allows, their tile counts balanced.  (With a mask the per-key-block
+// lists of live steps are not ranged: such problems recompute dQ instead.)
+constexpr int kRangeSteps = 16;
+// bytes of the dS tiles of query steps [lo, hi) over every (batch, head)
+int64_t range_bytes(const FaBwdParams* p, int lo, int hi) {
+  const int64_t nk32 = (p->seqlen_k + 31) / 32;
+  const bool causal = p->is_causal != 0;
+  return (int64_t)p->batch * p->heads_q * (fa::ds_row(hi, nk32, causal) - fa::ds_row(lo, nk32, causal)) * 1024 *
+         ds_tile_parts(p) * 2;
+}
+// Greedy ranges of at most `cap` bytes: their count (-1 if one 512-row
+// chunk exceeds it); step bounds into `bounds` when given.
+int ranges_under(const FaBwdParams* p, int64_t cap, std::vector<int>* bounds) {
+  const int nq32 = (p->seqlen_q + 31) / 32;
+  if (bounds) bounds->assign(1, 0);
+  int n = 0;
+  for (int lo = 0; lo < nq32;) {
+    int hi = lo;
+    while (hi < nq32 && range_bytes(p, lo, std::min(hi + kRangeSteps, nq32)) <= cap) hi = std::min(hi + kRangeSteps, nq32);
+    if (hi == lo) return -1;
+    ++n;
+    if (bounds) bounds->push_back(hi);
+    lo = hi;
+  }
+  return n;
+}
+// Number of row ranges (0: none), step bounds into `bounds` (n + 1 entries).
+int row_ranges(const FaBwdParams* p, std::vector<int>* bounds) {
+  if (p->mask || p->head_dim > 128) return 0;
+  const int64_t limit = ds_limit_of(p);
+  const int64_t unit = ds_unit_elems(p);
+  if (limit < 0 || unit <= 0 || limit / (2 * unit) >= 1) return 0;   // a unit fits: unit slices, or none
+  const int n = ranges_under(p, limit, nullptr);
+  if (n < 2) return 0;   // a 512-row chunk of every unit exceeds the limit: dQ is recomputed
+  // the smallest cap that keeps n ranges balances their tile counts
+  const int64_t total = range_bytes(p, 0, (p->seqlen_q + 31) / 32);
+  int64_t lo = (total + n - 1) / n - 1, hi = limit;   // count(lo) > n (or -1), count(hi) == n
+  while (hi - lo > 1) {
+    const int64_t mid = lo + (hi - lo) / 2;
+    const int c = ranges_under(p, mid, nullptr);
+    if (c > 0 && c <= n) hi = mid;
+    else lo = mid;
+  }
+  return ranges_under(p, hi, bounds);
+}
+
 int64_t ds_slice_units(const FaBwdParams* p) {
   if (p->head_dim > 128) return 0;   // head dim 256: dQ is always recomputed
-  const int64_t limit = p->ds_limit_bytes == 0 ? kDsLimitDefault : p->ds_limit_bytes;
+  const int64_t limit = ds_limit_of(p);
   if (limit < 0) return 0;
   const int64_t units = (int64_t)p->batch * p->heads_k, unit = ds_unit_elems(p);
   if (unit <= 0) return units;
   const int64_t most = std::min(units, limit / (2 * unit));
-  if (most <= 0) return 0;
+  if (most <= 0) return row_ranges(p, nullptr) > 0 ? units : 0;   // row ranges hold every unit
   // as few slices as the limit allows, of (nearly) equal size
   const int64_t slices = (units + most - 1) / most;
   return (units + slices - 1) / slices;
 }
-int64_t ds_elems(const FaBwdParams* p) { return ds_slice_units(p) * ds_unit_elems(p); }
+int64_t ds_elems(const FaBwdParams* p) {
+  std::vector<int> rb;
+  const int nr = row_ranges(p, &rb);
+  if (nr > 0) {
+    int64_t most = 0;
+    for (int r = 0; r < nr; ++r) most = std::max(most, range_bytes(p, rb[r], rb[r + 1]) / 2);
+    return most;
+  }
+  return ds_slice_units(p) * ds_unit_elems(p);
+}
+// launches of the dS route: unit slices, or row ranges
 int ds_slices(const FaBwdParams* p) {
+  const int nr = row_ranges(p, nullptr);
+  if (nr > 0) return nr;
   const int64_t per = ds_slice_units(p);
   return per > 0 ? (int)(((int64_t)p->batch * p->heads_k + per - 1) / per) : 0;
 }
@@ -156,7 +223,7 @@ constexpr int64_t kCus = 256;
 // below that, 2-8 key ranges per block are added with fp32 atomics, more
 // while the grid is below ~1024 workgroups and each range keeps >= 4 steps.
 int dq_split_of(const FaBwdParams* p) {
-  if (route_of(p) != kDsAtomic) return 1;
+  if (route_of(p) != kDsAtomic || row_ranges(p, nullptr) > 0) return 1;   // (row ranges: dQ written per range)
   const int64_t nblk = dq_groups(p, fa::kDqDsRows);
   const int nks = (p->seqlen_k + 31) / 32;
   if (nblk >= kCus || nks < 2) return 1;
@@ -188,6 +255,7 @@ int dq_rows(const FaBwdParams* p) {
 
 int choose_split(const FaBwdParams* p) {
   if (p->kv_split > 0) return p->kv_split;
+  if (row_ranges(p, nullptr) > 0) return 1;   // every unit in each launch; one fp32 sum
   const int G = p->heads_q / p->heads_k;
   const int kb = kv_block_keys(p);
   const int nkt = (p->seqlen_k + kb - 1) / kb;
@@ -362,6 +430,15 @@ static int check_bwd(const FaBwdParams* p, int split) {
     return fail(FA_ERR_WORKSPACE, "kv_split %d needs dk_accum and dv_accum", split);
   if (split > 1 && (!aligned16(p->dk_accum) || !aligned16(p->dv_accum)))
     return fail(FA_ERR_STRIDE, "dk_accum/dv_accum must be 16-byte aligned");
+  if (row_ranges(p, nullptr) > 0) {
+    if (split != 1)
+      return fail(FA_ERR_SHAPE, "kv_split %d: the backward over row ranges (one unit's dS tiles exceed ds_limit_bytes) "
+                  "runs with kv_split 1", split);
+    if (!p->dk_accum || !p->dv_accum)
+      return fail(FA_ERR_WORKSPACE, "the backward over row ranges needs dk_accum and dv_accum (plan.dkv_accum_elems)");
+    if (!aligned16(p->dk_accum) || !aligned16(p->dv_accum))
+      return fail(FA_ERR_STRIDE, "dk_accum/dv_accum must be 16-byte aligned");
+  }
   if (ds_elems(p) > 0 && !p->ds_tiles) return fail(FA_ERR_WORKSPACE, "dQ from dS tiles needs ds_tiles (plan.ds_elems)");
   if (ds_elems(p) > 0 && p->ds_tiles_elems < ds_elems(p))
     return fail(FA_ERR_WORKSPACE, "ds_tiles holds %lld elements, the plan needs %lld (with a mask or a score each "
@@ -389,6 +466,8 @@ int fa_bwd_plan(const FaBwdParams* p, FaBwdPlan* plan) {
   plan->dkv_accum_zeroed = split > 1 && r == kFusedAtomic ? 1 : 0;
   plan->dkv_accum_elems =
       split > 1 ? (int64_t)(r == kFusedAtomic ? 1 : split) * p->batch * p->seqlen_k * p->heads_k * p->head_dim : 0;
+  // row ranges: one fp32 sum each for dK and dV, written by the first range
+  if (row_ranges(p, nullptr) > 0) plan->dkv_accum_elems = (int64_t)p->batch * p->seqlen_k * p->heads_k * p->head_dim;
   plan->ds_elems = ds_elems(p);
   plan->dq_split = dq_split_of(p);
   return FA_OK;
@@ -441,6 +520,9 @@ static fa::BwdArgs bwd_args(const FaBwdParams* p, int split) {
   a.nqt = (p->seqlen_q + dq_rows_rc - 1) / dq_rows_rc;
   a.bk0 = 0;
   a.nbk = p->batch * p->heads_k;
+  a.q32_lo = 0;
+  a.q32_hi = (p->seqlen_q + 31) / 32;
+  a.acc_mode = 0;
   a.split = split;
   a.do_dq = dq_atomics(p) ? 1 : 0;
   a.dq_split = dq_split_of(p);
@@ -476,6 +558,30 @@ int fa_bwd(const FaBwdParams* p) {
   } else if (!a.ds || ds_slices(p) == 1) {
     // pipelined dK/dV (+ dS tiles when the plan has them) here, dQ in fa_bwd_finalize
     if ((st = launch_status(fa::launch_bwd_dkdv2(a, p->head_dim, p->dtype, causal, s), "dkdv"))) return st;
+  } else if (std::vector<int> rb; row_ranges(p, &rb) > 0) {
+    // row ranges: dK/dV of every unit over each range's rows (adding to fp32
+    // sums that the first range writes and the last turns into dK/dV), then
+    // dQ of those rows from the range's tiles (same stream: a range's tiles
+    // are consumed before the next range overwrites them)
+    const int nr = (int)rb.size() - 1;
+    const int64_t nk32 = a.nk32;
+    for (int r = 0; r < nr; ++r) {
+      fa::BwdArgs k = a;
+      k.q32_lo = rb[r];
+      k.q32_hi = rb[r + 1];
+      k.acc_mode = r == 0 ? 1 : (r + 1 == nr ? 3 : 2);
+      k.ds_plane = fa::ds_row(k.q32_hi, nk32, causal) - fa::ds_row(k.q32_lo, nk32, causal);
+      if ((st = launch_status(fa::launch_bwd_dkdv2(k, p->head_dim, p->dtype, causal, s), "dkdv"))) return st;
+      fa::BwdArgs q = k;
+      q.acc_mode = 0;
+      const int rows = std::min(p->seqlen_q, 32 * k.q32_hi) - 32 * k.q32_lo;
+      // 512-row blocks (8 waves sharing each K tile) when they still give every CU one
+      const bool wide = p->head_dim == 128 && !p->score &&
+                        (int64_t)p->batch * p->heads_q * (rows / fa::kDqDsRowsWide) >= kCus;
+      q.dq_rows = wide ? fa::kDqDsRowsWide : fa::kDqDsRows;
+      q.nqt = (rows + q.dq_rows - 1) / q.dq_rows;
+      if ((st = launch_status(fa::launch_bwd_dq_ds(q, p->head_dim, p->dtype, causal, s), "dq"))) return st;
+    }
   } else {
     // the workspace holds a slice of (batch, kv-head) units: dK/dV and then
     // dQ of each slice (same stream, so a slice's tiles are consumed before

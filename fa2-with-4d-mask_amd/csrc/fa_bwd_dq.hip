@@ -100,7 +100,9 @@ __global__ __launch_bounds__(NW * 64, 2) void dq_ds_kernel(const BwdArgs a) {
   const int g = rem - qb_rank * a.G;
   const int b = bk / a.Hk, kvh = bk - b * a.Hk;
   const int h = kvh * a.G + g;
-  const int qb = MASK ? mask_order(a.ml, a.mws, mask_plane(a.ml, b, h), 2)[qb_rank] : nqb - 1 - qb_rank;
+  // (over a range of rows, block 0 of the launch is the range's first)
+  const int qb0 = a.q32_lo / (kDqRows / 32);
+  const int qb = MASK ? mask_order(a.ml, a.mws, mask_plane(a.ml, b, h), 2)[qb_rank] : qb0 + nqb - 1 - qb_rank;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, hf = lane >> 5;
@@ -198,7 +200,7 @@ __global__ __launch_bounds__(NW * 64, 2) void dq_ds_kernel(const BwdArgs a) {
     sd[u] = opaque(lds0 + KTILE + wv * DSW + ch * 512 + ((skey ^ (4 * ch)) & 31) * 16);
   }
   const uint16_t* __restrict__ dsp = (const uint16_t*)a.ds;
-  const int64_t plane = ((int64_t)b * a.Hq + h - (int64_t)a.bk0 * a.G) * a.ds_plane;
+  const int64_t plane = ((int64_t)b * a.Hq + h - (int64_t)a.bk0 * a.G) * a.ds_plane - ds_row(a.q32_lo, nk32, CAUSAL);
   int64_t row0[kDqSteps];
 #pragma unroll
   for (int i = 0; i < kDqSteps; ++i) row0[i] = plane + ds_row(s0 + i, nk32, CAUSAL);

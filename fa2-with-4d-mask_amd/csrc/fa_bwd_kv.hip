@@ -134,8 +134,11 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
   const int gsz = a.G / a.split;
   const int g0 = sp * gsz;
   const int h_first = kvh * a.G + g0, h_end = h_first + gsz;
-  const int qstart = CAUSAL && !MASK ? (kt0 / kStep) * kStep : 0;   // rows above the block are masked
-  const int nst = qstart < Tq ? (Tq - qstart + kStep - 1) / kStep : 0;
+  // rows of this launch: [rlo, rhi) (a range of steps when the backward runs
+  // in row ranges; the lists of a mask are never ranged)
+  const int rlo = a.q32_lo * kStep, rhi = min(Tq, a.q32_hi * kStep);
+  const int qstart = max(CAUSAL && !MASK ? (kt0 / kStep) * kStep : 0, rlo);   // rows above the block are masked
+  const int nst = qstart < rhi ? (rhi - qstart + kStep - 1) / kStep : 0;
   // Causal without a mask walks each head's steps downwards, from the last
   // one (first row qfirst) to the one at the diagonal (qstart): the workgroups
   // of a (batch, kv-head) that run together then read the same Q/dO rows at
@@ -354,7 +357,7 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
       so_d += inc_d;
       so_l += kStep * 4;
     }
-    if (DESC ? ld_qs < qstart : ld_qs >= Tq) {
+    if (DESC ? ld_qs < qstart : ld_qs >= rhi) {
       ++ld_h;
       ld_qs = qfirst;
       so_q = so_q0;
@@ -430,11 +433,12 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
   // pointer: no 64-bit multiply per step).
   const int kb32 = __builtin_amdgcn_readfirstlane(kw0) >> 5;
   const int64_t ds_u0 = (int64_t)a.bk0 * a.G;   // first dS plane (b Hq + h) of the workspace
+  const int64_t ds_r0 = ds_row(a.q32_lo, a.nk32, CAUSAL);   // first tile of the launch's steps in a plane
   const bool ds_on = a.ds != nullptr && kb32 < a.nk32;
   // tile bytes are chunk-major (chunk c of key row k at c 512 + k 16): store t
   // writes chunks 2 t + hf, i.e. one contiguous kilobyte of whole lines
   const uint32_t ds_vo = (uint32_t)(hf * 512 + l32 * 16);
-  const int64_t ds_h0 = ((int64_t)b * a.Hq + it_h - ds_u0) * a.ds_plane + ds_row(qfirst >> 5, a.nk32, CAUSAL) + kb32;
+  const int64_t ds_h0 = ((int64_t)b * a.Hq + it_h - ds_u0) * a.ds_plane + ds_row(qfirst >> 5, a.nk32, CAUSAL) - ds_r0 + kb32;
   const uint16_t* it_ptr = (const uint16_t*)a.ds + ds_h0 * 1024 * NPART;
   auto ds_rs = __builtin_amdgcn_make_buffer_rsrc((void*)a.ds, (short)0, 0, 0x00020000);
   // descriptor of step j's tile, then advance (it_h, it_qs, it_tile) to step j+1
@@ -447,7 +451,7 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
       // block state the dQ kernel reads, without a scalar load
       const bool any = __builtin_amdgcn_ballot_w64(mreg != 0u) != 0;
       const bool ok = ds_on && j < n && (!CAUSAL || kb32 <= s) && any;
-      const int64_t tile = ((int64_t)b * a.Hq + it_h - ds_u0) * a.ds_plane + ds_row(s, a.nk32, CAUSAL) + kb32;
+      const int64_t tile = ((int64_t)b * a.Hq + it_h - ds_u0) * a.ds_plane + ds_row(s, a.nk32, CAUSAL) - ds_r0 + kb32;
       ds_rs = __builtin_amdgcn_make_buffer_rsrc((void*)((uint16_t*)a.ds + tile * 1024 * NPART), (short)0,
                                                 ok ? 2048 * NPART : 0, 0x00020000);
       // step j+1 as the load cursor queued it (padding steps: row 0 of the
@@ -465,7 +469,7 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
       it_qs += kStep;
       it_ptr += (int64_t)(CAUSAL ? min(s + 1, a.nk32) : a.nk32) * 1024 * NPART;
     }
-    if (DESC ? it_qs < qstart : it_qs >= Tq) {
+    if (DESC ? it_qs < qstart : it_qs >= rhi) {
       ++it_h;
       it_qs = qfirst;
       it_ptr = (const uint16_t*)a.ds + (ds_h0 + (int64_t)(it_h - (kvh * a.G + g0)) * a.ds_plane) * 1024 * NPART;
@@ -513,7 +517,7 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
       } else {
         hn = it_h;
         qn = DESC ? it_qs - kStep : it_qs + kStep;
-        if (DESC ? qn < qstart : qn >= Tq) { ++hn; qn = qfirst; }
+        if (DESC ? qn < qstart : qn >= rhi) { ++hn; qn = qfirst; }
       }
     }
     const auto srs_next = score_rs(min(hn, h_end - 1), qn, SCORE && j + 1 < n);
@@ -780,7 +784,7 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
   const bool dead = a.dead[b * a.Hk + kvh] != 0;
   const float nanv = __builtin_nanf("");
   lds_barrier();
-  if (a.split == 1) {
+  if (a.split == 1 && (a.acc_mode == 0 || a.acc_mode == 3)) {
     // stage [key][d] through LDS (wave-private rows), then coalesced 16-byte stores
     T* stg = (T*)smem + wave * 32 * OS;
     auto put = [&](const f32x16 (&acc)[NB], bool nan_out, T* dst, int64_t dstt) __attribute__((always_inline)) {
@@ -809,13 +813,34 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
       }
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     };
+    if (a.acc_mode == 3) {
+      // last row range: the fp32 sums of the earlier ranges join (dK's scaled)
+      if (key < Tk) {
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) dkt[nb] *= scale;
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+          for (int gi = 0; gi < 4; ++gi) {
+            const int64_t o = (((int64_t)b * Tk + key) * a.Hk + kvh) * D + nb * 32 + gi * 8 + hf * 4;
+            const f32x4 k4 = *(const f32x4*)(a.dk_accum + o), v4 = *(const f32x4*)(a.dv_accum + o);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+              dkt[nb][gi * 4 + t] = dkt[nb][gi * 4 + t] * scale + k4[t];
+              dvt[nb][gi * 4 + t] += v4[t];
+            }
+          }
+      }
+    } else {
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) dkt[nb] *= scale;
+    }
     put(dkt, false, (T*)a.dk + b * a.dksb + kvh * a.dksh, a.dkst);
     put(dvt, dead, (T*)a.dv + b * a.dvsb + kvh * a.dvsh, a.dvst);
   } else {
-    // head-group split: fp32 slabs [split][B, Tk, Hk, D], summed in a fixed order later
+    // fp32 slabs [split][B, Tk, Hk, D]: one per head-group split, summed in a
+    // fixed order later; or, over row ranges, the running sums (acc_mode 1
+    // writes them, 2 adds to them, in launch order)
     const int64_t slab = (int64_t)sp * a.B * Tk * a.Hk * D;
+    const bool add = a.acc_mode == 2;
     if (key < Tk) {
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb)
@@ -826,6 +851,10 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
           f32x4 k4, v4;
 #pragma unroll
           for (int t = 0; t < 4; ++t) { k4[t] = dkt[nb][gi * 4 + t] * scale; v4[t] = dead ? nanv : dvt[nb][gi * 4 + t]; }
+          if (add) {
+            k4 += *(const f32x4*)(a.dk_accum + o);
+            v4 += *(const f32x4*)(a.dv_accum + o);
+          }
           *(f32x4*)(a.dk_accum + o) = k4;
           *(f32x4*)(a.dv_accum + o) = v4;
         }

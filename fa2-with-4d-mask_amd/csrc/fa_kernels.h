@@ -142,6 +142,15 @@ struct BwdArgs {
   // when the tiles of all units exceed the workspace; the workspace then
   // holds the planes of the slice, from unit bk0 on.  Others: 0, B Hk.
   int bk0, nbk;
+  // Query steps (32 rows) of this launch: [q32_lo, q32_hi).  The dS-tile
+  // kernels run in ranges of rows when not even one unit's tiles fit the
+  // workspace; its planes then hold the tiles of those steps only, step s at
+  // ds_row(s) - ds_row(q32_lo).  Others: 0, nq32.
+  int q32_lo, q32_hi;
+  // dK/dV kernel over row ranges (split 1): 0 writes dK/dV (the whole row
+  // range in one launch); 1 writes fp32 sums to dk_accum/dv_accum [B, Tk,
+  // Hk, D] (first range), 2 adds to them, 3 adds them and writes dK/dV (last).
+  int acc_mode;
   int nqt;              // query tiles per (b, h) (dQ kernel)
   int dq_rows;          // query rows per dQ-from-dS workgroup: kDqDsRows or kDqDsRowsWide
   int split;            // query-head-group split of the dK/dV kernel

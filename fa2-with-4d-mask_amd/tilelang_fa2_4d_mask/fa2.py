@@ -319,9 +319,10 @@ def _backward_impl(do, q, k, v, O, LSE, mask, score, mask_ws, mst, sst, scale: f
     dead = torch.zeros((B * Hk,), dtype=torch.int32, device=dev)
     dq_acc = torch.empty((B, Tq, Hq, D), dtype=torch.float32, device=dev) if plan.needs_dq_accum else None
     dk_acc = dv_acc = None
-    if plan.kv_split > 1:
+    if plan.dkv_accum_elems > 0:
         # fused atomic kernel: zeroed accumulators; otherwise one fully
-        # overwritten fp32 slab per head-group split.
+        # overwritten fp32 slab per head-group split, or the running sums of
+        # a backward over row ranges.
         alloc = torch.zeros if plan.dkv_accum_zeroed else torch.empty
         dk_acc = alloc((plan.dkv_accum_elems,), dtype=torch.float32, device=dev)
         dv_acc = alloc((plan.dkv_accum_elems,), dtype=torch.float32, device=dev)

@@ -259,7 +259,9 @@ def test_plan_ds_tiles(lib):
     # 5 units would fit: 8 units run as 2 slices of 4 (balanced)
     assert _plan(lib, atomic_dq=0, ds_limit_bytes=(3 << 30) - 1).ds_elems == 4 * unit
     assert _plan(lib, ds_limit_bytes=1 << 29).ds_elems == unit   # atomic mode slices too
-    assert _plan(lib, atomic_dq=0, ds_limit_bytes=(1 << 29) - 2).ds_elems == 0
+    # below one unit: ranges of query rows over every unit (next test); below
+    # one 512-row range of them, or none at all -> dQ recomputed
+    assert _plan(lib, atomic_dq=0, ds_limit_bytes=(1 << 28) - 2).ds_elems == 0
     assert _plan(lib, atomic_dq=0, is_causal=1, ds_limit_bytes=-1).ds_elems == 0
     assert _plan(lib, atomic_dq=0, is_causal=1, ds_limit_bytes=3 << 30).ds_elems > 0
     # with a mask or a score every stored block is a pair of tiles (dS and
@@ -269,6 +271,45 @@ def test_plan_ds_tiles(lib):
         assert _plan(lib, atomic_dq=0, ds_limit_bytes=1 << 30, **side).ds_elems == 2 * unit
         # the default 4 GiB holds half of them: two slices of four units
         assert _plan(lib, **side).ds_elems == 4 * 2 * unit
+
+
+def test_plan_row_ranges(lib):
+    """Without a mask, a limit below one (batch, kv-head) unit's tiles runs
+    the dS kernels over ranges of query rows, every unit in each launch:
+    512-row chunks (16 steps), as few ranges as the limit allows, balanced;
+    head-group split 1, one fp32 sum each for dK and dV, dQ written per range
+    (no fp32 atomics, in atomic mode too)."""
+    chunk = 32 * 16 * 256 * 1024   # tiles of 512 rows x 8192 keys over the 32 heads (256 MiB)
+    for atomic in (0, 1):
+        plan = _plan(lib, atomic_dq=atomic, ds_limit_bytes=(1 << 29) - 2)   # 1 chunk fits: 16 ranges
+        assert plan.ds_elems == chunk and plan.kv_split == 1 and plan.dq_split == 1
+        assert plan.needs_dq_accum == 0 and plan.dq_accum_elems == 0
+        assert plan.dkv_accum_elems == 8192 * 8 * 128 and plan.dkv_accum_zeroed == 0
+    # MQA (Hk 1: one unit is all 16 chunks): 9 chunks fit, two ranges of 8 (not 9 + 7)
+    assert _plan(lib, atomic_dq=0, heads_k=1, ds_limit_bytes=9 * chunk * 2).ds_elems == 8 * chunk
+    # causal (one unit: 269 MB; the last 512-row chunk of every head: 260 MB):
+    # ranges balanced by tile count (later rows hold more tiles), the largest
+    # within the limit; below the last chunk, dQ recomputed
+    for limit in (1 << 28, 265_000_000):
+        plan = _plan(lib, atomic_dq=0, is_causal=1, ds_limit_bytes=limit)
+        assert 0 < 2 * plan.ds_elems <= limit and plan.kv_split == 1, limit
+        assert plan.dkv_accum_elems == 8192 * 8 * 128, limit
+    assert _plan(lib, atomic_dq=0, is_causal=1, ds_limit_bytes=250_000_000).ds_elems == 0
+    # T 32768 under the default 4 GiB: one unit is 8 GiB, 4 chunks of 1 GiB fit
+    long = dict(seqlen_q=32768, seqlen_k=32768)
+    plan = _plan(lib, atomic_dq=0, **long)
+    assert plan.ds_elems == 4 * 32 * 16 * 1024 * 1024 and plan.kv_split == 1
+    # a mask keeps the recompute route below one unit; so does head dim 256
+    assert _plan(lib, atomic_dq=0, ds_limit_bytes=(1 << 29) - 2, mask=FAKE).ds_elems == 0
+    assert _plan(lib, atomic_dq=0, **long, mask=FAKE).ds_elems == 0
+    # the row ranges need the fp32 sums and head-group split 1
+    p = bwd_params(atomic_dq=0, ds_limit_bytes=(1 << 29) - 2, ds_tiles=FAKE, ds_tiles_elems=chunk)
+    assert lib.fa_bwd(ctypes.byref(p)) == 8
+    assert "needs dk_accum and dv_accum" in lib.fa_last_error().decode()
+    p = bwd_params(atomic_dq=0, ds_limit_bytes=(1 << 29) - 2, ds_tiles=FAKE, ds_tiles_elems=chunk, kv_split=2,
+                   dk_accum=FAKE, dv_accum=FAKE)
+    assert lib.fa_bwd(ctypes.byref(p)) == 2
+    assert "runs with kv_split 1" in lib.fa_last_error().decode()
 
 
 def test_det_path_needs_ds_tiles(lib):

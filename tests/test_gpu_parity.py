@@ -17,6 +17,7 @@ Tolerances (bf16/fp16, every output O, dQ, dK, dV):
     row's dQ must be exactly 0.
 """
 
+import ctypes
 import math
 
 import pytest
@@ -44,15 +45,27 @@ def _one_unit_limit(cfg):
     return 2 * (cfg.Hq // cfg.Hk) * plane * 1024
 
 
+def _rows_limit(cfg):
+    """dS workspace bytes of the largest 512-row range of every (batch, head)
+    plane: below one unit (Tq > 512 B Hk) the backward then runs one range of
+    query rows per launch pair; otherwise it slices by units."""
+    nq, nk = -(-cfg.Tq // 32), -(-cfg.Tk // 32)
+    parts = 2 if (cfg.mask is not None or cfg.score is not None) else 1
+    tiles = [min(s + 1, nk) if cfg.is_causal else nk for s in range(nq)]
+    best = max(sum(tiles[c:c + 16]) for c in range(0, nq, 16))
+    return 2 * parts * cfg.B * cfg.Hq * best * 1024
+
+
 def run_ours(case, cfg, *, atomic=True, scale=None, attention_mask=None, backward=True, ds_limit=0):
     """ds_limit: dS workspace limit of the backward (0 = default, dQ from the
     stored dS tiles; -1 = no workspace: dQ recomputed (deterministic) or fused
     fp32 atomics; "unit" = one (batch, kv-head) unit: the dS kernels run once
-    per unit)."""
+    per unit; "rows" = one 512-row range of every unit, see _rows_limit)."""
     api = _api()
     import tilelang_fa2_4d_mask.fa2 as fa2mod
 
-    fa2mod.DS_LIMIT_BYTES = _one_unit_limit(cfg) if ds_limit == "unit" else ds_limit
+    fa2mod.DS_LIMIT_BYTES = {"unit": _one_unit_limit, "rows": _rows_limit}[ds_limit](cfg) if isinstance(
+        ds_limit, str) else ds_limit
     dev = torch.device("cuda:0")
     q = case["q"].to(dev).detach().requires_grad_(backward)
     k = case["k"].to(dev).detach().requires_grad_(backward)
@@ -162,9 +175,12 @@ SMALL = [
 # fp32-atomic dQ fused into the dK/dV kernel (no dS workspace); deterministic
 # with dQ from the stored dS tiles; deterministic with dQ recomputed (no dS
 # workspace allowed); both dS modes with a workspace of one (batch, kv-head)
-# unit, so that the dS kernels run slice by slice
+# unit, so that the dS kernels run slice by slice; both with a workspace of
+# one 512-row range of every unit (ranges of rows where Tq > 512 B Hk without
+# a mask; unit slices or recompute otherwise)
 MODES = {"atomic": (True, 0), "atomic_fused": (True, -1), "det_ds": (False, 0), "det_recompute": (False, -1),
-         "atomic_sliced": (True, "unit"), "det_sliced": (False, "unit")}
+         "atomic_sliced": (True, "unit"), "det_sliced": (False, "unit"),
+         "atomic_rows": (True, "rows"), "det_rows": (False, "rows")}
 
 
 @pytest.mark.parametrize("mode", list(MODES))
@@ -198,6 +214,52 @@ def test_wide_dq_vs_oracle(cuda, cfg, mode):
     ours = run_ours(case, cfg, atomic=atomic, ds_limit=ds_limit)
     ref = run_oracle_cpu(case, cfg)
     check(ours, ref, label=f"{cfg.name}/{mode}")
+
+
+# The backward over ranges of query rows (Tq > 512 B Hk, no mask, head dim
+# <= 128): 2-5 ranges, so the dK/dV sums are written, added to and finished;
+# MQA and GQA, causal with Tq > Tk, a score (dS tile pairs), fp16 bshd, head
+# dim 64.
+ROWS = [
+    C("rows_mqa", 1, 1500, 1100, 4, 1, 128),
+    C("rows_mqa_causal", 1, 1500, 1100, 4, 1, 128, is_causal=True),
+    C("rows_gqa_ragged", 1, 2100, 600, 4, 2, 128),
+    C("rows_score_d64", 1, 1100, 700, 2, 1, 64, score="normal"),
+    C("rows_fp16_bshd_causal", 1, 1200, 1000, 8, 1, 128, torch.float16, layout="bshd", is_causal=True),
+]
+
+
+def _plan_of(cfg, limit, atomic):
+    from tilelang_fa2_4d_mask import _ext
+
+    p = _ext.FaBwdParams()
+    p.batch, p.seqlen_q, p.seqlen_k, p.heads_q, p.heads_k, p.head_dim = cfg.B, cfg.Tq, cfg.Tk, cfg.Hq, cfg.Hk, cfg.D
+    p.scale, p.is_causal, p.atomic_dq, p.dtype = cfg.D ** -0.5, int(cfg.is_causal), int(atomic), 0
+    p.ds_limit_bytes = limit
+    p.score = 16 if cfg.score is not None else None
+    plan = _ext.FaBwdPlan()
+    lib = _ext.load_library()
+    assert lib.fa_bwd_plan(ctypes.byref(p), ctypes.byref(plan)) == 0
+    return plan
+
+
+@pytest.mark.parametrize("mode", ["det_rows", "atomic_rows"])
+@pytest.mark.parametrize("cfg", ROWS, ids=[c.name for c in ROWS])
+def test_row_ranges_vs_oracle(cuda, cfg, mode):
+    atomic, ds_limit = MODES[mode]
+    plan = _plan_of(cfg, _rows_limit(cfg), atomic)
+    # the route really is the ranged one: dS tiles, split 1, the fp32 sums, no dQ atomics
+    assert plan.ds_elems > 0 and plan.kv_split == 1 and plan.dkv_accum_elems == cfg.B * cfg.Tk * cfg.Hk * cfg.D
+    assert plan.needs_dq_accum == 0
+    case = I.make_case(cfg, seed=7)
+    print(f"case {cfg.name} mode={mode}", flush=True)
+    ours = run_ours(case, cfg, atomic=atomic, ds_limit=ds_limit)
+    ref = run_oracle_cpu(case, cfg)
+    check(ours, ref, label=f"{cfg.name}/{mode}")
+    # dQ of a row comes from the same dS tiles in the same key order as the
+    # unranged launch: bitwise equal to it
+    one = run_ours(case, cfg, atomic=False, ds_limit=0)
+    assert torch.equal(ours["dq"], one["dq"]) and torch.equal(ours["out"], one["out"])
 
 
 @pytest.mark.parametrize("mode", ["atomic", "det_ds"])
@@ -240,6 +302,7 @@ SCORE_DEAD = [
     C("score_dead_mask_causal", 1, 320, 320, 4, 2, 128, is_causal=True, mask="bernoulli", score="normal"),
     C("score_dead_nomask", 2, 256, 200, 4, 2, 128, score="normal"),
     C("score_dead_nomask_causal", 1, 300, 300, 4, 1, 64, is_causal=True, score="normal"),
+    C("score_dead_rows", 1, 1100, 700, 4, 1, 64, score="normal"),   # ranges of rows in the *_rows modes
 ]
 
 
