@@ -108,14 +108,18 @@ int64_t ds_unit_elems(const FaBwdParams* p) {
 }
 int64_t ds_limit_of(const FaBwdParams* p) { return p->ds_limit_bytes == 0 ? kDsLimitDefault : p->ds_limit_bytes; }
 
-// Row ranges.  Without a mask, when not even one unit's tiles fit the limit,
-// the dS route runs over ranges of query rows instead of groups of units:
-// each range's dK/dV launch covers every unit (the workgroups of the whole
-// problem, each over the range's rows) and adds its partial dK/dV to fp32
-// sums; its dQ launch completes dQ for the range's rows.  Ranges start on
-// 512-row boundaries (whole dQ row blocks); their count is the smallest the
-// limit allows, their tile counts balanced.  (With a mask the per-key-block
-// lists of live steps are not ranged: such problems recompute dQ instead.)
+// Row ranges.  Without a mask the dS route can run over ranges of query rows
+// instead of groups of units: each range's dK/dV launch covers every unit
+// (the workgroups of the whole problem, each over the range's rows) and adds
+// its partial dK/dV to fp32 sums; its dQ launch completes dQ for the range's
+// rows.  Ranges start on 512-row boundaries (whole dQ row blocks); their
+// count is the smallest the limit allows, their tile counts balanced.  Used
+// when the tiles exceed the limit and either not even one unit fits it, or
+// the problem is causal (unit slices of a causal problem split each head
+// group to balance their workgroups, through fp32 slabs: measured 5-25 %
+// slower than ranges at 0.5-4 GiB; non-causal unit slices ran 1-3 % faster
+// than ranges).  With a mask the per-key-block lists of live steps are not
+// ranged: below one unit such problems recompute dQ.
 constexpr int kRangeSteps = 16;
 // bytes of the dS tiles of query steps [lo, hi) over every (batch, head)
 int64_t range_bytes(const FaBwdParams* p, int lo, int hi) {
@@ -145,11 +149,13 @@ int row_ranges(const FaBwdParams* p, std::vector<int>* bounds) {
   if (p->mask || p->head_dim > 128) return 0;
   const int64_t limit = ds_limit_of(p);
   const int64_t unit = ds_unit_elems(p);
-  if (limit < 0 || unit <= 0 || limit / (2 * unit) >= 1) return 0;   // a unit fits: unit slices, or none
+  if (limit < 0 || unit <= 0) return 0;
+  const int64_t total = range_bytes(p, 0, (p->seqlen_q + 31) / 32);
+  if (total <= limit) return 0;                                           // one launch
+  if (!p->is_causal && limit / (2 * unit) >= 1) return 0;                 // unit slices
   const int n = ranges_under(p, limit, nullptr);
   if (n < 2) return 0;   // a 512-row chunk of every unit exceeds the limit: dQ is recomputed
   // the smallest cap that keeps n ranges balances their tile counts
-  const int64_t total = range_bytes(p, 0, (p->seqlen_q + 31) / 32);
   int64_t lo = (total + n - 1) / n - 1, hi = limit;   // count(lo) > n (or -1), count(hi) == n
   while (hi - lo > 1) {
     const int64_t mid = lo + (hi - lo) / 2;
@@ -166,8 +172,9 @@ int64_t ds_slice_units(const FaBwdParams* p) {
   if (limit < 0) return 0;
   const int64_t units = (int64_t)p->batch * p->heads_k, unit = ds_unit_elems(p);
   if (unit <= 0) return units;
+  if (row_ranges(p, nullptr) > 0) return units;   // row ranges hold every unit
   const int64_t most = std::min(units, limit / (2 * unit));
-  if (most <= 0) return row_ranges(p, nullptr) > 0 ? units : 0;   // row ranges hold every unit
+  if (most <= 0) return 0;
   // as few slices as the limit allows, of (nearly) equal size
   const int64_t slices = (units + most - 1) / most;
   return (units + slices - 1) / slices;

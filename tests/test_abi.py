@@ -295,6 +295,15 @@ def test_plan_row_ranges(lib):
         assert 0 < 2 * plan.ds_elems <= limit and plan.kv_split == 1, limit
         assert plan.dkv_accum_elems == 8192 * 8 * 128, limit
     assert _plan(lib, atomic_dq=0, is_causal=1, ds_limit_bytes=250_000_000).ds_elems == 0
+    # causal problems take ranges whenever they slice at all (unit slices would
+    # split each head group through fp32 slabs): 2.2 GB of tiles under 1 GiB
+    for atomic in (0, 1):
+        plan = _plan(lib, atomic_dq=atomic, is_causal=1, ds_limit_bytes=1 << 30)
+        assert 0 < 2 * plan.ds_elems <= 1 << 30 and plan.kv_split == 1 and plan.dq_split == 1
+        assert plan.dkv_accum_elems == 8192 * 8 * 128
+    # ... but not when every tile fits (the headline's causal 2.2 GB under the default)
+    plan = _plan(lib, atomic_dq=0, is_causal=1)
+    assert plan.ds_elems == 32 * (256 * 257 // 2) * 1024 and plan.dkv_accum_elems == 0
     # T 32768 under the default 4 GiB: one unit is 8 GiB, 4 chunks of 1 GiB fit
     long = dict(seqlen_q=32768, seqlen_k=32768)
     plan = _plan(lib, atomic_dq=0, **long)

@@ -1,21 +1,26 @@
-"""The backward over slices of (batch, kv-head) units at a long sequence.
+"""The sliced backward at long sequences.
 
 At T = 16384 with the headline's heads (B1 Hq32 Hk8 D128) the dS tiles of all
-units (17 GB, 8.6 GB causal) exceed the default 4 GiB workspace, so the
-backward runs the dK/dV and dQ kernels once per slice of units
-(csrc/fa_api.cpp ``ds_slice_units``).  The same call with a limit that holds
-every unit runs them once.  Checks:
+units (17 GB, 8.6 GB causal) exceed the default 4 GiB workspace.  The
+non-causal backward then runs the dK/dV and dQ kernels once per slice of
+(batch, kv-head) units (csrc/fa_api.cpp ``ds_slice_units``); the causal one
+once per range of query rows over every unit (``row_ranges``: dK/dV added to
+fp32 sums across the ranges).  The same call with a limit that holds every
+unit runs them once.  Checks:
 
 * non-causal, deterministic: the sliced and the single-launch gradients are
   bitwise equal (the same workgroups do the same arithmetic; only the launch
   they belong to differs);
-* causal, deterministic: sliced launches split each head group in two (fp32
-  dK/dV slabs summed in a fixed order), so dK and dV may round to the
-  neighbouring bf16 value (0.07 % of the entries at this size); dQ is
-  bitwise equal, dK/dV within one bf16 step of the single launch (slicing
-  alone, at an equal split, is bitwise exact);
+* causal, deterministic: dQ is bitwise equal (the same dS tiles, summed in
+  the same key order); dK and dV are sums over the ranges in fp32 and may
+  round to the neighbouring bf16 value: within one bf16 step of the single
+  launch;
 * atomic mode, non-causal: sliced and single-launch dQ agree within fp32
   summation order (dK/dV bitwise).
+
+At T = 32768 one unit's tiles (8 GiB) exceed the default limit: both modes
+run over row ranges there (16 ranges of 2048 rows non-causal), checked
+against the single launch (an 80 GiB limit: 64 GiB of tiles, 34 GB causal).
 
 The route, the slices and the head-group split depend on the problem and the
 limit only (the default limit is a constant): the deterministic backward is
@@ -69,6 +74,28 @@ def test_sliced_backward_matches_single_launch(cuda, causal, atomic):
             assert (diff <= step).all(), f"{name}: max diff {diff.max().item():.3e}"
         del a, b
     del sliced, single
+    torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("causal", [False, True], ids=["noncausal", "causal"])
+def test_row_ranges_match_single_launch_at_32k(cuda, causal):
+    T = 32768
+    g = torch.Generator().manual_seed(13)
+    q, k, v, do = (torch.randn(1, T, h, 128, generator=g).to(torch.bfloat16).to(cuda).transpose(1, 2)
+                   for h in (32, 8, 8, 32))
+    print(f"case T={T} causal={causal}: row ranges (default limit) vs one launch (80 GiB)", flush=True)
+    ranged = _grads(q, k, v, do, causal=causal, atomic=False, limit=0)
+    single = _grads(q, k, v, do, causal=causal, atomic=False, limit=80 << 30)
+    for name, a, b in zip(("dq", "dk", "dv"), ranged, single):
+        assert torch.isfinite(a).all(), name
+        if name == "dq":
+            assert torch.equal(a, b), name
+        else:
+            bf = b.float()
+            step = bf.abs() * 2.0 ** -7 + 1e-5 * bf.abs().max()
+            diff = (a.float() - bf).abs()
+            assert (diff <= step).all(), f"{name}: max diff {diff.max().item():.3e}"
+    del ranged, single
     torch.cuda.empty_cache()
 
 
