@@ -19,7 +19,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must be loaded before the HIP library, see above)
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libfa2_4d_mask.so"
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 FA_DTYPE_BF16 = 0
 FA_DTYPE_FP16 = 1

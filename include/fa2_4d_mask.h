@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define FA_ABI_VERSION 5
+#define FA_ABI_VERSION 6
 
 enum FaDtype { FA_DTYPE_BF16 = 0, FA_DTYPE_FP16 = 1 };
 
@@ -91,7 +91,8 @@ typedef struct FaBwdParams {
   int32_t* dead_flags;           /* workspace [B * Hk] int32, zeroed by the caller */
   const uint8_t* mask; const float* score;
   float* dq_accum;               /* workspace [B, Hq, Tq, D] fp32 contiguous, head-major (atomic dQ) */
-  float* dk_accum;               /* workspace of plan.dkv_accum_elems fp32, only when plan.kv_split > 1 */
+  float* dk_accum;               /* workspace of plan.dkv_accum_elems fp32, when that is > 0 (head-group
+                                    split slabs, or the running sums over ranges of query rows) */
   float* dv_accum;               /* idem */
   void* dq; void* dk; void* dv;  /* outputs, dtype, strided like q/k/v */
   int64_t q_stride_b, q_stride_t, q_stride_h;
@@ -113,7 +114,8 @@ typedef struct FaBwdParams {
   void* stream;
   void* ds_tiles;                /* workspace of plan.ds_elems 16-bit values (deterministic path), else unused */
   int64_t ds_limit_bytes;        /* largest dS workspace the caller accepts; 0 = 4 GiB, < 0 = none
-                                    (below the whole need: the backward runs in slices of units) */
+                                    (below the whole need: the backward runs in slices of units, or
+                                    in ranges of query rows; see FaBwdPlan.ds_elems) */
   const void* mask_ws;           /* prepared mask, as for fa_fwd; required with a mask */
   const void* o_lo;              /* optional: the o_lo fa_fwd wrote; Delta = sum_d dO (O + o_lo) */
   int64_t o_lo_stride_b, o_lo_stride_t, o_lo_stride_h;
@@ -139,17 +141,25 @@ typedef struct FaMaskParams {
 
 /* What fa_bwd will do for a problem, so the caller can size workspaces. */
 typedef struct FaBwdPlan {
-  int32_t kv_split;              /* >1: dK/dV accumulate in fp32 dk_accum/dv_accum (zeroed) */
+  int32_t kv_split;              /* >1: dK/dV of each head-group part go to fp32 dk_accum/dv_accum slabs,
+                                    summed by fa_bwd_finalize */
   int32_t needs_dq_accum;        /* 1 if dq_accum is used: dQ added with fp32 atomics (atomic_dq = 1 and
                                     dq_split > 1, or the fused kernel); else dQ is written directly */
   int64_t dq_accum_elems;        /* B*Tq*Hq*D when used, else 0 */
-  int64_t dkv_accum_elems;       /* B*Tk*Hk*D when kv_split > 1, else 0 */
-  int64_t ds_elems;              /* size of ds_tiles (16-bit dS of every stored 32x32 block of a slice of
-                                    (batch, kv-head) units: all units when they fit ds_limit_bytes, else
-                                    as many as fit, in nearly equal slices that fa_bwd runs one after the
-                                    other); 0 when not even one unit fits: dQ is then recomputed
-                                    (atomic_dq = 0, or with a mask or a score) or added per key block by
-                                    the fused dK/dV kernel (atomic_dq = 1 without mask and score) */
+  int64_t dkv_accum_elems;       /* kv_split > 1: B*Tk*Hk*D per slab (kv_split slabs; one for the fused
+                                    kernel); ranges of query rows (ds_elems): B*Tk*Hk*D, the running
+                                    sums, written by the first range; else 0 */
+  int64_t ds_elems;              /* size of ds_tiles: 16-bit dS of every stored 32x32 block of all
+                                    (batch, kv-head) units when they fit ds_limit_bytes; else of a slice
+                                    of as many units as fit (nearly equal slices, run one after the
+                                    other); else, without a mask, of the largest range of query rows
+                                    (512-row multiples, every unit; fa_bwd runs the ranges one after
+                                    the other and sums dK/dV across them in dk_accum/dv_accum) -- causal
+                                    problems without a mask take the ranges whenever they do not fit
+                                    at once.  0 when not even one unit, nor one 512-row range, fits:
+                                    dQ is then recomputed (atomic_dq = 0, or with a mask or a score) or
+                                    added per key block by the fused dK/dV kernel (atomic_dq = 1 without
+                                    mask and score) */
   int32_t dkv_accum_zeroed;      /* 1: dk_accum/dv_accum must be zeroed by the caller (fused atomic kernel) */
   int32_t dq_split;              /* atomic_dq = 1 with dS tiles: key ranges whose dQ partials are added
                                     (2-8) when the 256-row query blocks are fewer than the CUs; 1: each
