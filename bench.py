@@ -25,7 +25,10 @@ allocates beyond what is live before it (throughput_check.py:218-243);
 4 GiB, unless ``--ds-limit`` sets one).  ``breakdown`` also times the headline
 fwd and fwd+bwd replayed from a captured HIP graph (the reference's
 ``--cudagraph`` mode, benchmark/throughput_check.py:249-250): the same kernels
-without the host work of the Python and autograd layers between launches.
+without the host work of the Python and autograd layers between launches;
+and the deterministic fwd+bwd under a 1 GiB dS workspace (``*_ds1g``:
+non-causal in slices of (batch, kv-head) units, causal in ranges of query
+rows), the cost of a bounded backward workspace.
 
 ``roofline`` is for the dominant kernel of the step, the dK/dV kernel launched
 by ``fa_bwd`` on the deterministic path: 4 GEMMs (S, dP, dV, dK), i.e.
@@ -401,6 +404,21 @@ def main() -> int:
             out.backward(do)
         return f
 
+    import tilelang_fa2_4d_mask.fa2 as fa2mod
+
+    def fwd_bwd_limited(causal, limit):
+        # deterministic fwd+bwd with the dS workspace capped at `limit` bytes
+        inner = fwd_bwd(causal, False)
+
+        def f():
+            prev = fa2mod.DS_LIMIT_BYTES
+            fa2mod.DS_LIMIT_BYTES = limit
+            try:
+                inner()
+            finally:
+                fa2mod.DS_LIMIT_BYTES = prev
+        return f
+
     log(f"device: {torch.cuda.get_device_name(dev)}; workload B{B} T{T} Hq{HQ} Hk{HK} D{D} bf16")
     flush = Flusher(torch, dev)
     from tilelang_fa2_4d_mask.fa2 import ds_limit_bytes
@@ -413,6 +431,8 @@ def main() -> int:
         ("fwd_bwd_causal", fwd_bwd(True, False), "fwd_bwd", True),
         ("fwd_bwd_atomic", fwd_bwd(False, True), "fwd_bwd", False),
         ("fwd_bwd_causal_atomic", fwd_bwd(True, True), "fwd_bwd", True),
+        ("fwd_bwd_ds1g", fwd_bwd_limited(False, 1 << 30), "fwd_bwd", False),
+        ("fwd_bwd_causal_ds1g", fwd_bwd_limited(True, 1 << 30), "fwd_bwd", True),
     ):
         tm, kern = time_steps(torch, fn, args.steps, args.warmup, record_kernel_events, flush)
         ms = tm["ms"]

@@ -262,7 +262,8 @@ int dq_rows(const FaBwdParams* p) {
 
 int choose_split(const FaBwdParams* p) {
   if (p->kv_split > 0) return p->kv_split;
-  if (row_ranges(p, nullptr) > 0) return 1;   // every unit in each launch; one fp32 sum
+  const bool ranged = row_ranges(p, nullptr) > 0;
+  if (ranged && !p->is_causal) return 1;   // every unit in each launch, equal work: one fp32 sum
   const int G = p->heads_q / p->heads_k;
   const int kb = kv_block_keys(p);
   const int nkt = (p->seqlen_k + kb - 1) / kb;
@@ -276,7 +277,11 @@ int choose_split(const FaBwdParams* p) {
   // size is faster without the split's fp32 slabs.  Sliced non-causal
   // launches aim at one workgroup per CU (equal work: one round), which
   // halves the split and its slabs (H with a 1 GiB limit: -2.4 %).
-  const bool sliced = units < (int64_t)p->batch * p->heads_k;
+  // Causal row ranges: the first range's work per key block is a triangle
+  // (its longest workgroup walks several times the average), which a split
+  // of the head group evens out; each part keeps its own fp32 slab across
+  // the ranges.
+  const bool sliced = ranged || units < (int64_t)p->batch * p->heads_k;
   const int64_t target = sliced ? (p->is_causal ? 1024 : kCus) : 512;
   int split = 1;
   while (split * 2 <= G && G % (split * 2) == 0 && base * split < target) split *= 2;
@@ -438,9 +443,6 @@ static int check_bwd(const FaBwdParams* p, int split) {
   if (split > 1 && (!aligned16(p->dk_accum) || !aligned16(p->dv_accum)))
     return fail(FA_ERR_STRIDE, "dk_accum/dv_accum must be 16-byte aligned");
   if (row_ranges(p, nullptr) > 0) {
-    if (split != 1)
-      return fail(FA_ERR_SHAPE, "kv_split %d: the backward over row ranges (one unit's dS tiles exceed ds_limit_bytes) "
-                  "runs with kv_split 1", split);
     if (!p->dk_accum || !p->dv_accum)
       return fail(FA_ERR_WORKSPACE, "the backward over row ranges needs dk_accum and dv_accum (plan.dkv_accum_elems)");
     if (!aligned16(p->dk_accum) || !aligned16(p->dv_accum))
@@ -473,8 +475,10 @@ int fa_bwd_plan(const FaBwdParams* p, FaBwdPlan* plan) {
   plan->dkv_accum_zeroed = split > 1 && r == kFusedAtomic ? 1 : 0;
   plan->dkv_accum_elems =
       split > 1 ? (int64_t)(r == kFusedAtomic ? 1 : split) * p->batch * p->seqlen_k * p->heads_k * p->head_dim : 0;
-  // row ranges: one fp32 sum each for dK and dV, written by the first range
-  if (row_ranges(p, nullptr) > 0) plan->dkv_accum_elems = (int64_t)p->batch * p->seqlen_k * p->heads_k * p->head_dim;
+  // row ranges: one fp32 sum (split 1) or slab per split each for dK and dV,
+  // written by the first range
+  if (row_ranges(p, nullptr) > 0)
+    plan->dkv_accum_elems = (int64_t)split * p->batch * p->seqlen_k * p->heads_k * p->head_dim;
   plan->ds_elems = ds_elems(p);
   plan->dq_split = dq_split_of(p);
   return FA_OK;
@@ -576,7 +580,9 @@ int fa_bwd(const FaBwdParams* p) {
       fa::BwdArgs k = a;
       k.q32_lo = rb[r];
       k.q32_hi = rb[r + 1];
-      k.acc_mode = r == 0 ? 1 : (r + 1 == nr ? 3 : 2);
+      // one sum (split 1): the last range writes dK/dV; slabs (split > 1):
+      // fa_bwd_finalize sums them
+      k.acc_mode = r == 0 ? 1 : (r + 1 == nr && split == 1 ? 3 : 2);
       k.ds_plane = fa::ds_row(k.q32_hi, nk32, causal) - fa::ds_row(k.q32_lo, nk32, causal);
       if ((st = launch_status(fa::launch_bwd_dkdv2(k, p->head_dim, p->dtype, causal, s), "dkdv"))) return st;
       fa::BwdArgs q = k;

@@ -277,8 +277,10 @@ def test_plan_row_ranges(lib):
     """Without a mask, a limit below one (batch, kv-head) unit's tiles runs
     the dS kernels over ranges of query rows, every unit in each launch:
     512-row chunks (16 steps), as few ranges as the limit allows, balanced;
-    head-group split 1, one fp32 sum each for dK and dV, dQ written per range
-    (no fp32 atomics, in atomic mode too)."""
+    dQ written per range (no fp32 atomics, in atomic mode too).  Non-causal:
+    head-group split 1, one fp32 sum each for dK and dV; causal: the group
+    split of a sliced causal launch (1024 workgroups), one fp32 slab per part,
+    summed by fa_bwd_finalize."""
     chunk = 32 * 16 * 256 * 1024   # tiles of 512 rows x 8192 keys over the 32 heads (256 MiB)
     for atomic in (0, 1):
         plan = _plan(lib, atomic_dq=atomic, ds_limit_bytes=(1 << 29) - 2)   # 1 chunk fits: 16 ranges
@@ -292,15 +294,15 @@ def test_plan_row_ranges(lib):
     # within the limit; below the last chunk, dQ recomputed
     for limit in (1 << 28, 265_000_000):
         plan = _plan(lib, atomic_dq=0, is_causal=1, ds_limit_bytes=limit)
-        assert 0 < 2 * plan.ds_elems <= limit and plan.kv_split == 1, limit
-        assert plan.dkv_accum_elems == 8192 * 8 * 128, limit
+        assert 0 < 2 * plan.ds_elems <= limit and plan.kv_split == 2, limit
+        assert plan.dkv_accum_elems == 2 * 8192 * 8 * 128 and plan.dkv_accum_zeroed == 0, limit
     assert _plan(lib, atomic_dq=0, is_causal=1, ds_limit_bytes=250_000_000).ds_elems == 0
     # causal problems take ranges whenever they slice at all (unit slices would
     # split each head group through fp32 slabs): 2.2 GB of tiles under 1 GiB
     for atomic in (0, 1):
         plan = _plan(lib, atomic_dq=atomic, is_causal=1, ds_limit_bytes=1 << 30)
-        assert 0 < 2 * plan.ds_elems <= 1 << 30 and plan.kv_split == 1 and plan.dq_split == 1
-        assert plan.dkv_accum_elems == 8192 * 8 * 128
+        assert 0 < 2 * plan.ds_elems <= 1 << 30 and plan.kv_split == 2 and plan.dq_split == 1
+        assert plan.dkv_accum_elems == 2 * 8192 * 8 * 128
     # ... but not when every tile fits (the headline's causal 2.2 GB under the default)
     plan = _plan(lib, atomic_dq=0, is_causal=1)
     assert plan.ds_elems == 32 * (256 * 257 // 2) * 1024 and plan.dkv_accum_elems == 0
@@ -311,14 +313,12 @@ def test_plan_row_ranges(lib):
     # a mask keeps the recompute route below one unit; so does head dim 256
     assert _plan(lib, atomic_dq=0, ds_limit_bytes=(1 << 29) - 2, mask=FAKE).ds_elems == 0
     assert _plan(lib, atomic_dq=0, **long, mask=FAKE).ds_elems == 0
-    # the row ranges need the fp32 sums and head-group split 1
+    # the row ranges need the fp32 sums; a caller's split gives one slab per part
     p = bwd_params(atomic_dq=0, ds_limit_bytes=(1 << 29) - 2, ds_tiles=FAKE, ds_tiles_elems=chunk)
     assert lib.fa_bwd(ctypes.byref(p)) == 8
     assert "needs dk_accum and dv_accum" in lib.fa_last_error().decode()
-    p = bwd_params(atomic_dq=0, ds_limit_bytes=(1 << 29) - 2, ds_tiles=FAKE, ds_tiles_elems=chunk, kv_split=2,
-                   dk_accum=FAKE, dv_accum=FAKE)
-    assert lib.fa_bwd(ctypes.byref(p)) == 2
-    assert "runs with kv_split 1" in lib.fa_last_error().decode()
+    plan = _plan(lib, atomic_dq=0, ds_limit_bytes=(1 << 29) - 2, kv_split=4)
+    assert plan.kv_split == 4 and plan.dkv_accum_elems == 4 * 8192 * 8 * 128 and plan.ds_elems == chunk
 
 
 def test_det_path_needs_ds_tiles(lib):

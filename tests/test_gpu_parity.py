@@ -248,9 +248,10 @@ def _plan_of(cfg, limit, atomic):
 def test_row_ranges_vs_oracle(cuda, cfg, mode):
     atomic, ds_limit = MODES[mode]
     plan = _plan_of(cfg, _rows_limit(cfg), atomic)
-    # the route really is the ranged one: dS tiles, split 1, the fp32 sums, no dQ atomics
-    assert plan.ds_elems > 0 and plan.kv_split == 1 and plan.dkv_accum_elems == cfg.B * cfg.Tk * cfg.Hk * cfg.D
-    assert plan.needs_dq_accum == 0
+    # the route really is the ranged one: dS tiles, the fp32 sums (one per
+    # head-group part; causal launches split the group), no dQ atomics
+    assert plan.ds_elems > 0 and plan.dkv_accum_elems == plan.kv_split * cfg.B * cfg.Tk * cfg.Hk * cfg.D
+    assert plan.needs_dq_accum == 0 and (plan.kv_split == 1 or cfg.is_causal)
     case = I.make_case(cfg, seed=7)
     print(f"case {cfg.name} mode={mode}", flush=True)
     ours = run_ours(case, cfg, atomic=atomic, ds_limit=ds_limit)
