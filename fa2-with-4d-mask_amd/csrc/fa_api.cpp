@@ -166,6 +166,31 @@ int row_ranges(const FaBwdParams* p, std::vector<int>* bounds) {
   return ranges_under(p, hi, bounds);
 }
 
+// Parts of a head group.  With a mask (whose lists of live steps are not
+// ranged), when not even one unit's tiles fit the limit, the head group
+// splits into parts of whole query heads -- the dK/dV kernel's head-group
+// split, one fp32 slab per part summed by fa_bwd_finalize -- and each slice
+// holds the planes of some parts of one unit: the smallest split whose part
+// fits, the parts of a unit in nearly equal slices.  Returns the split (0:
+// none) and the parts per slice.
+int part_split(const FaBwdParams* p, int* per) {
+  if (!p->mask || p->head_dim > 128) return 0;
+  const int64_t limit = ds_limit_of(p), unit = ds_unit_elems(p);
+  if (limit < 0 || unit <= 0 || limit / (2 * unit) >= 1) return 0;
+  const int G = p->heads_q / p->heads_k;
+  for (int s = 2; s <= G; ++s) {
+    if (G % s != 0 || (p->kv_split > 0 && s != p->kv_split)) continue;
+    const int64_t part = 2 * (unit / s);   // bytes of one part's planes
+    if (part > limit) continue;
+    if (per) {
+      const int nsl = (int)((s + limit / part - 1) / (limit / part));   // slices per unit
+      *per = (s + nsl - 1) / nsl;
+    }
+    return s;
+  }
+  return 0;
+}
+
 int64_t ds_slice_units(const FaBwdParams* p) {
   if (p->head_dim > 128) return 0;   // head dim 256: dQ is always recomputed
   const int64_t limit = ds_limit_of(p);
@@ -180,6 +205,8 @@ int64_t ds_slice_units(const FaBwdParams* p) {
   return (units + slices - 1) / slices;
 }
 int64_t ds_elems(const FaBwdParams* p) {
+  int per = 0;
+  if (const int s = part_split(p, &per)) return per * (ds_unit_elems(p) / s);
   std::vector<int> rb;
   const int nr = row_ranges(p, &rb);
   if (nr > 0) {
@@ -193,6 +220,8 @@ int64_t ds_elems(const FaBwdParams* p) {
 int ds_slices(const FaBwdParams* p) {
   const int nr = row_ranges(p, nullptr);
   if (nr > 0) return nr;
+  int parts = 0;
+  if (const int s = part_split(p, &parts)) return p->batch * p->heads_k * ((s + parts - 1) / parts);
   const int64_t per = ds_slice_units(p);
   return per > 0 ? (int)(((int64_t)p->batch * p->heads_k + per - 1) / per) : 0;
 }
@@ -230,7 +259,8 @@ constexpr int64_t kCus = 256;
 // below that, 2-8 key ranges per block are added with fp32 atomics, more
 // while the grid is below ~1024 workgroups and each range keeps >= 4 steps.
 int dq_split_of(const FaBwdParams* p) {
-  if (route_of(p) != kDsAtomic || row_ranges(p, nullptr) > 0) return 1;   // (row ranges: dQ written per range)
+  // (row ranges and head-group parts: dQ written per launch)
+  if (route_of(p) != kDsAtomic || row_ranges(p, nullptr) > 0 || part_split(p, nullptr) > 0) return 1;
   const int64_t nblk = dq_groups(p, fa::kDqDsRows);
   const int nks = (p->seqlen_k + 31) / 32;
   if (nblk >= kCus || nks < 2) return 1;
@@ -262,6 +292,7 @@ int dq_rows(const FaBwdParams* p) {
 
 int choose_split(const FaBwdParams* p) {
   if (p->kv_split > 0) return p->kv_split;
+  if (const int s = part_split(p, nullptr)) return s;
   const bool ranged = row_ranges(p, nullptr) > 0;
   if (ranged && !p->is_causal) return 1;   // every unit in each launch, equal work: one fp32 sum
   const int G = p->heads_q / p->heads_k;
@@ -534,6 +565,11 @@ static fa::BwdArgs bwd_args(const FaBwdParams* p, int split) {
   a.q32_lo = 0;
   a.q32_hi = (p->seqlen_q + 31) / 32;
   a.acc_mode = 0;
+  a.sp0 = 0;
+  a.nsp = split;
+  a.g0 = 0;
+  a.ng = a.G;
+  a.ds_p0 = 0;
   a.split = split;
   a.do_dq = dq_atomics(p) ? 1 : 0;
   a.dq_split = dq_split_of(p);
@@ -595,6 +631,26 @@ int fa_bwd(const FaBwdParams* p) {
       q.nqt = (rows + q.dq_rows - 1) / q.dq_rows;
       if ((st = launch_status(fa::launch_bwd_dq_ds(q, p->head_dim, p->dtype, causal, s), "dq"))) return st;
     }
+  } else if (int pper = 0, ps = part_split(p, &pper); ps > 0) {
+    // parts of each unit's head group: per slice of parts, the dK/dV launch
+    // writing those parts' fp32 slabs, then the dQ launch of their heads
+    const int units = p->batch * p->heads_k, G = p->heads_q / p->heads_k, gsz = G / ps;
+    for (int u = 0; u < units; ++u)
+      for (int s0 = 0; s0 < ps; s0 += pper) {
+        fa::BwdArgs k = a;
+        k.bk0 = u;
+        k.nbk = 1;
+        k.sp0 = s0;
+        k.nsp = std::min(pper, ps - s0);
+        k.ds_p0 = (int64_t)u * G + (int64_t)s0 * gsz;
+        if ((st = launch_status(fa::launch_bwd_dkdv2(k, p->head_dim, p->dtype, causal, s), "dkdv"))) return st;
+        fa::BwdArgs q = k;
+        q.g0 = s0 * gsz;
+        q.ng = k.nsp * gsz;
+        q.dq_rows = fa::kDqDsRows;
+        q.nqt = (p->seqlen_q + q.dq_rows - 1) / q.dq_rows;
+        if ((st = launch_status(fa::launch_bwd_dq_ds(q, p->head_dim, p->dtype, causal, s), "dq"))) return st;
+      }
   } else {
     // the workspace holds a slice of (batch, kv-head) units: dK/dV and then
     // dQ of each slice (same stream, so a slice's tiles are consumed before
@@ -607,6 +663,7 @@ int fa_bwd(const FaBwdParams* p) {
       fa::BwdArgs k = a;
       k.bk0 = q.bk0 = u0;
       k.nbk = q.nbk = std::min(per, units - u0);
+      k.ds_p0 = q.ds_p0 = (int64_t)u0 * a.G;
       if ((st = launch_status(fa::launch_bwd_dkdv2(k, p->head_dim, p->dtype, causal, s), "dkdv"))) return st;
       if ((st = launch_status(fa::launch_bwd_dq_ds(q, p->head_dim, p->dtype, causal, s), "dq"))) return st;
     }

@@ -88,16 +88,17 @@ __global__ __launch_bounds__(NW * 64, 2) void dq_ds_kernel(const BwdArgs a) {
   // live key steps.
   const int nqb = a.nqt;
   const int nsp = ATOMIC ? a.dq_split : 1;
-  const int nblk = a.nbk * a.G * nqb * nsp;
+  const int ng = a.ng;                   // heads of each group in this launch, from g0
+  const int nblk = a.nbk * ng * nqb * nsp;
   const int W0 = xcd_remap(blockIdx.x, nblk);
   const int W = ATOMIC ? W0 / nsp : W0;
   const int ksp = ATOMIC ? W0 - W * nsp : 0;        // key split of this workgroup
-  const int per_kv = a.G * nqb;
+  const int per_kv = ng * nqb;
   const int bkl = W / per_kv;             // unit within this launch's slice
   const int bk = a.bk0 + bkl;
   const int rem = W - bkl * per_kv;
-  const int qb_rank = rem / a.G;
-  const int g = rem - qb_rank * a.G;
+  const int qb_rank = rem / ng;
+  const int g = a.g0 + rem - qb_rank * ng;
   const int b = bk / a.Hk, kvh = bk - b * a.Hk;
   const int h = kvh * a.G + g;
   // (over a range of rows, block 0 of the launch is the range's first)
@@ -200,7 +201,7 @@ __global__ __launch_bounds__(NW * 64, 2) void dq_ds_kernel(const BwdArgs a) {
     sd[u] = opaque(lds0 + KTILE + wv * DSW + ch * 512 + ((skey ^ (4 * ch)) & 31) * 16);
   }
   const uint16_t* __restrict__ dsp = (const uint16_t*)a.ds;
-  const int64_t plane = ((int64_t)b * a.Hq + h - (int64_t)a.bk0 * a.G) * a.ds_plane - ds_row(a.q32_lo, nk32, CAUSAL);
+  const int64_t plane = ((int64_t)b * a.Hq + h - a.ds_p0) * a.ds_plane - ds_row(a.q32_lo, nk32, CAUSAL);
   int64_t row0[kDqSteps];
 #pragma unroll
   for (int i = 0; i < kDqSteps; ++i) row0[i] = plane + ds_row(s0 + i, nk32, CAUSAL);
@@ -365,7 +366,7 @@ __global__ __launch_bounds__(NW * 64, 2) void dq_ds_kernel(const BwdArgs a) {
 
 template <typename T, int D, bool CAUSAL, bool ATOMIC, bool PREC>
 hipError_t launch_p(const BwdArgs& a, hipStream_t s) {
-  const dim3 grid((unsigned)(a.nbk * a.G * a.nqt * (ATOMIC ? a.dq_split : 1)));
+  const dim3 grid((unsigned)(a.nbk * a.ng * a.nqt * (ATOMIC ? a.dq_split : 1)));
   if (PREC && a.mask) {
     // With a mask the row blocks stay at 256 rows (the prepared lists are per
     // 256-row block).  At head dim 128: 8 waves of one 32-row step each (with

@@ -84,17 +84,18 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
   __shared__ __attribute__((aligned(1024))) char smem[LOFF + NBUF * LBUF];
 
   // ---- which (batch, kv-head, split, key block) ------------------------------
-  const int nblk = a.nbk * a.nkt * a.split;
+  const int nblk = a.nbk * a.nkt * a.nsp;
   const int W = xcd_remap(blockIdx.x, nblk);
-  const int per_bk = a.split * a.nkt;
+  const int per_bk = a.nsp * a.nkt;
   const int bkl = W / per_bk;             // unit within this launch's slice
   const int bk = a.bk0 + bkl;
   const int rem = W - bkl * per_bk;
-  const int sp = rem / a.nkt;
+  const int spl = rem / a.nkt;            // part within this launch's parts
+  const int sp = a.sp0 + spl;
   const int b = bk / a.Hk, kvh = bk - b * a.Hk;
   // longest workgroups first: key blocks ascending (causal work shrinks with
   // the block), with a mask by the count of live steps of the group's first head
-  const int kt_rank = rem - sp * a.nkt;
+  const int kt_rank = rem - spl * a.nkt;
   const int kt = MASK ? mask_order(a.ml, a.mws, mask_plane(a.ml, b, kvh * a.G + sp * (a.G / a.split)), 1)[kt_rank]
                       : kt_rank;
 
@@ -432,7 +433,7 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
   // it_ptr: tile of (it_h, step it_qs / 32) and this wave's keys (a running
   // pointer: no 64-bit multiply per step).
   const int kb32 = __builtin_amdgcn_readfirstlane(kw0) >> 5;
-  const int64_t ds_u0 = (int64_t)a.bk0 * a.G;   // first dS plane (b Hq + h) of the workspace
+  const int64_t ds_u0 = a.ds_p0;                 // first dS plane (b Hq + h) of the workspace
   const int64_t ds_r0 = ds_row(a.q32_lo, a.nk32, CAUSAL);   // first tile of the launch's steps in a plane
   const bool ds_on = a.ds != nullptr && kb32 < a.nk32;
   // tile bytes are chunk-major (chunk c of key row k at c 512 + k 16): store t
@@ -864,7 +865,7 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
 
 template <typename T, int D, bool CAUSAL>
 hipError_t launch_t(const BwdArgs& a, hipStream_t s) {
-  const dim3 grid((unsigned)(a.nbk * a.nkt * a.split)), block(kKvWaves * 64);
+  const dim3 grid((unsigned)(a.nbk * a.nkt * a.nsp)), block(kKvWaves * 64);
   const bool m = a.mask != nullptr, sc = a.score != nullptr;
   if (m && sc) hipLaunchKernelGGL((dkdv2_kernel<T, D, CAUSAL, true, true>), grid, block, 0, s, a);
   else if (m) hipLaunchKernelGGL((dkdv2_kernel<T, D, CAUSAL, true, false>), grid, block, 0, s, a);

@@ -147,10 +147,18 @@ struct BwdArgs {
   // workspace; its planes then hold the tiles of those steps only, step s at
   // ds_row(s) - ds_row(q32_lo).  Others: 0, nq32.
   int q32_lo, q32_hi;
-  // dK/dV kernel over row ranges (split 1): 0 writes dK/dV (the whole row
-  // range in one launch); 1 writes fp32 sums to dk_accum/dv_accum [B, Tk,
-  // Hk, D] (first range), 2 adds to them, 3 adds them and writes dK/dV (last).
+  // dK/dV kernel over row ranges: 0 writes dK/dV, or with a head-group split
+  // its part's fp32 slab (the whole row range in one launch); 1 writes the
+  // fp32 sums dk_accum/dv_accum [B, Tk, Hk, D] (a slab per part with a split)
+  // (first range), 2 adds to them, 3 adds them and writes dK/dV (last range,
+  // split 1).
   int acc_mode;
+  // Slices within a head group: the dK/dV kernel runs parts sp0 .. sp0 +
+  // nsp - 1 of its head-group split, the dQ kernel heads g0 .. g0 + ng - 1
+  // of each group; the workspace's first dS plane is (b Hq + h) = ds_p0.
+  // Others: 0, split, 0, G, bk0 G.
+  int sp0, nsp, g0, ng;
+  int64_t ds_p0;
   int nqt;              // query tiles per (b, h) (dQ kernel)
   int dq_rows;          // query rows per dQ-from-dS workgroup: kDqDsRows or kDqDsRowsWide
   int split;            // query-head-group split of the dK/dV kernel

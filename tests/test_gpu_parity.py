@@ -56,15 +56,27 @@ def _rows_limit(cfg):
     return 2 * parts * cfg.B * cfg.Hq * best * 1024
 
 
+def _one_plane_limit(cfg):
+    """dS workspace bytes of one (batch, head) plane, tile pairs included (a
+    mask or a score): below one unit, a masked backward splits each head
+    group into parts of one head."""
+    nq, nk = -(-cfg.Tq // 32), -(-cfg.Tk // 32)
+    plane = sum(min(s + 1, nk) for s in range(nq)) if cfg.is_causal else nq * nk
+    parts = 2 if (cfg.mask is not None or cfg.score is not None) else 1
+    return 2 * parts * plane * 1024
+
+
 def run_ours(case, cfg, *, atomic=True, scale=None, attention_mask=None, backward=True, ds_limit=0):
     """ds_limit: dS workspace limit of the backward (0 = default, dQ from the
     stored dS tiles; -1 = no workspace: dQ recomputed (deterministic) or fused
     fp32 atomics; "unit" = one (batch, kv-head) unit: the dS kernels run once
-    per unit; "rows" = one 512-row range of every unit, see _rows_limit)."""
+    per unit; "rows" = one 512-row range of every unit, see _rows_limit;
+    "plane" = one (batch, head) plane, see _one_plane_limit)."""
     api = _api()
     import tilelang_fa2_4d_mask.fa2 as fa2mod
 
-    fa2mod.DS_LIMIT_BYTES = {"unit": _one_unit_limit, "rows": _rows_limit}[ds_limit](cfg) if isinstance(
+    fa2mod.DS_LIMIT_BYTES = {"unit": _one_unit_limit, "rows": _rows_limit, "plane": _one_plane_limit}[ds_limit](
+        cfg) if isinstance(
         ds_limit, str) else ds_limit
     dev = torch.device("cuda:0")
     q = case["q"].to(dev).detach().requires_grad_(backward)
@@ -175,12 +187,16 @@ SMALL = [
 # fp32-atomic dQ fused into the dK/dV kernel (no dS workspace); deterministic
 # with dQ from the stored dS tiles; deterministic with dQ recomputed (no dS
 # workspace allowed); both dS modes with a workspace of one (batch, kv-head)
-# unit, so that the dS kernels run slice by slice; both with a workspace of
-# one 512-row range of every unit (ranges of rows where Tq > 512 B Hk without
-# a mask; unit slices or recompute otherwise)
+# unit, so that the dS kernels run slice by slice (sized without the tile
+# pairs of a mask or score: half a unit there, so a masked group splits in
+# two); both with a workspace of one 512-row range of every unit (ranges of
+# rows where Tq > 512 B Hk without a mask; unit slices or recompute
+# otherwise); both with a workspace of one (batch, head) plane (a masked
+# head group then splits into one-head parts)
 MODES = {"atomic": (True, 0), "atomic_fused": (True, -1), "det_ds": (False, 0), "det_recompute": (False, -1),
          "atomic_sliced": (True, "unit"), "det_sliced": (False, "unit"),
-         "atomic_rows": (True, "rows"), "det_rows": (False, "rows")}
+         "atomic_rows": (True, "rows"), "det_rows": (False, "rows"),
+         "atomic_parts": (True, "plane"), "det_parts": (False, "plane")}
 
 
 @pytest.mark.parametrize("mode", list(MODES))
@@ -237,6 +253,7 @@ def _plan_of(cfg, limit, atomic):
     p.scale, p.is_causal, p.atomic_dq, p.dtype = cfg.D ** -0.5, int(cfg.is_causal), int(atomic), 0
     p.ds_limit_bytes = limit
     p.score = 16 if cfg.score is not None else None
+    p.mask = 16 if cfg.mask is not None else None
     plan = _ext.FaBwdPlan()
     lib = _ext.load_library()
     assert lib.fa_bwd_plan(ctypes.byref(p), ctypes.byref(plan)) == 0
@@ -259,6 +276,39 @@ def test_row_ranges_vs_oracle(cuda, cfg, mode):
     check(ours, ref, label=f"{cfg.name}/{mode}")
     # dQ of a row comes from the same dS tiles in the same key order as the
     # unranged launch: bitwise equal to it
+    one = run_ours(case, cfg, atomic=False, ds_limit=0)
+    assert torch.equal(ours["dq"], one["dq"]) and torch.equal(ours["out"], one["out"])
+
+
+# The masked backward over parts of head groups (one (batch, head) plane of
+# workspace, below one unit): GQA with batch 2, packed documents with a score
+# in MQA causal, a group of three heads (split 3) with a head-broadcast mask in
+# fp16 bshd.
+PARTS = [
+    C("parts_mask_gqa", 2, 700, 600, 8, 2, 128, mask="bernoulli"),
+    C("parts_docs_mqa_causal_score", 1, 512, 512, 4, 1, 64, is_causal=True, mask="packed_docs", mask_heads=1,
+      score="normal"),
+    C("parts_mask_g3_fp16_bshd", 1, 300, 333, 6, 2, 128, torch.float16, layout="bshd", mask="bernoulli",
+      mask_heads=1),
+]
+
+
+@pytest.mark.parametrize("mode", ["det_parts", "atomic_parts"])
+@pytest.mark.parametrize("cfg", PARTS, ids=[c.name for c in PARTS])
+def test_head_group_parts_vs_oracle(cuda, cfg, mode):
+    atomic, ds_limit = MODES[mode]
+    plan = _plan_of(cfg, _one_plane_limit(cfg), atomic)
+    # the route really is the one of parts: one head per part, dS tiles, a slab
+    # per part, no dQ atomics
+    assert plan.ds_elems > 0 and plan.kv_split == cfg.Hq // cfg.Hk and plan.dq_split == 1
+    assert plan.needs_dq_accum == 0 and plan.dkv_accum_elems == plan.kv_split * cfg.B * cfg.Tk * cfg.Hk * cfg.D
+    case = I.make_case(cfg, seed=9)
+    print(f"case {cfg.name} mode={mode}", flush=True)
+    ours = run_ours(case, cfg, atomic=atomic, ds_limit=ds_limit)
+    ref = run_oracle_cpu(case, cfg)
+    check(ours, ref, label=f"{cfg.name}/{mode}")
+    # dQ of a head comes from the same dS tiles in the same key order as the
+    # unsliced launch: bitwise equal to it
     one = run_ours(case, cfg, atomic=False, ds_limit=0)
     assert torch.equal(ours["dq"], one["dq"]) and torch.equal(ours["out"], one["out"])
 
