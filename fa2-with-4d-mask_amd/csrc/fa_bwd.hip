@@ -459,9 +459,8 @@ constexpr int kDqBN = 64;    // keys per tile
 template <typename T, int D, bool CAUSAL, bool MASK, bool SCORE>
 __global__ __launch_bounds__(256, 1) void dq_kernel(const BwdArgs a) {
   using V8 = typename Vec8<T>::type;
-  // head dim 256: 32-key tiles (the staging and S/dP registers of 64 keys
-  // beside 256 of Q/dO fragments and dQ accumulators spill)
-  constexpr int BM = kDqBM, BN = D > 128 ? 32 : kDqBN;
+  static_assert(D <= 128, "head dim 256 recomputes dQ in fa_wide.hip");
+  constexpr int BM = kDqBM, BN = kDqBN;
   constexpr int NKB = BN / 32;   // 32-key blocks per tile
   constexpr int DS = D / 16, NB = D / 32, CH = D / 8;
   constexpr int KS = D + 40;   // K: row-wise and transposed reads
@@ -514,13 +513,30 @@ __global__ __launch_bounds__(256, 1) void dq_kernel(const BwdArgs a) {
     }
   }
   const int qrow_c = min(qrow, Tq - 1);
-  const uint8_t* mrow = nullptr;
   const float* srow = nullptr;
-  if constexpr (MASK) mrow = a.mask + b * a.msb + h * a.msh + (int64_t)qrow_c * a.msq;
   if constexpr (SCORE) srow = a.score + b * a.ssb + h * a.ssh + (int64_t)qrow_c * a.ssq;
 
+  // Key tiles: 0 .. ntiles-1, or with a mask the live 64-key tiles of the
+  // prepared list of this block's 256-row unit (the forward's lists; causality
+  // folded in; bit 31: every entry kept), and the keep bits of this lane's
+  // row from the prepared bit array
+  static_assert(!MASK || (BN == kFwdKeys && kFwdRows % BM == 0), "prepared-mask list shape");
+  const int32_t* flist = nullptr;
+  const uint32_t* mbits = nullptr;
+  if constexpr (MASK) {
+    const int pm = mask_plane(a.ml, b, h);
+    flist = (const int32_t*)(a.mws + a.ml.lfwd + pm * a.ml.plfwd) + (int64_t)(q0 / kFwdRows) * (1 + a.ml.nft);
+    mbits = (const uint32_t*)(a.mws + a.ml.bits + pm * a.ml.pbits) + (int64_t)qrow_c * a.ml.wk;
+  }
   const int kv_end = CAUSAL ? min(Tk, q0 + BM) : Tk;
-  const int ntiles = (kv_end + BN - 1) / BN;
+  const int ntiles = MASK ? flist[0] : (kv_end + BN - 1) / BN;
+  // list entries of positions j, j+1, j+2 (the next tile's loads are issued a
+  // tile ahead, its entry read a tile before that)
+  auto entry = [&](int j) __attribute__((always_inline)) -> int32_t {
+    if constexpr (MASK) return j < ntiles ? flist[1 + j] : 0;
+    else return j;
+  };
+  int32_t e_cur = entry(0), e_nx = entry(1);
 
   u32x4 kreg[U], vreg[U];
   // Keys past Tk are loaded from key Tk-1 (unconditional loads): their P is
@@ -553,13 +569,14 @@ __global__ __launch_bounds__(256, 1) void dq_kernel(const BwdArgs a) {
   const int tr_row = 4 * hf + ((lane >> 2) & 3);
   const int tr_col = ((lane >> 4) & 1) * 16 + (lane & 3) * 4;
 
-  load_tile(0);
+  load_tile((e_cur & 0x7fffffff) * BN);
   store_tile(0);
   __syncthreads();
   for (int j = 0; j < ntiles; ++j) {
-    const int k0 = j * BN;
+    const int k0 = (e_cur & 0x7fffffff) * BN;
     const bool more = j + 1 < ntiles;
-    if (more) load_tile(k0 + BN);
+    if (more) load_tile((e_nx & 0x7fffffff) * BN);
+    const int32_t e_nx2 = entry(j + 2);
     const T* ks = smem + (j & 1) * (KT + VT);
     const T* vs = ks + KT;
     const bool active = !CAUSAL || (k0 <= q0w + 31);
@@ -577,7 +594,13 @@ __global__ __launch_bounds__(256, 1) void dq_kernel(const BwdArgs a) {
           pacc[kb] = mfma32(as_vec8<T>(vx), dof[ds], pacc[kb]);
         }
       }
-      const bool edge = MASK || (k0 + BN > Tk) || (CAUSAL && k0 + BN - 1 > q0w);
+      // (with a mask: keep words of this tile's two 32-key blocks)
+      uint32_t mw[MASK ? NKB : 1] = {};
+      if constexpr (MASK) {
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb) mw[kb] = (k0 >> 5) + kb < a.ml.nk32 ? mbits[(k0 >> 5) + kb] : 0u;
+      }
+      const bool edge = (MASK && e_cur >= 0) || (k0 + BN > Tk) || (CAUSAL && k0 + BN - 1 > q0w);
 #pragma unroll
       for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
@@ -594,7 +617,7 @@ __global__ __launch_bounds__(256, 1) void dq_kernel(const BwdArgs a) {
             if (edge) {
               bool keep = kx < Tk;
               if constexpr (CAUSAL) keep = keep && kx <= qrow;
-              if constexpr (MASK) keep = keep && mrow[min(kx, Tk - 1)] != 0;
+              if constexpr (MASK) keep = keep && ((mw[kb] >> (kx & 31)) & 1u) != 0;
               p = keep ? p : 0.f;
             }
             sacc[kb][i] = p * (pacc[kb][i] - delta_q) * scale;
@@ -634,6 +657,8 @@ __global__ __launch_bounds__(256, 1) void dq_kernel(const BwdArgs a) {
     }
     if (more) store_tile((j + 1) & 1);
     __syncthreads();
+    e_cur = e_nx;
+    e_nx = e_nx2;
   }
 
   T* os = smem + wave * 32 * OS;
@@ -741,11 +766,9 @@ hipError_t launch_bwd_dq(const BwdArgs& a, int D, int dtype, bool causal, hipStr
   if (dtype == 0) {
     if (D == 128) return causal ? launch_dq_t<bf16, 128, true>(a, s) : launch_dq_t<bf16, 128, false>(a, s);
     if (D == 64) return causal ? launch_dq_t<bf16, 64, true>(a, s) : launch_dq_t<bf16, 64, false>(a, s);
-    if (D == 256) return causal ? launch_dq_t<bf16, 256, true>(a, s) : launch_dq_t<bf16, 256, false>(a, s);
   } else {
     if (D == 128) return causal ? launch_dq_t<f16, 128, true>(a, s) : launch_dq_t<f16, 128, false>(a, s);
     if (D == 64) return causal ? launch_dq_t<f16, 64, true>(a, s) : launch_dq_t<f16, 64, false>(a, s);
-    if (D == 256) return causal ? launch_dq_t<f16, 256, true>(a, s) : launch_dq_t<f16, 256, false>(a, s);
   }
   return hipErrorInvalidValue;
 }
