@@ -170,25 +170,25 @@ int row_ranges(const FaBwdParams* p, std::vector<int>* bounds) {
 // ranged), when not even one unit's tiles fit the limit, the head group
 // splits into parts of whole query heads -- the dK/dV kernel's head-group
 // split, one fp32 slab per part summed by fa_bwd_finalize -- and each slice
-// holds the planes of some parts of one unit: the smallest split whose part
-// fits, the parts of a unit in nearly equal slices.  Returns the split (0:
-// none) and the parts per slice.
+// holds the planes of some parts of one unit, in nearly equal slices.  One
+// head per part (unless the caller sets the split): a slice's planes then
+// give the most workgroups (two-head parts halve them for the same planes:
+// T 20000 with packed documents, fwd+bwd 3.7 ms against 3.3 with one-head
+// parts).  Returns the split (0: none) and the parts per slice.
 int part_split(const FaBwdParams* p, int* per) {
   if (!p->mask || p->head_dim > 128) return 0;
   const int64_t limit = ds_limit_of(p), unit = ds_unit_elems(p);
   if (limit < 0 || unit <= 0 || limit / (2 * unit) >= 1) return 0;
   const int G = p->heads_q / p->heads_k;
-  for (int s = 2; s <= G; ++s) {
-    if (G % s != 0 || (p->kv_split > 0 && s != p->kv_split)) continue;
-    const int64_t part = 2 * (unit / s);   // bytes of one part's planes
-    if (part > limit) continue;
-    if (per) {
-      const int nsl = (int)((s + limit / part - 1) / (limit / part));   // slices per unit
-      *per = (s + nsl - 1) / nsl;
-    }
-    return s;
+  const int s = p->kv_split > 0 ? p->kv_split : G;
+  if (s < 2 || G % s != 0) return 0;
+  const int64_t part = 2 * (unit / s);   // bytes of one part's planes
+  if (part > limit) return 0;
+  if (per) {
+    const int nsl = (int)((s + limit / part - 1) / (limit / part));   // slices per unit
+    *per = (s + nsl - 1) / nsl;
   }
-  return 0;
+  return s;
 }
 
 int64_t ds_slice_units(const FaBwdParams* p) {

@@ -322,15 +322,16 @@ def test_plan_row_ranges(lib):
 
 def test_plan_head_group_parts(lib):
     """With a mask, a limit below one (batch, kv-head) unit's tiles (the
-    group's planes, pairs of tiles with a mask) splits the head group: the
-    smallest split whose part fits, each slice some parts of one unit, one
-    fp32 slab per part (fully written), dQ written per launch."""
+    group's planes, pairs of tiles with a mask) splits the head group into
+    one-head parts (or the caller's split), each slice as many parts of one
+    unit as fit, balanced; one fp32 slab per part (fully written), dQ written
+    per launch."""
     plane = 256 * 256 * 1024 * 2          # one head's tile pairs at T 8192 (256 MiB of elements x 2 B)
     for atomic in (0, 1):
-        # 1 GiB per unit: 600 MiB holds two planes -> split 2, one part per slice
+        # 1 GiB per unit: 600 MiB holds two planes -> split 4, two parts per slice
         plan = _plan(lib, atomic_dq=atomic, mask=FAKE, ds_limit_bytes=600 << 20)
-        assert plan.kv_split == 2 and plan.ds_elems == 2 * plane and plan.dq_split == 1
-        assert plan.needs_dq_accum == 0 and plan.dkv_accum_elems == 2 * 8192 * 8 * 128
+        assert plan.kv_split == 4 and plan.ds_elems == 2 * plane and plan.dq_split == 1
+        assert plan.needs_dq_accum == 0 and plan.dkv_accum_elems == 4 * 8192 * 8 * 128
         assert plan.dkv_accum_zeroed == 0
     # 300 MiB: one plane -> split 4
     plan = _plan(lib, atomic_dq=0, mask=FAKE, ds_limit_bytes=300 << 20)
@@ -338,13 +339,14 @@ def test_plan_head_group_parts(lib):
     # below one plane: dQ recomputed
     assert _plan(lib, atomic_dq=0, mask=FAKE, ds_limit_bytes=200 << 20).ds_elems == 0
     # mask and score at T 20000 under the default 4 GiB: a unit's four planes
-    # take 6.4 GB, two of them 3.2 GB -> split 2, one part per slice
+    # take 6.4 GB, two of them 3.2 GB -> split 4, two parts per slice
     big = dict(seqlen_q=20000, seqlen_k=20000, mask=FAKE, score=FAKE)
     plan = _plan(lib, atomic_dq=0, **big)
-    assert plan.kv_split == 2 and plan.ds_elems == 2 * 625 * 625 * 1024 * 2
-    # the caller's split is kept when a part fits
-    plan = _plan(lib, atomic_dq=0, mask=FAKE, ds_limit_bytes=600 << 20, kv_split=4)
-    assert plan.kv_split == 4 and plan.ds_elems == 2 * plane
+    assert plan.kv_split == 4 and plan.ds_elems == 2 * 625 * 625 * 1024 * 2
+    # the caller's split is kept when a part fits, refused (dQ recomputed) when not
+    plan = _plan(lib, atomic_dq=0, mask=FAKE, ds_limit_bytes=600 << 20, kv_split=2)
+    assert plan.kv_split == 2 and plan.ds_elems == 2 * plane
+    assert _plan(lib, atomic_dq=0, mask=FAKE, ds_limit_bytes=300 << 20, kv_split=2).ds_elems == 0
 
 
 def test_det_path_needs_ds_tiles(lib):
