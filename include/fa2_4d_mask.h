@@ -156,7 +156,9 @@ typedef struct FaBwdPlan {
                                     (512-row multiples, every unit; fa_bwd runs the ranges one after
                                     the other and sums dK/dV across them in dk_accum/dv_accum) -- causal
                                     problems without a mask take the ranges whenever they do not fit
-                                    at once.  0 when not even one unit, nor one 512-row range, fits:
+                                    at once; with a mask, of as many one-head parts of a unit's group
+                                    as fit (kv_split = the group size, one slab per part).  0 when
+                                    not even one unit, 512-row range, nor (with a mask) plane fits:
                                     dQ is then recomputed (atomic_dq = 0, or with a mask or a score) or
                                     added per key block by the fused dK/dV kernel (atomic_dq = 1 without
                                     mask and score) */
