@@ -1,26 +1,17 @@
 // FlashAttention-2 backward for gfx950 (MI355X) with optional 4D keep-mask and
-// 4D fp32 score.  Restates the maths of the reference's TileLang backward
-// (python/fa2.py:142-426) as hand-written wave64 MFMA kernels:
+// 4D fp32 score: the kernels around the dK/dV kernel (fa_bwd_kv.hip) and the
+// dQ kernels (fa_bwd_dq.hip).  Restates the maths of the reference's TileLang
+// backward (python/fa2.py:142-426):
 //
 //   preprocess   Delta[b,h,i] = sum_d O*dO (fp32)          (python/fa2.py:142-179)
-//                + zeroes the fp32 dQ accumulator, marks rows with no kept key
-//   dkdv         one workgroup per (128 keys, kv-head, batch[, head split]);
-//                loops over the query heads of the GQA group and the query
-//                tiles, so dK/dV of a group meet in registers, not atomics
-//                (python/fa2.py:181-302 / 305-426 reduce over the group with
-//                atomics or a host sum instead).  Optionally also produces dQ
-//                with fp32 atomics (use_atomic_backward=True).
-//   dq           deterministic dQ (use_atomic_backward=False): one workgroup per
-//                (128 query rows, head, batch), recomputes P and dS per key tile.
-//   convert      fp32 accumulators -> bf16/fp16 outputs.
-//
-// Per query tile (64 rows) and wave (32 keys) the dkdv kernel runs
-//   S  = Q K^T, dP = dO V^T     A = Q / dO rows from LDS, B = K / V resident
-//   P  = exp2(S*scale*log2e - LSE2), dS = P (dP - Delta) scale   (fp32)
-//   dV += P^T dO, dK += dS^T Q  A = P / dS straight from the accumulators,
-//                               B = dO / Q through ds_read_b64_tr_b16
-//   dQ  = dS K                  dS goes through LDS (key-major) and is read
-//                               back transposed; K^T resident in registers
+//                + the backward's LSE, rows with no kept key, a zeroed fp32
+//                dQ accumulator where dQ partials are added
+//   dq           dQ without a dS workspace: one workgroup per (128 query
+//                rows, head, batch) recomputes S, P, dP and dS per key tile
+//                (with a mask only the prepared lists' live tiles) and
+//                forms dQ = dS K in registers
+//   convert      fp32 accumulators (dQ partials, dK/dV slabs of a head-group
+//                split) -> bf16/fp16 outputs, slabs summed in a fixed order.
 #include "fa_common.h"
 #include "fa_kernels.h"
 
@@ -118,346 +109,19 @@ __global__ __launch_bounds__(256) void preprocess_kernel(const PreArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// dK / dV (+ atomic dQ)
-// ---------------------------------------------------------------------------
-constexpr int kKvBN = 128;   // keys per workgroup (4 waves x 32)
-constexpr int kKvBM = 64;    // query rows per inner tile
-
-template <typename T, int D, bool CAUSAL, bool MASK, bool SCORE, bool DQ>
-__global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdArgs a) {
-  using V8 = typename Vec8<T>::type;
-  constexpr int BN = kKvBN, BM = kKvBM;
-  constexpr int DS = D / 16, NB = D / 32, CH = D / 8;
-  // Q/dO tiles are read both row-wise (ds_read_b128, 16 rows) and by the
-  // transpose read (4 rows): a stride of 20 dwords mod 64 makes the first
-  // conflict-free and the second at most 2-way.
-  constexpr int QS = D + 40;
-  constexpr int QT = BM * QS;
-  constexpr int SS = BM + 40;            // dS tile [BN keys][BM queries]
-  constexpr int UQ = BM * CH / 256;      // chunks per thread per Q (or dO) tile
-  constexpr int NPAIR = (BM / 32) * NB / 4;  // (q-block, d-block) dQ pairs per wave
-  static_assert(NPAIR == 1 || NPAIR == 2, "dQ work split");
-  static_assert(BN * QS <= 2 * QT, "K staging fits in the Q buffers");
-  __shared__ __attribute__((aligned(16))) T sQ[2 * QT];
-  __shared__ __attribute__((aligned(16))) T sdO[2 * QT];
-  __shared__ __attribute__((aligned(16))) T sdS[DQ ? BN * SS : 8];
-  __shared__ __attribute__((aligned(16))) float sL[2 * BM];
-  __shared__ __attribute__((aligned(16))) float sDl[2 * BM];
-
-  const int nblk = a.B * a.Hk * a.nkt * a.split;
-  const int W = xcd_remap(blockIdx.x, nblk);
-  const int per_bk = a.split * a.nkt;
-  const int bk = W / per_bk;
-  const int rem = W - bk * per_bk;
-  const int sp = rem / a.nkt;
-  const int kt = rem - sp * a.nkt;        // ascending = most causal work first
-  const int b = bk / a.Hk, kvh = bk - b * a.Hk;
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int l32 = lane & 31, hf = lane >> 5;
-  const int Tq = a.Tq, Tk = a.Tk;
-  const int kt0 = kt * BN, kw0 = kt0 + wave * 32;
-  const int key = kw0 + l32;              // this lane's key (column of S)
-  const float c2 = a.scale_log2, scale = a.scale;
-  const int tr_row = (lane >> 2) & 3;
-  const int tr_col = ((lane >> 4) & 1) * 16 + (lane & 3) * 4;
-
-  const T* __restrict__ kp = (const T*)a.k + b * a.ksb + kvh * a.ksh;
-  const T* __restrict__ vp = (const T*)a.v + b * a.vsb + kvh * a.vsh;
-
-  // K, V fragments: B operands of S = Q K^T and dP = dO V^T.
-  // Keys past Tk are zero: their dK/dV rows are never stored and, with K = 0,
-  // their dS contributes nothing to dQ.
-  V8 kf[DS], vf[DS];
-  if (key < Tk) {
-#pragma unroll
-    for (int ds = 0; ds < DS; ++ds) {
-      kf[ds] = as_vec8<T>(gload16(kp + (int64_t)key * a.kst + ds * 16 + hf * 8));
-      vf[ds] = as_vec8<T>(gload16(vp + (int64_t)key * a.vst + ds * 16 + hf * 8));
-    }
-  } else {
-#pragma unroll
-    for (int ds = 0; ds < DS; ++ds) {
-      kf[ds] = as_vec8<T>(u32x4{0, 0, 0, 0});
-      vf[ds] = as_vec8<T>(u32x4{0, 0, 0, 0});
-    }
-  }
-
-  // K^T fragment for dQ = dS K: B[key slot][d], k-step s covers block keys
-  // 16 s .. 16 s + 15, slot (hf, t) <-> key 16 s + 8 hf + t.
-  const int db = (wave * NPAIR) / 2;      // this wave's 32-wide d block of dQ
-  V8 ktf[DQ ? 8 : 1];
-  if constexpr (DQ) {
-#pragma unroll
-    for (int u = 0; u < BN * CH / 256; ++u) {
-      const int idx = tid + u * 256;
-      const int r = idx / CH, c = idx % CH;
-      const int kk = kt0 + r;
-      const u32x4 x = kk < Tk ? gload16(kp + (int64_t)kk * a.kst + c * 8) : u32x4{0, 0, 0, 0};
-      lds_write16(sQ + r * QS + c * 8, x);
-    }
-    __syncthreads();
-#pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      const int row = s * 16 + 8 * hf + tr_row;
-      const int col = db * 32 + tr_col;
-      ktf[s] = cat_tr<T>(lds_read_tr(sQ + row * QS + col), lds_read_tr(sQ + (row + 4) * QS + col));
-    }
-    __syncthreads();
-  }
-
-  const int gsz = a.G / a.split;
-  const int g0 = sp * gsz;
-  const int qt_first = CAUSAL ? kt0 / BM : 0;
-  const int nqt = (Tq + BM - 1) / BM;
-  const int nq = max(0, nqt - qt_first);
-  const int iters = gsz * nq;
-
-  // Query tiles are visited in a per-block rotated order so that the key
-  // blocks of one kv-head add their dQ partials to different rows at any time
-  // (the atomics would otherwise all target the same cache lines).
-  const int qrot = nq > 0 ? (int)(((int64_t)kt * nq) / a.nkt) % nq : 0;
-  auto tile_of = [&](int it, int& g, int& qt) {
-    const int gi = it / nq;
-    int r = it - gi * nq + qrot;
-    if (r >= nq) r -= nq;
-    g = g0 + gi;
-    qt = qt_first + r;
-  };
-
-  u32x4 qreg[UQ], dreg[UQ];
-  float lreg = 0.f, dlreg = 0.f;
-  bool lrow_ok = true;
-  const float* __restrict__ lse_p = a.lse;
-  const float* __restrict__ delta_p = a.delta;
-  auto load_q = [&](int it) {
-    int g, qt;
-    tile_of(it, g, qt);
-    const int h = kvh * a.G + g, qs = qt * BM;
-    const T* qp = (const T*)a.q + b * a.qsb + h * a.qsh;
-    const T* dp = (const T*)a.dout + b * a.dsb + h * a.dsh;
-    // Rows past Tq are loaded from row Tq-1 (unconditional loads, no zero
-    // fill): their LSE is set to +inf, so P = dS = 0 and they add nothing.
-#pragma unroll
-    for (int u = 0; u < UQ; ++u) {
-      const int idx = tid + u * 256;
-      const int r = idx / CH, c = idx % CH;
-      const int row = min(qs + r, Tq - 1);
-      qreg[u] = gload16(qp + (int64_t)row * a.qst + c * 8);
-      dreg[u] = gload16(dp + (int64_t)row * a.dst + c * 8);
-    }
-    {
-      const int row = qs + (tid & (BM - 1));
-      const int64_t ri = ((int64_t)b * a.Hq + h) * Tq + min(row, Tq - 1);
-      lreg = lse_p[ri];
-      dlreg = delta_p[ri];
-      lrow_ok = row < Tq;  // applied at store time, when the loads have landed
-    }
-  };
-  auto store_q = [&](int buf) {
-#pragma unroll
-    for (int u = 0; u < UQ; ++u) {
-      const int idx = tid + u * 256;
-      const int r = idx / CH, c = idx % CH;
-      lds_write16(sQ + buf * QT + r * QS + c * 8, qreg[u]);
-      lds_write16(sdO + buf * QT + r * QS + c * 8, dreg[u]);
-    }
-    if (tid < BM) {
-      sL[buf * BM + tid] = lrow_ok ? lreg : kPosInf;
-      sDl[buf * BM + tid] = lrow_ok ? dlreg : 0.f;
-    }
-  };
-
-  f32x16 dk[NB], dv[NB];
-#pragma unroll
-  for (int nb = 0; nb < NB; ++nb) { dk[nb] = f32x16{}; dv[nb] = f32x16{}; }
-
-  if (iters > 0) {
-    load_q(0);
-    store_q(0);
-  }
-  __syncthreads();
-
-  for (int it = 0; it < iters; ++it) {
-    const int buf = it & 1;
-    int g, qt;
-    tile_of(it, g, qt);
-    const int h = kvh * a.G + g, qs = qt * BM;
-    if (it + 1 < iters) load_q(it + 1);
-    const T* Qs = sQ + buf * QT;
-    const T* dOs = sdO + buf * QT;
-    const bool active = !CAUSAL || (qs + BM - 1 >= kw0);
-    if (active) {
-      const bool edge = MASK || (CAUSAL && kw0 + 31 > qs);
-      const int kc = min(key, Tk - 1);
-      // The 64-row tile is processed as two 32-row halves to keep the S / dP
-      // accumulators at 32 registers.
-#pragma unroll
-      for (int qb = 0; qb < 2; ++qb) {
-        // ---- S = Q K^T, dP = dO V^T for rows 32 qb .. 32 qb + 31 -----------------
-        f32x16 sacc = f32x16{}, pacc = f32x16{};
-#pragma unroll
-        for (int ds = 0; ds < DS; ++ds) {
-          const u32x4 xq = lds_read16(Qs + (qb * 32 + l32) * QS + ds * 16 + hf * 8);
-          const u32x4 xd = lds_read16(dOs + (qb * 32 + l32) * QS + ds * 16 + hf * 8);
-          sacc = mfma32(as_vec8<T>(xq), kf[ds], sacc);
-          pacc = mfma32(as_vec8<T>(xd), vf[ds], pacc);
-        }
-        // lane's entry i is query qs + 32 qb + 8 (i/4) + 4 hf + i%4, key `key`
-
-        // ---- P and dS ----------------------------------------------------------
-#pragma unroll
-        for (int gi = 0; gi < 4; ++gi) {
-          const int qr0 = qb * 32 + gi * 8 + hf * 4;
-          const f32x4 L4 = *(const FA_LDS f32x4*)(uintptr_t)(sL + buf * BM + qr0);
-          const f32x4 D4 = *(const FA_LDS f32x4*)(uintptr_t)(sDl + buf * BM + qr0);
-#pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            const int i = gi * 4 + t;
-            const int q = qs + qr0 + t;
-            const int qc = min(q, Tq - 1);
-            float sv = sacc[i];
-            if constexpr (SCORE) {
-              const float sc = a.score[b * a.ssb + h * a.ssh + (int64_t)qc * a.ssq + kc];
-              sv += key < Tk ? sc : 0.f;
-            }
-            if (a.zero_scale) sv = 0.f;
-            float p = exp2_fast(fmaf(sv, c2, -L4[t]));
-            if (edge) {
-              bool keep = true;
-              if constexpr (CAUSAL) keep = key <= q;
-              if constexpr (MASK) keep = keep && key < Tk && a.mask[b * a.msb + h * a.msh + (int64_t)qc * a.msq + kc] != 0;
-              p = keep ? p : 0.f;
-            }
-            sacc[i] = p;
-            pacc[i] = p * (pacc[i] - D4[t]) * scale;
-          }
-        }
-
-        // ---- dV += P^T dO, dK += dS^T Q ------------------------------------------
-#pragma unroll
-        for (int c = 0; c < 2; ++c) {
-          const V8 pa = pack8<T>(sacc[8 * c + 0], sacc[8 * c + 1], sacc[8 * c + 2], sacc[8 * c + 3],
-                                 sacc[8 * c + 4], sacc[8 * c + 5], sacc[8 * c + 6], sacc[8 * c + 7]);
-          const V8 dsa = pack8<T>(pacc[8 * c + 0], pacc[8 * c + 1], pacc[8 * c + 2], pacc[8 * c + 3],
-                                  pacc[8 * c + 4], pacc[8 * c + 5], pacc[8 * c + 6], pacc[8 * c + 7]);
-          const int row = qb * 32 + 16 * c + 4 * hf + tr_row;
-#pragma unroll
-          for (int nb = 0; nb < NB; ++nb) {
-            const int col = nb * 32 + tr_col;
-            const V8 bo = cat_tr<T>(lds_read_tr(dOs + row * QS + col), lds_read_tr(dOs + (row + 8) * QS + col));
-            const V8 bq = cat_tr<T>(lds_read_tr(Qs + row * QS + col), lds_read_tr(Qs + (row + 8) * QS + col));
-            dv[nb] = mfma32(pa, bo, dv[nb]);
-            dk[nb] = mfma32(dsa, bq, dk[nb]);
-          }
-        }
-        if constexpr (DQ) {
-#pragma unroll
-          for (int gi = 0; gi < 4; ++gi)
-            lds_write8(sdS + (wave * 32 + l32) * SS + qb * 32 + gi * 8 + hf * 4,
-                       pack4<T>(pacc[gi * 4 + 0], pacc[gi * 4 + 1], pacc[gi * 4 + 2], pacc[gi * 4 + 3]));
-        }
-      }
-    } else if constexpr (DQ) {
-#pragma unroll
-      for (int qb = 0; qb < 2; ++qb)
-#pragma unroll
-        for (int gi = 0; gi < 4; ++gi)
-          lds_write8(sdS + (wave * 32 + l32) * SS + qb * 32 + gi * 8 + hf * 4, u32x2{0u, 0u});
-    }
-
-    if constexpr (DQ) {
-      __syncthreads();  // every wave's dS is in LDS
-      // ---- dQ = dS K over the workgroup's 128 keys, atomically added -----------
-      f32x16 acc[NPAIR];
-#pragma unroll
-      for (int pp = 0; pp < NPAIR; ++pp) {
-        const int qb = (wave * NPAIR + pp) & 1;
-        acc[pp] = f32x16{};
-#pragma unroll
-        for (int s = 0; s < 8; ++s) {
-          const int row = s * 16 + 8 * hf + tr_row;
-          const int col = qb * 32 + tr_col;
-          const V8 av = cat_tr<T>(lds_read_tr(sdS + row * SS + col), lds_read_tr(sdS + (row + 4) * SS + col));
-          acc[pp] = mfma32(av, ktf[s], acc[pp]);
-        }
-      }
-      // Stage the next tile before issuing the atomics: its wait on the
-      // prefetch loads then does not also wait for this tile's atomics.
-      if (it + 1 < iters) store_q(buf ^ 1);
-      // dq_accum is head-major [B, Hq, Tq, D]: consecutive query rows are D floats
-      // apart, so one wave's 16 row-segments spread over many L2 channels (a
-      // [B, Tq, Hq, D] layout puts them Hq*D*4 bytes apart, all aliasing).
-      const int64_t rs = D;
-#pragma unroll
-      for (int pp = 0; pp < NPAIR; ++pp) {
-        const int qb = (wave * NPAIR + pp) & 1;
-        float* dqp = a.dq_accum + (((int64_t)b * a.Hq + h) * Tq + qs + qb * 32 + 4 * hf) * D + db * 32 + l32;
-        if (qs + BM <= Tq) {
-#pragma unroll
-          for (int i = 0; i < 16; ++i) unsafeAtomicAdd(dqp + (8 * (i >> 2) + (i & 3)) * rs, acc[pp][i]);
-        } else {
-#pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const int q = qs + qb * 32 + 8 * (i >> 2) + 4 * hf + (i & 3);
-            if (q < Tq) unsafeAtomicAdd(dqp + (8 * (i >> 2) + (i & 3)) * rs, acc[pp][i]);
-          }
-        }
-      }
-    } else {
-      if (it + 1 < iters) store_q(buf ^ 1);
-    }
-    __syncthreads();
-  }
-
-  // ---- epilogue: dK, dV (dV of a kv-head with a dead row is NaN) ----------------
-  const bool dead = a.dead[b * a.Hk + kvh] != 0;
-  const float nanv = __builtin_nanf("");
-  if (a.split == 1) {
-    T* dkp = (T*)a.dk + b * a.dksb + kvh * a.dksh;
-    T* dvp = (T*)a.dv + b * a.dvsb + kvh * a.dvsh;
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int kr = kw0 + 8 * (i >> 2) + 4 * hf + (i & 3);
-        if (kr < Tk) {
-          dkp[(int64_t)kr * a.dkst + nb * 32 + l32] = (T)dk[nb][i];
-          dvp[(int64_t)kr * a.dvst + nb * 32 + l32] = (T)(dead ? nanv : dv[nb][i]);
-        }
-      }
-  } else {
-    // Head-group split: fp32 partials.  With atomic dQ they are added into one
-    // zeroed accumulator; on the deterministic path every split owns a slab
-    // [split][B, Tk, Hk, D] that the finalize step sums in a fixed order.
-    const int64_t slab = DQ ? 0 : (int64_t)sp * a.B * Tk * a.Hk * D;
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int kr = kw0 + 8 * (i >> 2) + 4 * hf + (i & 3);
-        if (kr < Tk) {
-          const int64_t o = slab + (((int64_t)b * Tk + kr) * a.Hk + kvh) * D + nb * 32 + l32;
-          if constexpr (DQ) {
-            unsafeAtomicAdd(a.dk_accum + o, dk[nb][i]);
-            unsafeAtomicAdd(a.dv_accum + o, dead ? nanv : dv[nb][i]);
-          } else {
-            a.dk_accum[o] = dk[nb][i];
-            a.dv_accum[o] = dead ? nanv : dv[nb][i];
-          }
-        }
-      }
-  }
-}
-
-// ---------------------------------------------------------------------------
 // deterministic dQ
 // ---------------------------------------------------------------------------
 constexpr int kDqBM = 128;   // query rows per workgroup (4 waves x 32)
 constexpr int kDqBN = 64;    // keys per tile
 
+// Without a mask or a score two workgroups share a CU (256 registers per
+// wave, a dozen spilled): one wave's MFMAs overlap the other's softmax and
+// dS work, which a lone wave issues in sequence (H: 2.53 -> 1.82 ms, causal
+// 1.47 -> 0.97).  The masked and score instances (P and dS in two parts)
+// keep one wave per SIMD: 256 registers would spill about a hundred.
 template <typename T, int D, bool CAUSAL, bool MASK, bool SCORE>
-__global__ __launch_bounds__(256, 1) void dq_kernel(const BwdArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((MASK || SCORE) ? 1 : 2, (MASK || SCORE) ? 1 : 2)))
+void dq_kernel(const BwdArgs a) {
   using V8 = typename Vec8<T>::type;
   static_assert(D <= 128, "head dim 256 recomputes dQ in fa_wide.hip");
   constexpr int BM = kDqBM, BN = kDqBN;
@@ -704,23 +368,6 @@ __global__ __launch_bounds__(256) void convert_kernel(const CvtArgs a) {
   }
 }
 
-template <typename T, int D, bool CAUSAL, bool DQ>
-hipError_t launch_dkdv_t(const BwdArgs& a, hipStream_t s) {
-  const dim3 grid((unsigned)(a.B * a.Hk * a.nkt * a.split)), block(256);
-  const bool m = a.mask != nullptr, sc = a.score != nullptr;
-  if (m && sc) hipLaunchKernelGGL((dkdv_kernel<T, D, CAUSAL, true, true, DQ>), grid, block, 0, s, a);
-  else if (m) hipLaunchKernelGGL((dkdv_kernel<T, D, CAUSAL, true, false, DQ>), grid, block, 0, s, a);
-  else if (sc) hipLaunchKernelGGL((dkdv_kernel<T, D, CAUSAL, false, true, DQ>), grid, block, 0, s, a);
-  else hipLaunchKernelGGL((dkdv_kernel<T, D, CAUSAL, false, false, DQ>), grid, block, 0, s, a);
-  return hipGetLastError();
-}
-
-template <typename T, int D>
-hipError_t launch_dkdv_d(const BwdArgs& a, bool causal, hipStream_t s) {
-  if (a.do_dq) return causal ? launch_dkdv_t<T, D, true, true>(a, s) : launch_dkdv_t<T, D, false, true>(a, s);
-  return causal ? launch_dkdv_t<T, D, true, false>(a, s) : launch_dkdv_t<T, D, false, false>(a, s);
-}
-
 template <typename T, int D, bool CAUSAL>
 hipError_t launch_dq_t(const BwdArgs& a, hipStream_t s) {
   const dim3 grid((unsigned)(a.B * a.Hq * a.nqt)), block(256);
@@ -744,22 +391,10 @@ hipError_t launch_pre_t(const PreArgs& a, int D, hipStream_t s) {
 
 }  // namespace
 
-int dkdv_block_keys() { return kKvBN; }
 int dq_block_rows() { return kDqBM; }
 
 hipError_t launch_preprocess(const PreArgs& a, int D, int dtype, hipStream_t s) {
   return dtype == 0 ? launch_pre_t<bf16>(a, D, s) : launch_pre_t<f16>(a, D, s);
-}
-
-hipError_t launch_bwd_dkdv(const BwdArgs& a, int D, int dtype, bool causal, hipStream_t s) {
-  if (dtype == 0) {
-    if (D == 128) return launch_dkdv_d<bf16, 128>(a, causal, s);
-    if (D == 64) return launch_dkdv_d<bf16, 64>(a, causal, s);
-  } else {
-    if (D == 128) return launch_dkdv_d<f16, 128>(a, causal, s);
-    if (D == 64) return launch_dkdv_d<f16, 64>(a, causal, s);
-  }
-  return hipErrorInvalidValue;
 }
 
 hipError_t launch_bwd_dq(const BwdArgs& a, int D, int dtype, bool causal, hipStream_t s) {

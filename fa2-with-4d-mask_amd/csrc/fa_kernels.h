@@ -162,8 +162,8 @@ struct BwdArgs {
   int nqt;              // query tiles per (b, h) (dQ kernel)
   int dq_rows;          // query rows per dQ-from-dS workgroup: kDqDsRows or kDqDsRowsWide
   int split;            // query-head-group split of the dK/dV kernel
-  int do_dq;            // dQ accumulated with fp32 atomics into dq_accum (fused in the dK/dV
-                        // kernel, or by the dQ-from-dS kernel over dq_split key ranges)
+  int do_dq;            // dQ accumulated with fp32 atomics into dq_accum (by the dQ-from-dS
+                        // kernel over dq_split key ranges)
   int dq_split;         // key ranges of the atomic dQ-from-dS kernel
   float scale;          // softmax scale (dS multiplier)
   float scale_log2;     // |scale| * log2(e)  (1 when zero_scale)
@@ -200,7 +200,6 @@ struct CvtArgs {
 
 hipError_t launch_fwd(const FwdArgs& a, int D, int dtype, bool causal, hipStream_t s);
 hipError_t launch_preprocess(const PreArgs& a, int D, int dtype, hipStream_t s);
-hipError_t launch_bwd_dkdv(const BwdArgs& a, int D, int dtype, bool causal, hipStream_t s);
 hipError_t launch_bwd_dq(const BwdArgs& a, int D, int dtype, bool causal, hipStream_t s);
 // dK/dV of the deterministic path (no dQ), 4 waves x 32 keys per workgroup.
 hipError_t launch_bwd_dkdv2(const BwdArgs& a, int D, int dtype, bool causal, hipStream_t s);

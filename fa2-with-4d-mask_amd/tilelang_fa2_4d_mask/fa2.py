@@ -320,9 +320,8 @@ def _backward_impl(do, q, k, v, O, LSE, mask, score, mask_ws, mst, sst, scale: f
     dq_acc = torch.empty((B, Tq, Hq, D), dtype=torch.float32, device=dev) if plan.needs_dq_accum else None
     dk_acc = dv_acc = None
     if plan.dkv_accum_elems > 0:
-        # fused atomic kernel: zeroed accumulators; otherwise one fully
-        # overwritten fp32 slab per head-group split, or the running sums of
-        # a backward over row ranges.
+        # one fully overwritten fp32 slab per head-group part, or the running
+        # sums of a backward over row ranges (zeroed only if the plan asks)
         alloc = torch.zeros if plan.dkv_accum_zeroed else torch.empty
         dk_acc = alloc((plan.dkv_accum_elems,), dtype=torch.float32, device=dev)
         dv_acc = alloc((plan.dkv_accum_elems,), dtype=torch.float32, device=dev)

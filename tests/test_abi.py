@@ -178,7 +178,7 @@ def test_noalloc_validation(lib, over, code, msg):
 
 
 BWD_ERRORS = [
-    (dict(dq_accum=None, ds_limit_bytes=-1), 8, "needs dq_accum"),   # fused atomic kernel
+    (dict(dq_accum=None, seqlen_q=2048, seqlen_k=2048, heads_q=16, heads_k=2), 8, "needs dq_accum"),   # dq_split 8
     (dict(dq_accum=None, seqlen_q=1024, seqlen_k=1024, heads_q=16, heads_k=2), 8, "needs dq_accum"),
     (dict(kv_split=3), 2, "must divide"),
     (dict(kv_split=2), 8, "needs dk_accum"),
@@ -213,13 +213,13 @@ def _plan(lib, **over):
 
 def test_plan_headline_needs_no_split(lib):
     # atomic mode at the headline: 1024 dQ row blocks (>= one per CU) each
-    # own their rows, so no fp32 accumulator; the fused atomic kernel (no dS
-    # workspace) needs one
+    # own their rows, so no fp32 accumulator; without a dS workspace dQ is
+    # recomputed in both modes, no accumulator either
     plan = _plan(lib)
     assert plan.kv_split == 1 and plan.needs_dq_accum == 0 and plan.dq_split == 1
     assert plan.dq_accum_elems == 0 and plan.dkv_accum_elems == 0
     plan = _plan(lib, ds_limit_bytes=-1)
-    assert plan.needs_dq_accum == 1 and plan.dq_accum_elems == 8192 * 32 * 128
+    assert plan.needs_dq_accum == 0 and plan.dq_accum_elems == 0 and plan.ds_elems == 0
     plan = _plan(lib, atomic_dq=0)
     assert plan.needs_dq_accum == 0 and plan.dq_accum_elems == 0
 
@@ -238,7 +238,7 @@ def test_plan_ds_tiles(lib):
     assert plan.dq_split == 8 and plan.needs_dq_accum == 1 and plan.dq_accum_elems == 2048 * 16 * 128
     assert _plan(lib, atomic_dq=0, **small).dq_split == 1
     assert _plan(lib, atomic_dq=0).dq_split == 1
-    # ... and falls back to the fused atomic kernel when it does not
+    # ... and recomputes dQ when it does not
     plan = _plan(lib, ds_limit_bytes=-1)
     assert plan.ds_elems == 0 and plan.dq_split == 1
     plan = _plan(lib, atomic_dq=0, is_causal=1)
@@ -365,9 +365,9 @@ def test_plan_mqa_splits_the_group(lib):
         plan = _plan(lib, atomic_dq=atomic, **m)
         assert plan.kv_split == 4 and plan.dkv_accum_elems == 4 * 16384 * 64 and plan.dkv_accum_zeroed == 0
     assert _plan(lib, **m).dq_split == 1   # 256 dQ row blocks: one per CU, rows owned, no atomics
-    # fused atomic kernel (no dS workspace): one zeroed accumulator
+    # no dS workspace (dQ recomputed): the same split and slabs, nothing to zero
     plan = _plan(lib, ds_limit_bytes=-1, **m)
-    assert plan.kv_split == 4 and plan.dkv_accum_elems == 16384 * 64 and plan.dkv_accum_zeroed == 1
+    assert plan.kv_split == 4 and plan.dkv_accum_elems == 4 * 16384 * 64 and plan.dkv_accum_zeroed == 0
     plan = _plan(lib, kv_split=8, **m)
     assert plan.kv_split == 8
 

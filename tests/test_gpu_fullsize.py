@@ -124,8 +124,8 @@ def check(ours, ref, rnd, label, strict):
                 failures.append(f"{name}: misses the north-star bar (max {err.max().item():.3e}, mean {mean:.3e})")
         elif not met:
             # a floor cell that meets the bar against eager needs no floor
-            # argument (the fused atomic route rounds dS at another point than
-            # the restatement and lands inside the bar at H causal)
+            # argument (a route that rounds dS at another point than the
+            # restatement can land inside the bar)
             if derr.max().item() > MAX_ABS or derr.mean().item() > MEAN_ABS:
                 failures.append(f"{name}: not within the north-star bar of the rounding restatement")
             if mean > 1.05 * rmean + 1e-7 or over > rover:
@@ -189,19 +189,19 @@ NO_WS_CASES = [("H", True), ("H", False), ("H_causal", True), ("H_causal", False
 
 
 @pytest.mark.parametrize("name,atomic", NO_WS_CASES,
-                         ids=[f"{n}-{'fused_atomic' if a else 'recompute'}" for n, a in NO_WS_CASES])
+                         ids=[f"{n}-{'atomic' if a else 'det'}" for n, a in NO_WS_CASES])
 def test_fullsize_without_ds_workspace(cuda, name, atomic):
-    """The backward routes that keep memory O(T) (no dS workspace allowed):
-    atomic mode runs the fused dK/dV kernel that adds dQ with fp32 atomics,
-    the deterministic mode a dQ kernel that recomputes S, P and dP; with a
-    mask or a score both modes take the recompute route, whose kernels carry
-    P and dS in several 16-bit parts (P and S here: the strict cells).  The
-    library falls back to them when the dS tiles do not fit the limit; here
-    they are forced and held to the same cells as the default route."""
+    """The backward route that keeps memory O(T) (no dS workspace allowed),
+    in both modes: the dK/dV kernel, then a dQ kernel that recomputes S, P
+    and dP (no atomics); with a mask or a score its kernels carry P and dS in
+    several 16-bit parts (P and S here: the strict cells).  The library
+    falls back to it when the dS tiles do not fit the limit (nor a slice,
+    range or part of them); here it is forced and held to the same cells as
+    the default route."""
     import tilelang_fa2_4d_mask.fa2 as fa2mod
 
     cfg = I.CONFIGS[name]
-    route = "fused atomic" if atomic and cfg.mask is None and cfg.score is None else "recompute"
+    route = "recompute"
     print(f"case {name} no dS workspace ({route}) B{cfg.B} T{cfg.Tq} Hq{cfg.Hq} Hk{cfg.Hk} D{cfg.D}", flush=True)
     case = I.make_case(cfg, seed=4, device=cuda)
     fa2mod.DS_LIMIT_BYTES = -1

@@ -68,8 +68,8 @@ def _one_plane_limit(cfg):
 
 def run_ours(case, cfg, *, atomic=True, scale=None, attention_mask=None, backward=True, ds_limit=0):
     """ds_limit: dS workspace limit of the backward (0 = default, dQ from the
-    stored dS tiles; -1 = no workspace: dQ recomputed (deterministic) or fused
-    fp32 atomics; "unit" = one (batch, kv-head) unit: the dS kernels run once
+    stored dS tiles; -1 = no workspace: dQ recomputed, in both modes;
+    "unit" = one (batch, kv-head) unit: the dS kernels run once
     per unit; "rows" = one 512-row range of every unit, see _rows_limit;
     "plane" = one (batch, head) plane, see _one_plane_limit)."""
     api = _api()
@@ -184,16 +184,16 @@ SMALL = [
 
 
 # backward modes: fp32-atomic dQ over key ranges of the stored dS (default);
-# fp32-atomic dQ fused into the dK/dV kernel (no dS workspace); deterministic
-# with dQ from the stored dS tiles; deterministic with dQ recomputed (no dS
-# workspace allowed); both dS modes with a workspace of one (batch, kv-head)
+# atomic mode without a dS workspace (dQ recomputed, as in the deterministic
+# mode); deterministic with dQ from the stored dS tiles; deterministic with dQ
+# recomputed (no dS workspace allowed); both dS modes with a workspace of one (batch, kv-head)
 # unit, so that the dS kernels run slice by slice (sized without the tile
 # pairs of a mask or score: half a unit there, so a masked group splits in
 # two); both with a workspace of one 512-row range of every unit (ranges of
 # rows where Tq > 512 B Hk without a mask; unit slices or recompute
 # otherwise); both with a workspace of one (batch, head) plane (a masked
 # head group then splits into one-head parts)
-MODES = {"atomic": (True, 0), "atomic_fused": (True, -1), "det_ds": (False, 0), "det_recompute": (False, -1),
+MODES = {"atomic": (True, 0), "atomic_no_ws": (True, -1), "det_ds": (False, 0), "det_recompute": (False, -1),
          "atomic_sliced": (True, "unit"), "det_sliced": (False, "unit"),
          "atomic_rows": (True, "rows"), "det_rows": (False, "rows"),
          "atomic_parts": (True, "plane"), "det_parts": (False, "plane")}
@@ -535,7 +535,7 @@ def test_bhsd_contiguous_inputs(cuda):
     check(ours, run_oracle_cpu(case, cfg), label="bhsd-contiguous")
 
 
-@pytest.mark.parametrize("mode", ["atomic", "det_ds", "atomic_fused", "det_recompute"])
+@pytest.mark.parametrize("mode", ["atomic", "det_ds", "atomic_no_ws", "det_recompute"])
 def test_tiny_lengths(cuda, mode):
     # Boundary/indexing test (an indexing bug gives O(1) errors).  With a few
     # hundred entries per output the mean is dominated by single bf16 rounding
@@ -664,7 +664,7 @@ WIDE_D = [
 ]
 
 
-@pytest.mark.parametrize("mode", ["atomic", "det_ds", "atomic_fused"])
+@pytest.mark.parametrize("mode", ["atomic", "det_ds", "atomic_no_ws"])
 @pytest.mark.parametrize("cfg", WIDE_D, ids=[c.name for c in WIDE_D])
 def test_head_dim_256(cuda, cfg, mode):
     """Output and gradients at head dims above 128 against the CPU oracle and
