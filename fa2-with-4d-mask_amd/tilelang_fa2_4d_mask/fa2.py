@@ -49,7 +49,9 @@ from . import _ext
 # head-group split depend on the problem alone: calls are bitwise repeatable
 # whatever the allocator holds); negative = never (dQ is then recomputed from
 # Q, K, V, dO: O(T) extra memory, as the reference's backward).  Below the
-# whole need the backward runs in slices of (batch, kv-head) units.
+# whole need the backward runs in slices of (batch, kv-head) units, ranges of
+# query rows (causal, or a unit above the limit; no mask) or parts of head
+# groups (a unit above the limit, with a mask).
 DS_LIMIT_BYTES = 0
 DS_LIMIT_DEFAULT = 4 << 30
 

@@ -144,11 +144,11 @@ typedef struct FaBwdPlan {
   int32_t kv_split;              /* >1: dK/dV of each head-group part go to fp32 dk_accum/dv_accum slabs,
                                     summed by fa_bwd_finalize */
   int32_t needs_dq_accum;        /* 1 if dq_accum is used: dQ added with fp32 atomics (atomic_dq = 1 and
-                                    dq_split > 1, or the fused kernel); else dQ is written directly */
+                                    dq_split > 1); else dQ is written directly */
   int64_t dq_accum_elems;        /* B*Tq*Hq*D when used, else 0 */
-  int64_t dkv_accum_elems;       /* kv_split > 1: B*Tk*Hk*D per slab (kv_split slabs; one for the fused
-                                    kernel); ranges of query rows (ds_elems): B*Tk*Hk*D, the running
-                                    sums, written by the first range; else 0 */
+  int64_t dkv_accum_elems;       /* kv_split > 1: B*Tk*Hk*D per slab (kv_split slabs); ranges of query
+                                    rows (ds_elems) at kv_split 1: B*Tk*Hk*D, the running sums; written
+                                    by the kernels (first range), never read before; else 0 */
   int64_t ds_elems;              /* size of ds_tiles: 16-bit dS of every stored 32x32 block of all
                                     (batch, kv-head) units when they fit ds_limit_bytes; else of a slice
                                     of as many units as fit (nearly equal slices, run one after the
@@ -159,10 +159,8 @@ typedef struct FaBwdPlan {
                                     at once; with a mask, of as many one-head parts of a unit's group
                                     as fit (kv_split = the group size, one slab per part).  0 when
                                     not even one unit, 512-row range, nor (with a mask) plane fits:
-                                    dQ is then recomputed (atomic_dq = 0, or with a mask or a score) or
-                                    added per key block by the fused dK/dV kernel (atomic_dq = 1 without
-                                    mask and score) */
-  int32_t dkv_accum_zeroed;      /* 1: dk_accum/dv_accum must be zeroed by the caller (fused atomic kernel) */
+                                    dQ is then recomputed, in both modes */
+  int32_t dkv_accum_zeroed;      /* 1: dk_accum/dv_accum must be zeroed by the caller (0 in this ABI) */
   int32_t dq_split;              /* atomic_dq = 1 with dS tiles: key ranges whose dQ partials are added
                                     (2-8) when the 256-row query blocks are fewer than the CUs; 1: each
                                     block writes its rows, no atomics (as atomic_dq = 0) */
@@ -203,19 +201,16 @@ int fa_bwd_preprocess(const FaBwdParams* p);
  * kernel, writing dK/dV in dtype (kv_split = 1) or per-split fp32 slabs, and
  * storing dS into ds_tiles for fa_bwd_finalize (when ds_tiles holds a slice of the
  * (batch, kv-head) units, fa_bwd runs the dK/dV and the dQ kernel per slice and
- * fa_bwd_finalize only converts).  With plan.ds_elems = 0 and
- * atomic_dq = 1 without mask and score: one fused kernel that also adds dQ
- * into dq_accum with fp32 atomics (dK/dV added into zeroed dk_accum/dv_accum
- * when kv_split > 1); otherwise (atomic_dq = 0, or a mask or a score): the
- * dK/dV kernel only.  Must follow fa_bwd_preprocess on the same stream. */
+ * fa_bwd_finalize only converts; likewise over ranges of query rows, or parts of
+ * the head groups).  With plan.ds_elems = 0 (both modes): the dK/dV kernel only.
+ * Must follow fa_bwd_preprocess on the same stream. */
 int fa_bwd(const FaBwdParams* p);
 
 /* Backward finalisation.  dQ: from ds_tiles, dQ = scale dS K, written in dtype
  * (atomic_dq = 0, or plan.dq_split = 1) or added as fp32 partials over
  * plan.dq_split key ranges into dq_accum with atomics and converted (atomic_dq = 1,
  * plan.dq_split > 1); without ds_tiles,
- * recomputed from S, P and dP (atomic_dq = 0, or a mask or a score) or converted
- * from the dq_accum the fused kernel filled (atomic_dq = 1 without them).  dk, dv from dk_accum/dv_accum when
+ * recomputed from S, P and dP (both modes).  dk, dv from dk_accum/dv_accum when
  * kv_split > 1.  Replaces the casts of python/fa2.py:535-536, the group sum of
  * python/fa2.py:548-549 and autograd's cast of the fp32 dQ the reference returns
  * (python/fa2.py:527, 556); the dS-based dQ replaces the per-64-key dQ atomics of
