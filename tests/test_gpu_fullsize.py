@@ -209,7 +209,8 @@ def test_fullsize_without_ds_workspace(cuda, name, atomic):
         ours = run_ours(case, cfg, atomic=atomic)
     finally:
         fa2mod.DS_LIMIT_BYTES = 0
-    check(ours, run_oracle(case, cfg), run_rounded(case, cfg), f"{name}/no-ws/{route}", STRICT[name])
+    check(ours, run_oracle(case, cfg), run_rounded(case, cfg), f"{name}/no-ws/{'atomic' if atomic else 'det'}",
+          STRICT[name])
 
 
 def test_fullsize_deterministic_repeatable(cuda):
