@@ -242,6 +242,9 @@ ROWS = [
     C("rows_gqa_ragged", 1, 2100, 600, 4, 2, 128),
     C("rows_score_d64", 1, 1100, 700, 2, 1, 64, score="normal"),
     C("rows_fp16_bshd_causal", 1, 1200, 1000, 8, 1, 128, torch.float16, layout="bshd", is_causal=True),
+    # causal with Tq < Tk: key blocks past the last row get no step in any
+    # range (their sums stay 0 and dK/dV come out 0)
+    C("rows_causal_tq_lt_tk", 1, 1100, 1700, 4, 1, 128, is_causal=True),
 ]
 
 
@@ -290,6 +293,8 @@ PARTS = [
       score="normal"),
     C("parts_mask_g3_fp16_bshd", 1, 300, 333, 6, 2, 128, torch.float16, layout="bshd", mask="bernoulli",
       mask_heads=1),
+    # causal with Tq < Tk and a per-head mask: key blocks without a live step
+    C("parts_mask_causal_tq_lt_tk", 1, 200, 450, 4, 2, 64, is_causal=True, mask="bernoulli"),
 ]
 
 
