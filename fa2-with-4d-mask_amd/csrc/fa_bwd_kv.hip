@@ -165,7 +165,7 @@ __global__ __launch_bounds__(kKvWaves * 64, 1) __attribute__((amdgpu_waves_per_e
   // broadcast over them).  A scalar load per step instead cost a wait for
   // all of the wave's loads each step.
   const bool shared_list = MASK && a.ml.Hm == 1;
-  int32_t lreg_v[MASK ? 2 : 1] = {};
+  int32_t lreg_v[2] = {};   // unused without a mask
   int win_h = -1, win_base = -128;
   auto win_load = [&](int h, int base) __attribute__((always_inline)) {
     const int32_t* l = kv_list(h);
