@@ -26,6 +26,10 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
+// 64-bit minimum: the HIP headers' min overloads differ between the host and
+// device passes (the host pass picks min(int, int) for two int64_t).
+__host__ __device__ __forceinline__ int64_t min_i64(int64_t x, int64_t y) { return x < y ? x : y; }
+
 template <typename T> struct Vec8;
 template <> struct Vec8<bf16> { typedef bf16x8 type; };
 template <> struct Vec8<f16> { typedef f16x8 type; };

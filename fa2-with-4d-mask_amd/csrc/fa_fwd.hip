@@ -214,7 +214,7 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
   // p .. p+3).
   constexpr bool ENTV = MASK;
   constexpr bool MPRE = MASK && !SCORE;   // mask bits fetched a pair ahead (no registers to spare with a score)
-  int32_t ents[ENTV ? 2 : 1] = {};
+  int32_t ents[2] = {};   // unused without a mask
   int ebase = 0;
   // range-checked loads (positions past the row read 0): no wait on the count
   const auto rl = __builtin_amdgcn_make_buffer_rsrc((void*)flist, (short)0, MASK ? (1 + a.ml.nft) * 4 : 0, 0x00020000);
@@ -271,7 +271,7 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
     const T* tb = base;
     if (valid) {
       const int64_t rows = min(Tk - t * BN, BN);
-      nrec = (uint32_t)min((rows - 1) * st * 2 + ROWB, (int64_t)0xfffffff0);
+      nrec = (uint32_t)min_i64((rows - 1) * st * 2 + ROWB, 0xfffffff0);
       tb = base + (int64_t)t * BN * st;
     }
     return __builtin_amdgcn_make_buffer_rsrc((void*)tb, (short)0, (int)nrec, 0x00020000);
@@ -286,7 +286,7 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_kernel(const FwdArgs a) {
   // issued in the softmax phase, whose instruction issue bounds the step.
   const int nt_full = min(nt, Tk / BN);   // tiles [0, nt_full) are whole
   auto nrec_of = [&](int64_t st) __attribute__((always_inline)) -> uint32_t {
-    return (uint32_t)min((int64_t)(BN - 1) * st * 2 + ROWB, (int64_t)0xfffffff0);
+    return (uint32_t)min_i64((int64_t)(BN - 1) * st * 2 + ROWB, 0xfffffff0);
   };
   const uint32_t nrec_k = nrec_of(a.kst), nrec_v = nrec_of(a.vst);
   const uint32_t tail_k = (uint32_t)((int64_t)(Tk - nt_full * BN - 1) * a.kst * 2 + ROWB);
