@@ -1,11 +1,22 @@
 #!/usr/bin/env python3
-"""Builds libfa2_4d_mask.so (gfx950) in-tree with hipcc.
+r"""Builds libfa2_4d_mask.so (gfx950) in-tree with hipcc.
 
-Usage: python fa2-with-4d-mask_amd/build_ext.py [--jobs N] [--verbose]
+Usage: python fa2-with-4d-mask_amd/build_ext.py [--jobs N] [--verbose] [--host-sanitize]
 
 Objects go to fa2-with-4d-mask_amd/_build/, the shared library to
 fa2-with-4d-mask_amd/tilelang_fa2_4d_mask/_lib/libfa2_4d_mask.so, which is
 where the package's loader looks for it.
+
+--host-sanitize builds the same library with its host code (the C ABI's
+validation, planning and launch code) under AddressSanitizer and
+UndefinedBehaviorSanitizer -- the device code is built as usual -- into
+fa2-with-4d-mask_amd/_build_hostsan/libfa2_4d_mask_hostsan.so.  The CPU tests
+run against it with the sanitizer runtime loaded first:
+
+  LD_PRELOAD=$(/opt/rocm/llvm/bin/clang++ -print-file-name=libclang_rt.asan-x86_64.so) \
+  ASAN_OPTIONS=detect_leaks=0 UBSAN_OPTIONS=halt_on_error=1 \
+  FA2_4D_MASK_LIB=fa2-with-4d-mask_amd/_build_hostsan/libfa2_4d_mask_hostsan.so \
+  python -m pytest tests -m "not gpu"
 """
 
 from __future__ import annotations
@@ -23,6 +34,12 @@ CSRC = HERE / "csrc"
 BUILD = HERE / "_build"
 LIBDIR = HERE / "tilelang_fa2_4d_mask" / "_lib"
 LIB = LIBDIR / "libfa2_4d_mask.so"
+BUILD_SAN = HERE / "_build_hostsan"
+LIB_SAN = BUILD_SAN / "libfa2_4d_mask_hostsan.so"
+# Host-only sanitizers: each flag applies to the host compilation alone.
+HOST_SANITIZE = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined",
+                 "-Xarch_host", "-fno-sanitize-recover=undefined", "-Xarch_host", "-fno-omit-frame-pointer",
+                 "-Xarch_host", "-g"]
 SOURCES = ["fa_fwd.hip", "fa_bwd.hip", "fa_bwd_kv.hip", "fa_bwd_dq.hip", "fa_wide.hip", "fa_mask.hip", "fa_noalloc.hip",
            "fa_api.cpp"]
 # Per-file extra flags.  fa_bwd_kv.hip keeps its dK/dV accumulators in AGPRs
@@ -64,31 +81,43 @@ def _run(cmd: list[str], verbose: bool) -> None:
         print(out, flush=True)
 
 
-def build(jobs: int = 4, verbose: bool = False) -> Path:
-    BUILD.mkdir(exist_ok=True)
-    LIBDIR.mkdir(exist_ok=True)
+def build(jobs: int = 4, verbose: bool = False, host_sanitize: bool = False) -> Path:
+    out_dir, lib = (BUILD_SAN, LIB_SAN) if host_sanitize else (BUILD, LIB)
+    out_dir.mkdir(exist_ok=True)
+    lib.parent.mkdir(exist_ok=True)
     cc = hipcc()
-    flags = compile_flags()
+    flags = compile_flags() + (HOST_SANITIZE if host_sanitize else [])
 
     def obj(src: str) -> Path:
-        o = BUILD / (Path(src).stem + ".o")
+        o = out_dir / (Path(src).stem + ".o")
         _run([cc, *flags, *EXTRA_FLAGS.get(src, []), "-c", str(CSRC / src), "-o", str(o)], verbose)
         return o
 
     with ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
         objs = list(ex.map(obj, SOURCES))
-    tmp = LIB.with_suffix(".so.tmp")
-    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)], verbose)
-    os.replace(tmp, LIB)
-    return LIB
+    tmp = lib.with_suffix(".so.tmp")
+    if host_sanitize:
+        # host link against the shared sanitizer runtime (the device code is
+        # already embedded in each object)
+        rocm = Path(cc).resolve().parent.parent
+        link = [str(rocm / "llvm" / "bin" / "clang++"), "-shared", "-fPIC", "-shared-libsan",
+                "-fsanitize=address,undefined", *map(str, objs), f"-L{rocm / 'lib'}", "-lamdhip64",
+                f"-Wl,-rpath,{rocm / 'lib'}", "-o", str(tmp)]
+        _run(link, verbose)
+    else:
+        _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)], verbose)
+    os.replace(tmp, lib)
+    return lib
 
 
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--jobs", type=int, default=4)
     ap.add_argument("--verbose", action="store_true")
+    ap.add_argument("--host-sanitize", action="store_true",
+                    help="host code under ASan + UBSan, into _build_hostsan/ (see the module docstring)")
     args = ap.parse_args()
-    lib = build(args.jobs, args.verbose)
+    lib = build(args.jobs, args.verbose, args.host_sanitize)
     print(f"built {lib}")
     return 0
 

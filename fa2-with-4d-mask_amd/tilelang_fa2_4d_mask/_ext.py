@@ -2,7 +2,10 @@
 
 The library is loaded lazily on first use and must have been built in-tree
 (``python fa2-with-4d-mask_amd/build_ext.py``).  There is no fallback: a
-missing or unloadable library raises ``RuntimeError``.
+missing or unloadable library raises ``RuntimeError``.  The environment
+variable ``FA2_4D_MASK_LIB`` names another build of the same library to load
+instead (for instance the host-sanitized one that ``build_ext.py
+--host-sanitize`` writes).
 
 torch is imported before the library is loaded so that the library binds to
 the HIP runtime torch already holds (same SONAME), which keeps torch's stream
@@ -18,7 +21,8 @@ from pathlib import Path
 
 import torch  # noqa: F401  (must be loaded before the HIP library, see above)
 
-LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libfa2_4d_mask.so"
+LIB_PATH = (Path(os.environ["FA2_4D_MASK_LIB"]) if os.environ.get("FA2_4D_MASK_LIB")
+            else Path(__file__).resolve().parent / "_lib" / "libfa2_4d_mask.so")
 ABI_VERSION = 6
 
 FA_DTYPE_BF16 = 0

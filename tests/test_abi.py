@@ -392,6 +392,24 @@ def test_missing_library_fails_loudly(tmp_path):
         _ext().load_library(tmp_path / "nope.so")
 
 
+def test_library_path_override(tmp_path):
+    """FA2_4D_MASK_LIB names the build to load; a missing one raises, with no
+    fallback to the in-tree library (checked in a fresh interpreter, since the
+    path is read at import)."""
+    import os
+    import sys
+    pkg = Path(__file__).resolve().parents[1] / "fa2-with-4d-mask_amd"
+    code = ("import sys; sys.path.insert(0, %r)\n"
+            "from tilelang_fa2_4d_mask import _ext\n"
+            "print(_ext.LIB_PATH)\n"
+            "try:\n    _ext.load_library()\nexcept RuntimeError as e:\n    print('raised', 'not built' in str(e))\n") % str(pkg)
+    env = dict(os.environ, FA2_4D_MASK_LIB=str(tmp_path / "other.so"))
+    r = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr
+    lines = r.stdout.strip().splitlines()
+    assert lines[-2] == str(tmp_path / "other.so") and lines[-1] == "raised True", r.stdout
+
+
 def mask_params(**over):
     ext = _ext()
     p = ext.FaMaskParams()
