@@ -20,8 +20,8 @@ Checks:
   parameter.
 
 With left padding, transformers' masks leave the padding query rows with no kept
-key.  Under the eager semantics the build follows (as the reference's
-eager restatement and its wrapper), such a row's output is NaN and the dV of its
+key.  Under the eager semantics the build follows (the reference's eager
+attention, benchmark/precision_check.py:133-180), such a row's output is NaN and the dV of its
 kv-head is NaN; a NaN row then reaches the next layer as a masked key whose V is
 NaN (0 x NaN = NaN in P V, in eager attention too).  The padding cases therefore
 run one layer and check the forward only, on the non-padding tokens; padded
