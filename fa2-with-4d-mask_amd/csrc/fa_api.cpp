@@ -8,6 +8,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdarg>
+#include <cstdint>
 #include <cstdio>
 #include <cstring>
 #include <vector>
@@ -49,6 +50,18 @@ int check_operand(const char* name, const void* p, int64_t sb, int64_t st, int64
   return FA_OK;
 }
 
+// Rows of every head below 2^31 - 2^16: 32-bit row indices with room to
+// round any count up to a whole tile.
+constexpr int64_t kMaxRows = (1LL << 31) - (1LL << 16);
+// Products of non-negative sizes in the plans saturate at kSizeSat, so that
+// shapes whose dS tiles no device could hold still plan (to the recompute
+// route) with defined arithmetic; kSizeSat leaves room for doubling and sums.
+constexpr int64_t kSizeSat = INT64_MAX / 8;
+int64_t sat_mul(int64_t a, int64_t b) {
+  if (a == 0 || b == 0) return 0;
+  return a > kSizeSat / b ? kSizeSat : std::min(a * b, kSizeSat);
+}
+
 int check_dims(int32_t B, int32_t Tq, int32_t Tk, int32_t Hq, int32_t Hk, int32_t D, int32_t dtype, float scale) {
   if (B < 1 || Tq < 1 || Tk < 1 || Hq < 1 || Hk < 1)
     return fail(FA_ERR_SHAPE, "sizes must be >= 1 (B=%d Tq=%d Tk=%d Hq=%d Hk=%d)", B, Tq, Tk, Hq, Hk);
@@ -57,9 +70,10 @@ int check_dims(int32_t B, int32_t Tq, int32_t Tk, int32_t Hq, int32_t Hk, int32_
   if (D != 64 && D != 128 && D != 256) return fail(FA_ERR_HEAD_DIM, "head_dim %d not supported (64, 128, 256)", D);
   if (dtype != FA_DTYPE_BF16 && dtype != FA_DTYPE_FP16) return fail(FA_ERR_DTYPE, "unsupported dtype code %d", dtype);
   if (!std::isfinite(scale)) return fail(FA_ERR_SCALE, "scale must be finite");
-  // 32-bit indices inside the kernels: rows of every head must fit.
-  if ((int64_t)B * Hq * (int64_t)Tq >= (1LL << 31) || (int64_t)B * Hk * (int64_t)Tk >= (1LL << 31))
-    return fail(FA_ERR_SHAPE, "problem too large for 32-bit row indices");
+  // 32-bit indices inside the kernels and the host: rows of every head must
+  // fit, with room to round any of them up to a whole tile.
+  if ((int64_t)B * Hq * (int64_t)Tq >= kMaxRows || (int64_t)B * Hk * (int64_t)Tk >= kMaxRows)
+    return fail(FA_ERR_SHAPE, "problem too large for 32-bit row indices (B*H*T must stay below 2^31 - 2^16)");
   return FA_OK;
 }
 
@@ -103,9 +117,14 @@ constexpr int64_t kDsLimitDefault = (int64_t)4 << 30;
 int64_t ds_unit_elems(const FaBwdParams* p) {
   const int64_t nq32 = (p->seqlen_q + 31) / 32, nk32 = (p->seqlen_k + 31) / 32;
   const int64_t plane = fa::ds_row(nq32, nk32, p->is_causal != 0);
-  return (int64_t)(p->heads_q / p->heads_k) * plane * 1024 * ds_tile_parts(p);   // one unit: the group's planes
+  // one unit: the group's planes
+  return sat_mul(sat_mul(sat_mul(p->heads_q / p->heads_k, plane), 1024), ds_tile_parts(p));
 }
-int64_t ds_limit_of(const FaBwdParams* p) { return p->ds_limit_bytes == 0 ? kDsLimitDefault : p->ds_limit_bytes; }
+// The caller's limit, below kSizeSat / 4 (beyond any device): saturated sizes
+// then never fit it.
+int64_t ds_limit_of(const FaBwdParams* p) {
+  return p->ds_limit_bytes == 0 ? kDsLimitDefault : std::min<int64_t>(p->ds_limit_bytes, kSizeSat / 4);
+}
 
 // Row ranges.  Without a mask the dS route can run over ranges of query rows
 // instead of groups of units: each range's dK/dV launch covers every unit
@@ -124,8 +143,8 @@ constexpr int kRangeSteps = 16;
 int64_t range_bytes(const FaBwdParams* p, int lo, int hi) {
   const int64_t nk32 = (p->seqlen_k + 31) / 32;
   const bool causal = p->is_causal != 0;
-  return (int64_t)p->batch * p->heads_q * (fa::ds_row(hi, nk32, causal) - fa::ds_row(lo, nk32, causal)) * 1024 *
-         ds_tile_parts(p) * 2;
+  const int64_t steps = fa::ds_row(hi, nk32, causal) - fa::ds_row(lo, nk32, causal);
+  return sat_mul(sat_mul(sat_mul(sat_mul((int64_t)p->batch * p->heads_q, steps), 1024), ds_tile_parts(p)), 2);
 }
 // Greedy ranges of at most `cap` bytes: their count (-1 if one 512-row
 // chunk exceeds it); step bounds into `bounds` when given.

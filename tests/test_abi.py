@@ -138,6 +138,9 @@ FWD_ERRORS = [
     (dict(score=FAKE, score_stride_q=1 << 26), 5, "32 score rows"),
     (dict(mask=FAKE), 8, "prepared workspace"),
     (dict(mask=FAKE, mask_ws=FAKE + 16), 5, "mask_ws must be 256-byte aligned"),
+    # rows of every head below 2^31 - 2^16 (a tile round-up must not overflow)
+    (dict(heads_q=8, heads_k=8, seqlen_k=(1 << 28) - 64), 2, "32-bit row indices"),
+    (dict(heads_q=8, heads_k=8, seqlen_q=(1 << 28) - 64), 2, "32-bit row indices"),
 ]
 
 
@@ -385,6 +388,24 @@ def test_plan_head_dim_256_recomputes_dq(lib):
             assert plan.dkv_accum_elems == 2 * 4096 * 8 * 256
     plan = _plan(lib, atomic_dq=1, seqlen_q=8192, seqlen_k=8192, heads_q=8, heads_k=8, head_dim=256)
     assert plan.kv_split == 1 and plan.dkv_accum_elems == 0
+
+
+def test_plans_of_shapes_past_any_device(lib):
+    """Shapes just inside the row bound, whose dS tiles (2^62 bytes and more)
+    no device holds, still plan with defined arithmetic (the size products
+    saturate instead of overflowing): the recompute route under the default
+    and a negative limit; under a limit beyond any device (clamped to 2^58
+    bytes) a workspace within that clamp."""
+    big = dict(batch=1, heads_q=2, heads_k=1, seqlen_q=(1 << 30) - (1 << 16), seqlen_k=(1 << 31) - (1 << 17))
+    for causal in (0, 1):
+        for atomic in (0, 1):
+            for limit in (0, -1, 1 << 62):
+                plan = _plan(lib, is_causal=causal, atomic_dq=atomic, ds_limit_bytes=limit, **big)
+                if limit <= 0:
+                    assert plan.ds_elems == 0, (causal, atomic, limit)
+                else:
+                    assert 0 <= 2 * plan.ds_elems <= 1 << 58, (causal, atomic, plan.ds_elems)
+                assert plan.dq_accum_elems >= 0 and plan.dkv_accum_elems >= 0 and plan.kv_split >= 1
 
 
 def test_missing_library_fails_loudly(tmp_path):
